@@ -1,0 +1,112 @@
+"""ctypes binding of the C ABI in ``include/cudaforge_hip.h``.
+
+This is the binding a non-PyTorch caller writes; the
+parity tests and the benchmark use it to reach the kernels without the
+dispatcher in between. Pointers are passed as integers (``tensor.data_ptr()``)
+and streams as ``torch.cuda.current_stream().cuda_stream``.
+
+torch must be imported first on a GPU host, so that this library binds to the
+HIP runtime torch already loaded (both resolve ``libamdhip64.so.7``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from functools import lru_cache
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+HEADER = PACKAGE_DIR.parent / "include" / "cudaforge_hip.h"
+LIBRARY = PACKAGE_DIR / "libcudaforge_hip.so"
+
+CF_OK = 0
+CF_ERR_INVALID_ARGUMENT = 1
+CF_ERR_UNSUPPORTED = 2
+CF_ERR_HIP = 3
+
+CF_F32 = 0
+CF_F16 = 1
+CF_BF16 = 2
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); must cover every function the header declares.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "cf_last_error": (ctypes.c_char_p, []),
+    "cf_last_hip_error": (_I32, []),
+    "cf_hip_error_is_sticky": (_I32, [_I32]),
+    "cf_abi_version": (_I32, []),
+    "cf_quant_scale_count": (_I64, [_I64]),
+    "cf_quantize_int8": (_I32, [_P, _I32, _P, _P, _I64, _P]),
+    "cf_dequantize_int8": (_I32, [_P, _P, _P, _I32, _I64, _P]),
+    "cf_quantize_dequantize": (_I32, [_P, _P, _I32, _I64, _P]),
+    "cf_rmsnorm": (_I32, [_P, _P, _P, _I32, _I64, _I64, _F, _P]),
+    "cf_fused_residual_rmsnorm": (_I32, [_P, _P, _P, _P, _P, _I32, _I64, _I64, _F, _P]),
+    "cf_softmax": (_I32, [_P, _I32, _P, _I32, _I64, _I64, _P]),
+    "cf_reduce_sum_workspace_bytes": (_SZ, [_I64]),
+    "cf_reduce_sum": (_I32, [_P, _I32, _P, _I64, _P, _SZ, _I32, _P]),
+    "cf_row_sum": (_I32, [_P, _I32, _P, _I64, _I64, _P]),
+    "cf_lora_workspace_bytes": (_SZ, [_I64, _I64]),
+    "cf_lora_linear": (_I32, [_P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _F, _P]),
+    "cf_matmul": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _P]),
+    "cf_lora_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "cf_lora_backward": (
+        _I32,
+        [_P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _F, _P, _SZ, _P],
+    ),
+    "cf_silu": (_I32, [_P, _P, _I32, _I64, _P]),
+    "cf_gelu": (_I32, [_P, _P, _I32, _I64, _P]),
+    "cf_swiglu": (_I32, [_P, _P, _P, _I32, _I64, _P]),
+    "cf_copy_bytes": (_I32, [_P, _P, _I64, _P]),
+}
+
+
+def declared_functions(header: Path = HEADER) -> list[str]:
+    """Names of the functions the C header declares."""
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(encoding="utf-8"), flags=re.S)
+    return sorted(set(re.findall(r"\b(cf_[a-z0-9_]+)\s*\(", text)))
+
+
+class CfError(RuntimeError):
+    """A non-zero cf_status, with the library's message."""
+
+    def __init__(self, status: int, message: str) -> None:
+        super().__init__(f"cf status {status}: {message}")
+        self.status = status
+
+
+@lru_cache(maxsize=1)
+def load() -> ctypes.CDLL:
+    """Load the library and attach every signature; raises if it is not built."""
+    if not LIBRARY.exists():
+        raise FileNotFoundError(
+            f"{LIBRARY} is not built; run `python -m cuda_force_amd.build` or __graft_entry__.build()"
+        )
+    lib = ctypes.CDLL(str(LIBRARY))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return lib
+
+
+def check(status: int) -> None:
+    """Raise CfError for a non-zero status."""
+    if status != CF_OK:
+        message = load().cf_last_error().decode("utf-8", "replace")
+        raise CfError(status, message)
+
+
+def dtype_code(dtype: object) -> int:
+    """cf_dtype for a torch dtype."""
+    import torch
+
+    mapping = {torch.float32: CF_F32, torch.float16: CF_F16, torch.bfloat16: CF_BF16}
+    if dtype not in mapping:
+        raise TypeError(f"no cf_dtype for {dtype}")
+    return mapping[dtype]

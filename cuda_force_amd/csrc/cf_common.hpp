@@ -1,0 +1,323 @@
+// Shared device and host infrastructure for the gfx950 kernels.
+//
+// Device side: wave64 cross-lane reductions built on DPP (data-parallel
+// primitives: a lane reads a neighbour's register inside the same VALU
+// instruction, no LDS traffic, no barrier), 16-bit float conversions with
+// explicit round-to-nearest-even, and 128-bit vector load/store types.
+//
+// Host side: the thread-local error slot behind cf_last_error(), the
+// launch-check helper and cached per-device facts.
+//
+// The reference builds its reductions for 32-lane warps with
+// __shfl_down_sync (cuda/include/cudaforge/cuda_utils.cuh:27-115) and a
+// shared-memory exchange between warps. A CDNA4 wavefront has 64 lanes in
+// four DPP "rows" of 16, so a 64-element quantisation block or a 16-lane
+// group reduces with 4 DPP steps and no LDS at all, and a whole wave reduces
+// with 4 more reads of one lane per row.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/cudaforge_hip.h"
+
+namespace cf {
+
+/// Lanes per wavefront on CDNA (gfx9 family, gfx950 included). The reference
+/// hard-codes 32 (cpp/include/cudaforge/launch_config.hpp:22); every
+/// reduction here is written for 64.
+inline constexpr int kWaveSize = 64;
+
+/// Elements per quantisation scale; kQuantBlockSize in the reference
+/// (cuda/include/cudaforge/quantization.cuh:18).
+inline constexpr int kQuantBlockSize = 64;
+
+/// Default workgroup size for the streaming kernels: four waves, one per SIMD
+/// of a CU.
+inline constexpr int kDefaultBlockSize = 256;
+
+/// Largest workgroup HIP permits on gfx950.
+inline constexpr int kMaxBlockSize = 1024;
+
+// ---------------------------------------------------------------------------
+// Device: DPP cross-lane moves and reductions.
+// ---------------------------------------------------------------------------
+
+// DPP control words (GFX9 encoding).
+inline constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+inline constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+inline constexpr int kDppRowRor4 = 0x124;       // rotate by 4 within a 16-lane row
+inline constexpr int kDppRowRor8 = 0x128;       // rotate by 8 within a 16-lane row
+inline constexpr int kDppRowHalfMirror = 0x141; // reverse each 8-lane half row
+
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_mov_dpp(static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<kCtrl>(__float_as_uint(v)));
+}
+
+struct MaxU32 {
+    __device__ __forceinline__ static uint32_t apply(uint32_t a, uint32_t b) {
+        return a > b ? a : b;
+    }
+};
+
+struct AddF32 {
+    __device__ __forceinline__ static float apply(float a, float b) { return a + b; }
+};
+
+struct MaxF32 {
+    // fmaxf drops a NaN operand. Softmax inputs are never NaN in the configs;
+    // where NaN must propagate (quantisation absmax) the kernels reduce the
+    // integer bit pattern with MaxU32 instead.
+    __device__ __forceinline__ static float apply(float a, float b) { return fmaxf(a, b); }
+};
+
+/// Reduce across groups of `kLanes` consecutive lanes (4, 8 or 16). Every
+/// lane of the group ends with the group's result. All 64 lanes must be
+/// active.
+template <int kLanes, typename Op>
+__device__ __forceinline__ uint32_t group_reduce_u32(uint32_t v) {
+    static_assert(kLanes == 4 || kLanes == 8 || kLanes == 16, "group of 4, 8 or 16 lanes");
+    v = Op::apply(v, dpp_u32<kDppQuadXor1>(v));
+    v = Op::apply(v, dpp_u32<kDppQuadXor2>(v));
+    if constexpr (kLanes == 8) {
+        v = Op::apply(v, dpp_u32<kDppRowHalfMirror>(v));
+    } else if constexpr (kLanes == 16) {
+        v = Op::apply(v, dpp_u32<kDppRowRor4>(v));
+        v = Op::apply(v, dpp_u32<kDppRowRor8>(v));
+    }
+    return v;
+}
+
+template <int kLanes, typename Op>
+__device__ __forceinline__ float group_reduce_f32(float v) {
+    static_assert(kLanes == 4 || kLanes == 8 || kLanes == 16, "group of 4, 8 or 16 lanes");
+    v = Op::apply(v, dpp_f32<kDppQuadXor1>(v));
+    v = Op::apply(v, dpp_f32<kDppQuadXor2>(v));
+    if constexpr (kLanes == 8) {
+        v = Op::apply(v, dpp_f32<kDppRowHalfMirror>(v));
+    } else if constexpr (kLanes == 16) {
+        v = Op::apply(v, dpp_f32<kDppRowRor4>(v));
+        v = Op::apply(v, dpp_f32<kDppRowRor8>(v));
+    }
+    return v;
+}
+
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+/// Whole-wave reduction; the result is uniform across the wave. The four row
+/// results are combined in a fixed order, so the result is deterministic.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce_f32(float v) {
+    v = group_reduce_f32<16, Op>(v);
+    const float r0 = readlane_f32(v, 0);
+    const float r1 = readlane_f32(v, 16);
+    const float r2 = readlane_f32(v, 32);
+    const float r3 = readlane_f32(v, 48);
+    return Op::apply(Op::apply(r0, r1), Op::apply(r2, r3));
+}
+
+/// Workgroup-wide reduction for kWaves waves through a kWaves-float LDS slot.
+/// The result is returned to every thread. The trailing barrier lets the
+/// caller reuse `slot` for a following reduction (the reference's second
+/// barrier, cuda/include/cudaforge/cuda_utils.cuh:79-86, for the same reason).
+template <int kWaves, typename Op>
+__device__ __forceinline__ float block_reduce_f32(float v, float* slot) {
+    v = wave_reduce_f32<Op>(v);
+    if constexpr (kWaves == 1) {
+        return v;
+    } else {
+        const int wave = static_cast<int>(threadIdx.x) / kWaveSize;
+        if ((threadIdx.x & (kWaveSize - 1)) == 0) slot[wave] = v;
+        __syncthreads();
+        float total = slot[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) total = Op::apply(total, slot[w]);
+        __syncthreads();
+        return total;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Device: 16-bit float storage.
+// ---------------------------------------------------------------------------
+
+struct bf16_t {
+    uint16_t bits;
+};
+struct f16_t {
+    uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+/// fp32 -> bf16 with round-to-nearest-even; NaN becomes the canonical quiet
+/// NaN 0x7FC0. Bit-identical to c10::BFloat16's conversion, which is what the
+/// reference's `.to(torch.bfloat16)` uses.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+/// fp32 -> fp16, round-to-nearest-even (v_cvt_f16_f32 under the default mode).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+/// Storage traits: element type, how many fit a 16-byte vector, conversions.
+template <typename T>
+struct Storage;
+
+template <>
+struct Storage<float> {
+    using elem = float;
+    static constexpr int kPerVec = 4;
+    __device__ __forceinline__ static float load(const float* p) { return *p; }
+    __device__ __forceinline__ static void store(float* p, float v) { *p = v; }
+};
+
+template <>
+struct Storage<bf16_t> {
+    using elem = uint16_t;
+    static constexpr int kPerVec = 8;
+    __device__ __forceinline__ static float load(const bf16_t* p) {
+        return bf16_bits_to_f32(p->bits);
+    }
+    __device__ __forceinline__ static void store(bf16_t* p, float v) {
+        p->bits = static_cast<uint16_t>(f32_to_bf16_bits(v));
+    }
+    __device__ __forceinline__ static float from_bits(uint32_t h) { return bf16_bits_to_f32(h); }
+    __device__ __forceinline__ static uint32_t to_bits(float v) { return f32_to_bf16_bits(v); }
+};
+
+template <>
+struct Storage<f16_t> {
+    using elem = uint16_t;
+    static constexpr int kPerVec = 8;
+    __device__ __forceinline__ static float load(const f16_t* p) { return f16_bits_to_f32(p->bits); }
+    __device__ __forceinline__ static void store(f16_t* p, float v) {
+        p->bits = static_cast<uint16_t>(f32_to_f16_bits(v));
+    }
+    __device__ __forceinline__ static float from_bits(uint32_t h) { return f16_bits_to_f32(h); }
+    __device__ __forceinline__ static uint32_t to_bits(float v) { return f32_to_f16_bits(v); }
+};
+
+/// Unpack a 16-byte vector of T into 4 or 8 floats.
+template <typename T>
+__device__ __forceinline__ void unpack16(const uint4& v, float* out) {
+    if constexpr (Storage<T>::kPerVec == 4) {
+        out[0] = __uint_as_float(v.x);
+        out[1] = __uint_as_float(v.y);
+        out[2] = __uint_as_float(v.z);
+        out[3] = __uint_as_float(v.w);
+    } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            out[2 * i] = Storage<T>::from_bits(w[i] & 0xFFFFu);
+            out[2 * i + 1] = Storage<T>::from_bits(w[i] >> 16);
+        }
+    }
+}
+
+/// Pack 4 or 8 floats into a 16-byte vector of T (rounding to T).
+template <typename T>
+__device__ __forceinline__ uint4 pack16(const float* in) {
+    uint4 v;
+    if constexpr (Storage<T>::kPerVec == 4) {
+        v.x = __float_as_uint(in[0]);
+        v.y = __float_as_uint(in[1]);
+        v.z = __float_as_uint(in[2]);
+        v.w = __float_as_uint(in[3]);
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[i] = Storage<T>::to_bits(in[2 * i]) | (Storage<T>::to_bits(in[2 * i + 1]) << 16);
+        }
+        v.x = w[0];
+        v.y = w[1];
+        v.z = w[2];
+        v.w = w[3];
+    }
+    return v;
+}
+
+__device__ __forceinline__ bool aligned16(const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// ---------------------------------------------------------------------------
+// Host: errors, launch checks, device facts.
+// ---------------------------------------------------------------------------
+
+/// Record a failure for cf_last_error() and return its status.
+cf_status fail(cf_status status, const char* format, ...) __attribute__((format(printf, 2, 3)));
+
+/// Record a HIP failure (with its hipError_t) and return CF_ERR_HIP.
+cf_status fail_hip(hipError_t error, const char* what);
+
+/// After a launch: report launch-configuration errors, and with
+/// CUDAFORGE_DEBUG_SYNC set also wait for the stream and report faults.
+cf_status check_launch(const char* what, hipStream_t stream);
+
+/// Compute units of the current device (cached per device, thread-safe).
+int cu_count();
+
+/// True when `dtype` is one of the three storage types.
+inline bool valid_dtype(cf_dtype dtype) {
+    return dtype == CF_F32 || dtype == CF_F16 || dtype == CF_BF16;
+}
+
+inline const char* dtype_name(cf_dtype dtype) {
+    switch (dtype) {
+        case CF_F32:
+            return "float32";
+        case CF_F16:
+            return "float16";
+        case CF_BF16:
+            return "bfloat16";
+    }
+    return "unknown";
+}
+
+inline size_t dtype_size(cf_dtype dtype) { return dtype == CF_F32 ? 4 : 2; }
+
+inline bool host_aligned(const void* p, size_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+template <typename T>
+constexpr T ceil_div(T a, T b) {
+    return (a + b - 1) / b;
+}
+
+}  // namespace cf
+
+/// Return early with CF_ERR_INVALID_ARGUMENT and a message when `cond` fails.
+#define CF_REQUIRE(cond, ...)                                                   \
+    do {                                                                        \
+        if (!(cond)) return ::cf::fail(CF_ERR_INVALID_ARGUMENT, __VA_ARGS__);   \
+    } while (false)
+
+/// Run a host HIP call; on failure return CF_ERR_HIP naming the call.
+#define CF_HIP_TRY(expr)                                                        \
+    do {                                                                        \
+        const hipError_t cf_hip_status_ = (expr);                               \
+        if (cf_hip_status_ != hipSuccess) return ::cf::fail_hip(cf_hip_status_, #expr); \
+    } while (false)

@@ -1,0 +1,746 @@
+// LoRA linear (forward and adapter backward) and plain matmul for gfx950.
+//
+// Operator layout, as the reference's (cuda/include/cudaforge/lora_linear.cuh:26-31,
+// python/cudaforge/ops.py:289-332), all row-major:
+//   x [M, K]   w [K, N]   a [K, r]   b [r, N]   y [M, N]
+//   y = x @ w + scale * ((x @ a) @ b)
+//
+// Fast path (bf16, K % 64 == 0, N % 8 == 0, r <= 16, 16-byte aligned): one
+// fused kernel on the bf16 MFMA units.
+//   * 256x256 output tile per workgroup, 4 waves of 128x128, K-step 64,
+//     v_mfma_f32_32x32x16_bf16 with fp32 accumulators (256 per lane).
+//   * Operands are staged through LDS in a K-major layout with an XOR swizzle
+//     on 16-byte chunks (conflict-free fragment reads), double-buffered: the
+//     next K-tile's global loads are in flight while the current one feeds
+//     the MFMAs, one barrier per K-step.
+//   * w arrives N-major ([K, N] is what the reference's operator takes), so
+//     each thread loads an 8x8 bf16 block as eight 16-byte row segments and
+//     transposes it in registers with v_perm_b32 before the LDS store.
+//   * The adapter down-projection x @ a is accumulated in the same K-loop as
+//     16 extra output columns (v_mfma_f32_16x16x32_bf16 on the x tile already
+//     in LDS, about 6% more MFMA work), so x is read from HBM once.
+//   * Epilogue: x @ a is rounded to bf16 (as the reference's ATen path rounds
+//     the intermediate tensor), exchanged through LDS into MFMA A-operand
+//     layout, multiplied by b with one K=16 MFMA per 32x32 tile, scaled and
+//     added to the base accumulators, and the tile is stored as bf16. No
+//     second launch and no [M, r] round trip through HBM.
+//   * Workgroup ids are remapped so that the 64 tiles dispatched to one XCD
+//     (ids are dealt round-robin across the 8 XCDs) form a 4 x 16 band of
+//     output tiles sharing x row-panels in that XCD's L2.
+// The reference's fused kernel instead recomputes x @ a untiled in every
+// block (cuda/src/lora_linear.cu:138-203).
+//
+// Generic path (fp32, or shapes the fast path does not take): x @ a into a
+// fp32 [M, r] workspace (one wave per row), then a 64x64-tiled fp32 FMA GEMM
+// whose epilogue adds scale * (xa @ b).
+//
+// Backward (adapter only, op layout):
+//   G      = dy @ b^T            [M, r]   one wave per row of dy
+//   grad_b = scale * xa^T @ dy   [r, N]   column reduction over M
+//   grad_a = scale * x^T @ G     [K, r]   column reduction over M
+// The column reductions run in row chunks into an fp32 workspace and a second
+// kernel sums the chunks in a fixed order (deterministic).
+#include "cf_common.hpp"
+
+namespace cf {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxRank = 64;
+
+// ---------------------------------------------------------------------------
+// Generic path.
+// ---------------------------------------------------------------------------
+
+/// out[m, q] = sum_k x[m, k] * p[k * k_stride + q * q_stride] for q < rank,
+/// fp32, one wave per row. Used for x @ a (k_stride = r, q_stride = 1) and
+/// for dy @ b^T (k_stride = 1, q_stride = N).
+template <typename T>
+__global__ __launch_bounds__(kDefaultBlockSize) void row_dot_kernel(
+    const T* __restrict__ x, const T* __restrict__ p, float* __restrict__ out, int64_t rows,
+    int64_t inner, int64_t rank, int64_t k_stride, int64_t q_stride) {
+    const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kDefaultBlockSize / kWaveSize) +
+                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * (kDefaultBlockSize / kWaveSize);
+    for (int64_t row = wave; row < rows; row += waves) {
+        const T* xr = x + row * inner;
+        for (int64_t q0 = 0; q0 < rank; q0 += 16) {
+            float acc[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
+            for (int64_t k = lane; k < inner; k += kWaveSize) {
+                const float xv = Storage<T>::load(xr + k);
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    if (q0 + q < rank) {
+                        acc[q] += xv * Storage<T>::load(p + k * k_stride + (q0 + q) * q_stride);
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const float total = wave_reduce_f32<AddF32>(acc[q]);
+                if (lane == 0 && q0 + q < rank) out[row * rank + q0 + q] = total;
+            }
+        }
+    }
+}
+
+/// Round a float through the storage type T (identity for fp32).
+template <typename T>
+__device__ __forceinline__ float round_to(float v) {
+    if constexpr (sizeof(typename Storage<T>::elem) == 4) {
+        return v;
+    } else {
+        return Storage<T>::from_bits(Storage<T>::to_bits(v));
+    }
+}
+
+constexpr int kGT = 64;   // generic output tile edge
+constexpr int kGK = 16;   // generic K step
+
+/// y = x @ w (+ scale * (round_T(xa) @ b) when xa != nullptr), 64x64 tile per
+/// workgroup, 4x4 outputs per thread, fp32 FMA accumulation.
+template <typename T>
+__global__ __launch_bounds__(kDefaultBlockSize) void tiled_gemm_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const float* __restrict__ xa,
+    const T* __restrict__ b, T* __restrict__ y, int64_t M, int64_t N, int64_t K, int64_t rank,
+    float scale) {
+    __shared__ float as[kGK][kGT + 4];
+    __shared__ float bs[kGK][kGT + 4];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int ty = tid / 16;
+    const int tx = tid % 16;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kGT;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kGT;
+
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    }
+
+    for (int64_t k0 = 0; k0 < K; k0 += kGK) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = i * kDefaultBlockSize + tid;
+            const int am = e / kGK;
+            const int ak = e % kGK;
+            const int64_t gm = m0 + am;
+            const int64_t gk = k0 + ak;
+            as[ak][am] = (gm < M && gk < K) ? Storage<T>::load(x + gm * K + gk) : 0.0f;
+            const int bk = e / kGT;
+            const int bn = e % kGT;
+            const int64_t gk2 = k0 + bk;
+            const int64_t gn = n0 + bn;
+            bs[bk][bn] = (gk2 < K && gn < N) ? Storage<T>::load(w + gk2 * N + gn) : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kGK; ++k) {
+            float av[4];
+            float bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[i] = as[k][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[j] = bs[k][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+            }
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t gm = m0 + ty * 4 + i;
+        if (gm >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t gn = n0 + tx * 4 + j;
+            if (gn >= N) continue;
+            float v = acc[i][j];
+            if (xa != nullptr) {
+                float adapter = 0.0f;
+                for (int64_t q = 0; q < rank; ++q) {
+                    adapter += round_to<T>(xa[gm * rank + q]) * Storage<T>::load(b + q * N + gn);
+                }
+                v += scale * adapter;
+            }
+            Storage<T>::store(y + gm * N + gn, v);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fast path: fused bf16 MFMA kernel.
+// ---------------------------------------------------------------------------
+
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kBK = 64;
+constexpr int kLdsRow = kBK * 2;                    // bytes per K-major LDS row
+constexpr int kTileA = kBM * kLdsRow;               // 32 KiB
+constexpr int kTileB = kBN * kLdsRow;               // 32 KiB
+constexpr int kTileAdapter = 16 * kLdsRow;          // 2 KiB: a^T [16][64]
+constexpr int kStage = kTileA + kTileB + kTileAdapter;
+constexpr int kLdsBytes = 2 * kStage;               // 132 KiB
+constexpr int kFusedThreads = 256;
+
+/// Byte offset of 16-byte chunk `chunk` (0..7) of K-major row `row`. The XOR
+/// of both the low and the next three bits of the row spreads 8 consecutive
+/// rows (fragment reads) and rows 8 apart (transposed stores) over all banks.
+__device__ __forceinline__ int lds_offset(int row, int chunk) {
+    return row * kLdsRow + ((chunk ^ (row & 7) ^ ((row >> 3) & 7)) << 4);
+}
+
+/// Transpose an 8x8 block of bf16: in[r] holds row r (8 values, 2 per dword);
+/// out[j] receives column j (8 values).
+__device__ __forceinline__ void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t lo_row[4] = {in[2 * e].x, in[2 * e].y, in[2 * e].z, in[2 * e].w};
+        const uint32_t hi_row[4] = {in[2 * e + 1].x, in[2 * e + 1].y, in[2 * e + 1].z,
+                                    in[2 * e + 1].w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t even = __builtin_amdgcn_perm(hi_row[d], lo_row[d], 0x05040100u);
+            const uint32_t odd = __builtin_amdgcn_perm(hi_row[d], lo_row[d], 0x07060302u);
+            uint32_t* ce = reinterpret_cast<uint32_t*>(&out[2 * d]);
+            uint32_t* co = reinterpret_cast<uint32_t*>(&out[2 * d + 1]);
+            ce[e] = even;
+            co[e] = odd;
+        }
+    }
+}
+
+struct FusedArgs {
+    const uint16_t* x;
+    const uint16_t* w;
+    const uint16_t* a;
+    const uint16_t* b;
+    uint16_t* y;
+    float* xa_out;
+    int64_t M;
+    int64_t N;
+    int64_t K;
+    int64_t rank;
+    float scale;
+    int tiles_m;
+    int tiles_n;
+};
+
+/// Tile coordinates for workgroup `pid`: undo the round-robin XCD dealing so
+/// consecutive logical ids share an XCD, then walk 4-row bands of tiles.
+__device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    constexpr int kXcds = 8;
+    constexpr int kGroupM = 4;
+    const int total = tiles_m * tiles_n;
+    int logical = pid;
+    if (total % kXcds == 0) {
+        const int per_xcd = total / kXcds;
+        logical = (pid % kXcds) * per_xcd + pid / kXcds;
+    }
+    const int band = kGroupM * tiles_n;
+    const int group = logical / band;
+    const int first_m = group * kGroupM;
+    const int rows_in_group = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+    const int in_group = logical % band;
+    tm = first_m + in_group % rows_in_group;
+    tn = in_group / rows_in_group;
+}
+
+__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void lora_fused_bf16_kernel(FusedArgs args) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    int tm;
+    int tn;
+    tile_of(static_cast<int>(blockIdx.x), args.tiles_m, args.tiles_n, tm, tn);
+    const int64_t m0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+    const int64_t M = args.M;
+    const int64_t N = args.N;
+    const int64_t K = args.K;
+    const int64_t rank = args.rank;
+
+    // Per-thread global load coordinates.
+    //   x tile [256 rows][8 chunks]: chunk id i*256 + tid -> row id>>3, chunk id&7.
+    //   w tile [64 k][256 n] as 8x8 blocks: k-block tid>>5, n-block tid&31.
+    //   a tile [64 k][16 j]: 4 elements per thread, k = tid>>2, j = (tid&3)*4 + e.
+    const int wkb = tid >> 5;
+    const int wnb = tid & 31;
+    const bool w_valid = (n0 + wnb * 8) < N;
+    const int ak = tid >> 2;
+    const int aj = (tid & 3) * 4;
+
+    uint4 xr[8];
+    uint4 wr[8];
+    uint16_t ar[4];
+
+    auto load_global = [&](int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int id = i * kFusedThreads + tid;
+            const int64_t row = m0 + (id >> 3);
+            const int chunk = id & 7;
+            xr[i] = row < M ? *reinterpret_cast<const uint4*>(args.x + row * K + k0 + chunk * 8)
+                            : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int64_t k = k0 + wkb * 8 + r;
+            wr[r] = w_valid ? *reinterpret_cast<const uint4*>(args.w + k * N + n0 + wnb * 8)
+                            : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t j = aj + e;
+            ar[e] = j < rank ? args.a[(k0 + ak) * rank + j] : static_cast<uint16_t>(0);
+        }
+    };
+
+    auto store_lds = [&](int stage) {
+        uint8_t* base = lds + stage * kStage;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int id = i * kFusedThreads + tid;
+            *reinterpret_cast<uint4*>(base + lds_offset(id >> 3, id & 7)) = xr[i];
+        }
+        uint4 cols[8];
+        transpose8x8(wr, cols);
+        uint8_t* bt = base + kTileA;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            *reinterpret_cast<uint4*>(bt + lds_offset(wnb * 8 + j, wkb)) = cols[j];
+        }
+        uint8_t* at = base + kTileA + kTileB;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int j = aj + e;
+            *reinterpret_cast<uint16_t*>(at + lds_offset(j, ak >> 3) + (ak & 7) * 2) = ar[e];
+        }
+    };
+
+    f32x16_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+    f32x4_t xacc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xacc[i][r] = 0.0f;
+    }
+
+    const int64_t k_tiles = K / kBK;
+    load_global(0);
+    store_lds(0);
+    __syncthreads();
+
+    for (int64_t kt = 0; kt < k_tiles; ++kt) {
+        const int stage = static_cast<int>(kt & 1);
+        if (kt + 1 < k_tiles) load_global((kt + 1) * kBK);
+
+        const uint8_t* ta = lds + stage * kStage;
+        const uint8_t* tb = ta + kTileA;
+        const uint8_t* tat = tb + kTileB;
+#pragma unroll
+        for (int kk = 0; kk < kBK / 16; ++kk) {
+            const int chunk = kk * 2 + (lane >> 5);
+            bf16x8_t af[4];
+            bf16x8_t bfr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                af[i] = *reinterpret_cast<const bf16x8_t*>(
+                    ta + lds_offset(wm * 128 + i * 32 + (lane & 31), chunk));
+                bfr[i] = *reinterpret_cast<const bf16x8_t*>(
+                    tb + lds_offset(wn * 128 + i * 32 + (lane & 31), chunk));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] =
+                        __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        // Adapter down-projection: this wave's 64 rows x 16 columns.
+#pragma unroll
+        for (int kk = 0; kk < kBK / 32; ++kk) {
+            const int chunk = kk * 4 + (lane >> 4);
+            const bf16x8_t bv =
+                *reinterpret_cast<const bf16x8_t*>(tat + lds_offset(lane & 15, chunk));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(
+                    ta + lds_offset(wave * 64 + i * 16 + (lane & 15), chunk));
+                xacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, xacc[i], 0, 0, 0);
+            }
+        }
+
+        if (kt + 1 < k_tiles) store_lds(stage ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: adapter up-projection and store ----
+    // xa (bf16) exchange tile [256][16] in the (now idle) stage-0 buffer.
+    uint16_t* xa_lds = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = wave * 64 + i * 16 + 4 * (lane >> 4) + r;
+            const int col = lane & 15;
+            const float v = xacc[i][r];
+            xa_lds[row * 16 + col] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+            if (args.xa_out != nullptr && tn == 0 && col < rank && m0 + row < M) {
+                args.xa_out[(m0 + row) * rank + col] = v;
+            }
+        }
+    }
+    __syncthreads();
+
+    bf16x8_t xa_frag[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = wm * 128 + i * 32 + (lane & 31);
+        xa_frag[i] = *reinterpret_cast<const bf16x8_t*>(xa_lds + row * 16 + (lane >> 5) * 8);
+    }
+    bf16x8_t b_frag[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t col = n0 + wn * 128 + j * 32 + (lane & 31);
+        uint16_t vals[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t q = (lane >> 5) * 8 + e;
+            vals[e] = (q < rank && col < N) ? args.b[q * N + col] : static_cast<uint16_t>(0);
+        }
+        b_frag[j] = __builtin_bit_cast(bf16x8_t, vals);
+    }
+    const float scale = args.scale;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f32x16_t t;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) t[r] = 0.0f;
+            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa_frag[i], b_frag[j], t, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] += scale * t[r];
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t col = n0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < M && col < N) {
+                    args.y[row * N + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[i][j][r]));
+                }
+            }
+        }
+    }
+}
+
+bool fused_eligible(const void* x, const void* w, const void* a, const void* b, const void* y,
+                    int64_t M, int64_t N, int64_t K, int64_t rank) {
+    (void)a;
+    (void)b;
+    (void)y;
+    return K % kBK == 0 && K > 0 && N % 8 == 0 && rank <= 16 && host_aligned(x, 16) &&
+           host_aligned(w, 16) && ceil_div<int64_t>(M, kBM) * ceil_div<int64_t>(N, kBN) < (1LL << 31);
+}
+
+cf_status launch_fused(const void* x, const void* w, const void* a, const void* b, void* y,
+                       float* xa_out, int64_t M, int64_t N, int64_t K, int64_t rank, float scale,
+                       hipStream_t stream) {
+    FusedArgs args;
+    args.x = static_cast<const uint16_t*>(x);
+    args.w = static_cast<const uint16_t*>(w);
+    args.a = static_cast<const uint16_t*>(a);
+    args.b = static_cast<const uint16_t*>(b);
+    args.y = static_cast<uint16_t*>(y);
+    args.xa_out = xa_out;
+    args.M = M;
+    args.N = N;
+    args.K = K;
+    args.rank = rank;
+    args.scale = scale;
+    args.tiles_m = static_cast<int>(ceil_div<int64_t>(M, kBM));
+    args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
+    const int grid = args.tiles_m * args.tiles_n;
+    lora_fused_bf16_kernel<<<grid, kFusedThreads, 0, stream>>>(args);
+    return check_launch("launching the fused bf16 LoRA kernel", stream);
+}
+
+// ---------------------------------------------------------------------------
+// Backward: column reductions.
+// ---------------------------------------------------------------------------
+
+constexpr int kColThreads = 256;
+constexpr int kColRowsPerChunk = 256;
+
+/// part[chunk, q, n] = sum_{m in chunk} round_T(p[m, q]) * v[m, n] for
+/// q < rank (<= 16 per launch slice q0). Each wave takes a quarter of the
+/// chunk's rows for the same 64 columns per lane-group; the four waves are
+/// combined through LDS.
+template <typename T>
+__global__ __launch_bounds__(kColThreads) void column_reduce_kernel(
+    const float* __restrict__ p, const T* __restrict__ v, float* __restrict__ part, int64_t rows,
+    int64_t cols, int64_t rank, int64_t q0) {
+    __shared__ float red[kColThreads / kWaveSize][16][kWaveSize];
+    const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
+    const int wave = static_cast<int>(threadIdx.x) / kWaveSize;
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * kWaveSize + lane;
+    const int64_t chunk = blockIdx.y;
+    const int64_t row_begin = chunk * kColRowsPerChunk;
+    const int64_t row_end =
+        row_begin + kColRowsPerChunk < rows ? row_begin + kColRowsPerChunk : rows;
+    float acc[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
+    if (n < cols) {
+        for (int64_t m = row_begin + wave; m < row_end; m += kColThreads / kWaveSize) {
+            const float vv = Storage<T>::load(v + m * cols + n);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                if (q0 + q < rank) acc[q] += round_to<T>(p[m * rank + q0 + q]) * vv;
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) red[wave][q][lane] = acc[q];
+    __syncthreads();
+    if (wave == 0 && n < cols) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            if (q0 + q < rank) {
+                const float total = (red[0][q][lane] + red[1][q][lane]) +
+                                    (red[2][q][lane] + red[3][q][lane]);
+                part[(chunk * rank + q0 + q) * cols + n] = total;
+            }
+        }
+    }
+}
+
+/// out = scale * sum over chunks of part, written as [rank, cols] or, with
+/// kTransposed, as [cols, rank].
+template <typename T, bool kTransposed>
+__global__ __launch_bounds__(kDefaultBlockSize) void column_finish_kernel(
+    const float* __restrict__ part, T* __restrict__ out, int64_t chunks, int64_t rank,
+    int64_t cols, float scale) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rank * cols) return;
+    const int64_t q = i / cols;
+    const int64_t n = i % cols;
+    float total = 0.0f;
+    for (int64_t c = 0; c < chunks; ++c) total += part[(c * rank + q) * cols + n];
+    const int64_t dst = kTransposed ? n * rank + q : q * cols + n;
+    Storage<T>::store(out + dst, scale * total);
+}
+
+template <typename T>
+cf_status column_reduce(const float* p, const void* v, void* out, bool transposed, int64_t rows,
+                        int64_t cols, int64_t rank, float scale, float* part, hipStream_t stream) {
+    const int64_t chunks = ceil_div<int64_t>(rows, kColRowsPerChunk);
+    const dim3 grid(static_cast<unsigned>(ceil_div<int64_t>(cols, kWaveSize)),
+                    static_cast<unsigned>(chunks));
+    for (int64_t q0 = 0; q0 < rank; q0 += 16) {
+        column_reduce_kernel<T><<<grid, kColThreads, 0, stream>>>(p, static_cast<const T*>(v), part,
+                                                                 rows, cols, rank, q0);
+    }
+    const int64_t total = rank * cols;
+    const unsigned fgrid = static_cast<unsigned>(ceil_div<int64_t>(total, kDefaultBlockSize));
+    if (transposed) {
+        column_finish_kernel<T, true><<<fgrid, kDefaultBlockSize, 0, stream>>>(
+            part, static_cast<T*>(out), chunks, rank, cols, scale);
+    } else {
+        column_finish_kernel<T, false><<<fgrid, kDefaultBlockSize, 0, stream>>>(
+            part, static_cast<T*>(out), chunks, rank, cols, scale);
+    }
+    return check_launch("launching the LoRA backward column reduction", stream);
+}
+
+template <typename T>
+cf_status zero_gradients(void* grad_a, void* grad_b, int64_t in_features, int64_t out_features,
+                         int64_t rank, hipStream_t stream) {
+    if (in_features > 0) {
+        const unsigned grid =
+            static_cast<unsigned>(ceil_div<int64_t>(rank * in_features, kDefaultBlockSize));
+        column_finish_kernel<T, true><<<grid, kDefaultBlockSize, 0, stream>>>(
+            nullptr, static_cast<T*>(grad_a), 0, rank, in_features, 1.0f);
+    }
+    if (out_features > 0) {
+        const unsigned grid =
+            static_cast<unsigned>(ceil_div<int64_t>(rank * out_features, kDefaultBlockSize));
+        column_finish_kernel<T, false><<<grid, kDefaultBlockSize, 0, stream>>>(
+            nullptr, static_cast<T*>(grad_b), 0, rank, out_features, 1.0f);
+    }
+    return check_launch("zeroing the LoRA gradients", stream);
+}
+
+template <typename T>
+void launch_row_dot(const void* x, const void* p, float* out, int64_t rows, int64_t inner,
+                    int64_t rank, int64_t k_stride, int64_t q_stride, hipStream_t stream) {
+    const int64_t max_waves = static_cast<int64_t>(cu_count()) * 16;
+    const int64_t waves = rows < max_waves ? rows : max_waves;
+    const int64_t grid = ceil_div<int64_t>(waves, kDefaultBlockSize / kWaveSize);
+    row_dot_kernel<T><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+        static_cast<const T*>(x), static_cast<const T*>(p), out, rows, inner, rank, k_stride,
+        q_stride);
+}
+
+template <typename T>
+cf_status launch_generic(const void* x, const void* w, const void* a, const void* b, void* y,
+                         float* xa, int64_t M, int64_t N, int64_t K, int64_t rank, float scale,
+                         hipStream_t stream) {
+    if (rank > 0) {
+        launch_row_dot<T>(x, a, xa, M, K, rank, rank, 1, stream);
+    }
+    const dim3 grid(static_cast<unsigned>(ceil_div<int64_t>(N, kGT)),
+                    static_cast<unsigned>(ceil_div<int64_t>(M, kGT)));
+    tiled_gemm_kernel<T><<<grid, kDefaultBlockSize, 0, stream>>>(
+        static_cast<const T*>(x), static_cast<const T*>(w), rank > 0 ? xa : nullptr,
+        static_cast<const T*>(b), static_cast<T*>(y), M, N, K, rank, scale);
+    return check_launch("launching the tiled LoRA GEMM", stream);
+}
+
+}  // namespace
+}  // namespace cf
+
+extern "C" {
+
+size_t cf_lora_workspace_bytes(int64_t batch, int64_t rank) {
+    if (batch <= 0 || rank <= 0) return 0;
+    return static_cast<size_t>(batch) * static_cast<size_t>(rank) * sizeof(float);
+}
+
+cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void* b, void* y,
+                         float* xa_out, cf_dtype dtype, int64_t batch, int64_t in_features,
+                         int64_t out_features, int64_t rank, float scale, void* stream) {
+    if (batch <= 0 || out_features <= 0) return CF_OK;
+    CF_REQUIRE(in_features >= 0 && rank >= 0, "cf_lora_linear: negative dimension");
+    CF_REQUIRE(rank <= cf::kMaxRank, "cf_lora_linear: rank %lld exceeds the supported %d",
+               static_cast<long long>(rank), cf::kMaxRank);
+    CF_REQUIRE(x != nullptr && w != nullptr && y != nullptr, "cf_lora_linear: null pointer");
+    CF_REQUIRE(rank == 0 || (a != nullptr && b != nullptr), "cf_lora_linear: null adapter");
+    CF_REQUIRE(dtype == CF_F32 || dtype == CF_BF16,
+               "cf_lora_linear: dtype %s has no kernel (float32 or bfloat16)",
+               cf::dtype_name(dtype));
+    auto s = static_cast<hipStream_t>(stream);
+    if (dtype == CF_BF16 &&
+        cf::fused_eligible(x, w, a, b, y, batch, out_features, in_features, rank)) {
+        return cf::launch_fused(x, w, a, b, y, xa_out, batch, out_features, in_features, rank,
+                                scale, s);
+    }
+    CF_REQUIRE(rank == 0 || xa_out != nullptr,
+               "cf_lora_linear: this shape takes the unfused path, which needs xa_out "
+               "(cf_lora_workspace_bytes(batch, rank) bytes) as its workspace");
+    if (dtype == CF_F32) {
+        return cf::launch_generic<float>(x, w, a, b, y, xa_out, batch, out_features, in_features,
+                                         rank, scale, s);
+    }
+    return cf::launch_generic<cf::bf16_t>(x, w, a, b, y, xa_out, batch, out_features, in_features,
+                                          rank, scale, s);
+}
+
+cf_status cf_matmul(const void* a, const void* b, void* c, cf_dtype dtype, int64_t m, int64_t n,
+                    int64_t k, void* stream) {
+    if (m <= 0 || n <= 0) return CF_OK;
+    CF_REQUIRE(a != nullptr && b != nullptr && c != nullptr, "cf_matmul: null pointer");
+    CF_REQUIRE(dtype == CF_F32 || dtype == CF_BF16, "cf_matmul: dtype %s has no kernel",
+               cf::dtype_name(dtype));
+    auto s = static_cast<hipStream_t>(stream);
+    if (dtype == CF_BF16 && cf::fused_eligible(a, b, nullptr, nullptr, c, m, n, k, 0)) {
+        return cf::launch_fused(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);
+    }
+    if (dtype == CF_F32) {
+        return cf::launch_generic<float>(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);
+    }
+    return cf::launch_generic<cf::bf16_t>(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);
+}
+
+size_t cf_lora_backward_workspace_bytes(int64_t batch, int64_t in_features, int64_t out_features,
+                                        int64_t rank) {
+    if (batch <= 0 || rank <= 0) return 0;
+    const int64_t chunks = cf::ceil_div<int64_t>(batch, cf::kColRowsPerChunk);
+    const int64_t widest = in_features > out_features ? in_features : out_features;
+    const size_t g = static_cast<size_t>(batch * rank) * sizeof(float);
+    const size_t part = static_cast<size_t>(chunks * rank * widest) * sizeof(float);
+    return ((g + 255) / 256) * 256 + part;
+}
+
+cf_status cf_lora_backward(const void* x, const void* dy, const void* b, const float* xa,
+                           void* grad_a, void* grad_b, cf_dtype dtype, int64_t batch,
+                           int64_t in_features, int64_t out_features, int64_t rank, float scale,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    if (rank <= 0) return CF_OK;
+    CF_REQUIRE(batch >= 0 && in_features >= 0 && out_features >= 0,
+               "cf_lora_backward: negative dimension");
+    CF_REQUIRE(rank <= cf::kMaxRank, "cf_lora_backward: rank %lld exceeds the supported %d",
+               static_cast<long long>(rank), cf::kMaxRank);
+    CF_REQUIRE(dtype == CF_F32 || dtype == CF_BF16, "cf_lora_backward: dtype %s has no kernel",
+               cf::dtype_name(dtype));
+    CF_REQUIRE(grad_a != nullptr && grad_b != nullptr, "cf_lora_backward: null gradient output");
+    if (batch == 0) {
+        // Empty batch: both gradients are zero (a finish pass over zero chunks
+        // writes them without reading anything).
+        auto s0 = static_cast<hipStream_t>(stream);
+        return dtype == CF_F32 ? cf::zero_gradients<float>(grad_a, grad_b, in_features,
+                                                           out_features, rank, s0)
+                               : cf::zero_gradients<cf::bf16_t>(grad_a, grad_b, in_features,
+                                                                out_features, rank, s0);
+    }
+    CF_REQUIRE(x != nullptr && dy != nullptr && b != nullptr && xa != nullptr,
+               "cf_lora_backward: null input");
+    const size_t needed = cf_lora_backward_workspace_bytes(batch, in_features, out_features, rank);
+    CF_REQUIRE(workspace != nullptr && workspace_bytes >= needed,
+               "cf_lora_backward: workspace of %zu bytes given, %zu needed", workspace_bytes,
+               needed);
+    CF_REQUIRE(cf::host_aligned(workspace, 16), "cf_lora_backward: workspace must be 16-byte aligned");
+    auto s = static_cast<hipStream_t>(stream);
+    float* g = static_cast<float*>(workspace);
+    const size_t g_bytes = ((static_cast<size_t>(batch * rank) * sizeof(float) + 255) / 256) * 256;
+    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + g_bytes);
+    if (dtype == CF_F32) {
+        cf::launch_row_dot<float>(dy, b, g, batch, out_features, rank, 1, out_features, s);
+        cf_status st = cf::column_reduce<float>(xa, dy, grad_b, false, batch, out_features, rank,
+                                                scale, part, s);
+        if (st != CF_OK) return st;
+        return cf::column_reduce<float>(g, x, grad_a, true, batch, in_features, rank, scale, part,
+                                        s);
+    }
+    cf::launch_row_dot<cf::bf16_t>(dy, b, g, batch, out_features, rank, 1, out_features, s);
+    cf_status st = cf::column_reduce<cf::bf16_t>(xa, dy, grad_b, false, batch, out_features, rank,
+                                                 scale, part, s);
+    if (st != CF_OK) return st;
+    return cf::column_reduce<cf::bf16_t>(g, x, grad_a, true, batch, in_features, rank, scale, part,
+                                         s);
+}
+
+}  // extern "C"

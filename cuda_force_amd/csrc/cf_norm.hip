@@ -1,0 +1,227 @@
+// RMSNorm and residual-add + RMSNorm for gfx950.
+//
+// Semantics: _rmsnorm_reference (python/cudaforge/ops.py:164-171),
+//   y = (x * rsqrt(mean(x^2) + eps)) * w      fp32 arithmetic, eps inside the
+//                                             sqrt, rounded once to the
+//                                             storage type at the end,
+// and _fused_residual_rmsnorm_reference (ops.py:188-192): r = x + residual in
+// the storage type, then rmsnorm(r). rsqrt is taken as 1 / sqrt with IEEE
+// sqrt and divide, the way ATen's CPU rsqrt computes it.
+//
+// Design (fast path): one wavefront owns a row. The row is loaded once with
+// 16-byte loads into registers (a 4096-wide bf16 row is 8 loads per lane),
+// the sum of squares reduces with DPP inside the wave (no LDS, no barrier),
+// and the row is scaled and stored from the same registers, so HBM sees one
+// read and one write per element. The weight vector is loaded once per wave
+// and reused for every row that wave processes. The reference instead uses a
+// block per row with a 32-lane shuffle tree and an LDS exchange, and re-reads
+// the row for the normalising pass (cuda/src/rmsnorm.cu:46-83).
+//
+// Fallback: rows that do not fit the register tile, unaligned pointers or a
+// row length that is not a whole number of 16-byte vectors use a workgroup per
+// row that reads the row twice (the second pass hits L2).
+#include "cf_common.hpp"
+
+namespace cf {
+namespace {
+
+constexpr int kWavesPerBlock = kDefaultBlockSize / kWaveSize;
+
+/// rsqrt(mean + eps) from the row's sum of squares.
+__device__ __forceinline__ float inv_rms(float sum_squares, int64_t cols, float eps) {
+    const float mean = sum_squares / static_cast<float>(cols);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+template <typename T, int kVecs, bool kResidual>
+__global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
+    const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ w,
+    T* __restrict__ y, T* __restrict__ residual_out, int64_t rows, int64_t cols, float eps) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
+    const int64_t vec_cols = cols / kPer;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
+                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+
+    uint4 wv[kVecs];
+#pragma unroll
+    for (int j = 0; j < kVecs; ++j) {
+        const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
+        wv[j] = v < vec_cols ? reinterpret_cast<const uint4*>(w)[v] : make_uint4(0, 0, 0, 0);
+    }
+
+    for (int64_t row = wave; row < rows; row += waves) {
+        const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
+        uint4 xv[kVecs];
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
+            xv[j] = v < vec_cols ? xr[v] : make_uint4(0, 0, 0, 0);
+        }
+        if constexpr (kResidual) {
+            const uint4* rr = reinterpret_cast<const uint4*>(residual + row * cols);
+            uint4* ro = reinterpret_cast<uint4*>(residual_out + row * cols);
+#pragma unroll
+            for (int j = 0; j < kVecs; ++j) {
+                const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
+                if (v < vec_cols) {
+                    float a[kPer];
+                    float b[kPer];
+                    unpack16<T>(xv[j], a);
+                    unpack16<T>(rr[v], b);
+#pragma unroll
+                    for (int i = 0; i < kPer; ++i) a[i] = a[i] + b[i];
+                    // The sum is rounded to the storage type before the norm,
+                    // as `x + residual` is in the reference.
+                    xv[j] = pack16<T>(a);
+                    ro[v] = xv[j];
+                }
+            }
+        }
+
+        float partial[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            float a[kPer];
+            unpack16<T>(xv[j], a);
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) partial[i & 3] += a[i] * a[i];
+        }
+        const float total = wave_reduce_f32<AddF32>((partial[0] + partial[1]) +
+                                                    (partial[2] + partial[3]));
+        const float scale = inv_rms(total, cols, eps);
+
+        uint4* yr = reinterpret_cast<uint4*>(y + row * cols);
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
+            if (v < vec_cols) {
+                float a[kPer];
+                float g[kPer];
+                unpack16<T>(xv[j], a);
+                unpack16<T>(wv[j], g);
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) a[i] = (a[i] * scale) * g[i];
+                yr[v] = pack16<T>(a);
+            }
+        }
+    }
+}
+
+/// Any shape and alignment: one workgroup per row, two passes over the row.
+template <typename T, bool kResidual>
+__global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_block_kernel(
+    const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ w,
+    T* __restrict__ y, T* __restrict__ residual_out, int64_t rows, int64_t cols, float eps) {
+    __shared__ float slot[kWavesPerBlock];
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const T* xr = x + row * cols;
+        float partial = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+            float a = Storage<T>::load(xr + c);
+            if constexpr (kResidual) {
+                a = a + Storage<T>::load(residual + row * cols + c);
+                Storage<T>::store(residual_out + row * cols + c, a);
+                a = Storage<T>::load(residual_out + row * cols + c);
+            }
+            partial += a * a;
+        }
+        const float total = block_reduce_f32<kWavesPerBlock, AddF32>(partial, slot);
+        const float scale = inv_rms(total, cols, eps);
+        const T* src = kResidual ? residual_out + row * cols : xr;
+        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+            const float a = Storage<T>::load(src + c);
+            Storage<T>::store(y + row * cols + c, (a * scale) * Storage<T>::load(w + c));
+        }
+    }
+}
+
+template <typename T, int kVecs, bool kResidual>
+void launch_wave(const void* x, const void* residual, const void* w, void* y, void* residual_out,
+                 int64_t rows, int64_t cols, float eps, hipStream_t stream) {
+    // Enough waves to keep every SIMD busy with several rows in flight, but
+    // not more than there are rows.
+    const int64_t max_waves = static_cast<int64_t>(cu_count()) * 16;
+    const int64_t waves = rows < max_waves ? rows : max_waves;
+    const int64_t grid = ceil_div<int64_t>(waves, kWavesPerBlock);
+    rmsnorm_wave_kernel<T, kVecs, kResidual>
+        <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
+            static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
+}
+
+template <typename T, bool kResidual>
+cf_status dispatch(const void* x, const void* residual, const void* w, void* y,
+                   void* residual_out, int64_t rows, int64_t cols, float eps,
+                   hipStream_t stream) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    bool vec = cols % kPer == 0 && host_aligned(x, 16) && host_aligned(w, 16) &&
+               host_aligned(y, 16);
+    if (kResidual) vec = vec && host_aligned(residual, 16) && host_aligned(residual_out, 16);
+    const int64_t vectors_per_lane = ceil_div<int64_t>(cols / kPer, kWaveSize);
+    if (vec && vectors_per_lane <= 16) {
+        if (vectors_per_lane <= 1) {
+            launch_wave<T, 1, kResidual>(x, residual, w, y, residual_out, rows, cols, eps, stream);
+        } else if (vectors_per_lane <= 2) {
+            launch_wave<T, 2, kResidual>(x, residual, w, y, residual_out, rows, cols, eps, stream);
+        } else if (vectors_per_lane <= 4) {
+            launch_wave<T, 4, kResidual>(x, residual, w, y, residual_out, rows, cols, eps, stream);
+        } else if (vectors_per_lane <= 8) {
+            launch_wave<T, 8, kResidual>(x, residual, w, y, residual_out, rows, cols, eps, stream);
+        } else {
+            launch_wave<T, 16, kResidual>(x, residual, w, y, residual_out, rows, cols, eps, stream);
+        }
+    } else {
+        const int64_t max_blocks = static_cast<int64_t>(cu_count()) * 8;
+        const int64_t grid = rows < max_blocks ? rows : max_blocks;
+        rmsnorm_block_kernel<T, kResidual>
+            <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+                static_cast<const T*>(x), static_cast<const T*>(residual),
+                static_cast<const T*>(w), static_cast<T*>(y), static_cast<T*>(residual_out), rows,
+                cols, eps);
+    }
+    return check_launch(kResidual ? "launching fused_residual_rmsnorm" : "launching rmsnorm",
+                        stream);
+}
+
+template <bool kResidual>
+cf_status run(const void* x, const void* residual, const void* w, void* y, void* residual_out,
+              cf_dtype dtype, int64_t rows, int64_t cols, float eps, void* stream) {
+    auto s = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case CF_F32:
+            return dispatch<float, kResidual>(x, residual, w, y, residual_out, rows, cols, eps, s);
+        case CF_BF16:
+            return dispatch<bf16_t, kResidual>(x, residual, w, y, residual_out, rows, cols, eps,
+                                               s);
+        case CF_F16:
+            return dispatch<f16_t, kResidual>(x, residual, w, y, residual_out, rows, cols, eps,
+                                              s);
+    }
+    return fail(CF_ERR_UNSUPPORTED, "rmsnorm: unknown dtype %d", static_cast<int>(dtype));
+}
+
+}  // namespace
+}  // namespace cf
+
+extern "C" {
+
+cf_status cf_rmsnorm(const void* x, const void* w, void* y, cf_dtype dtype, int64_t rows,
+                     int64_t cols, float eps, void* stream) {
+    if (rows <= 0 || cols <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && w != nullptr && y != nullptr, "cf_rmsnorm: null pointer");
+    return cf::run<false>(x, nullptr, w, y, nullptr, dtype, rows, cols, eps, stream);
+}
+
+cf_status cf_fused_residual_rmsnorm(const void* x, const void* residual, const void* w, void* y,
+                                    void* residual_out, cf_dtype dtype, int64_t rows,
+                                    int64_t cols, float eps, void* stream) {
+    if (rows <= 0 || cols <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && residual != nullptr && w != nullptr && y != nullptr &&
+                   residual_out != nullptr,
+               "cf_fused_residual_rmsnorm: null pointer");
+    return cf::run<true>(x, residual, w, y, residual_out, dtype, rows, cols, eps, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,366 @@
+// Block-wise symmetric INT8 quantisation for gfx950.
+//
+// Semantics (bit-exact target): the reference's CPU path,
+// python/cudaforge/ops.py:215-229 and cpp/src/bindings.cpp:298-318:
+//
+//   s_b = absmax_b / 127          IEEE fp32 divide
+//   s_b = s_b > 0 ? s_b : 1       applied after the divide (a NaN absmax also
+//                                 lands on 1, since NaN > 0 is false)
+//   q_i = clamp(rint(x_i / s_b), -127, 127), round half to even, NaN -> 0
+//
+// The reference's CUDA kernel (cuda/src/quantization.cu:18-47) tests
+// `absmax > 0` before dividing instead; the two disagree when absmax/127
+// underflows to zero, and this file follows the CPU path.
+//
+// Mapping to CDNA4: a 64-element block is 256 bytes of fp32, so 16 lanes load
+// it with one 16-byte load each; 16 lanes are exactly one DPP row, and the
+// absmax reduces inside the row in 4 DPP steps - no LDS, no barrier, and each
+// wave quantises 4 blocks (8 for 16-bit inputs, 8 lanes per block) per step.
+// The absmax is reduced over the integer bit patterns of |x|, which orders
+// non-negative floats correctly and propagates NaN the way torch.amax does.
+//
+// The per-element divide is the only expensive arithmetic. x * (1/s) is within
+// 2.3e-5 of fl(x/s) for every |x| <= absmax; rint only depends on which side of
+// a half-integer the quotient lies, so the multiply is used unless it lands
+// within 6e-5 of a .5 boundary, where the exact IEEE divide is redone. Blocks
+// with a subnormal scale (1/s would overflow) always divide.
+#include "cf_common.hpp"
+
+namespace cf {
+namespace {
+
+constexpr int kUnroll = 4;
+constexpr float kTieMargin = 6.0e-5f;
+constexpr float kFltMinNormal = 1.17549435e-38f;
+
+struct BlockScale {
+    float s;
+    float inv;
+    bool exact;
+};
+
+__device__ __forceinline__ BlockScale block_scale(uint32_t absmax_bits) {
+    const float absmax = __uint_as_float(absmax_bits);
+    float s = absmax / 127.0f;
+    s = (s > 0.0f) ? s : 1.0f;
+    BlockScale b;
+    b.s = s;
+    b.inv = 1.0f / s;
+    b.exact = !(s >= kFltMinNormal);
+    return b;
+}
+
+/// rint(x / s) clamped to [-127, 127]; NaN gives 0 (what ATen's float->int8
+/// conversion of a NaN yields after torch.clamp propagates it).
+__device__ __forceinline__ int quant_code(float x, const BlockScale& b) {
+    const float quotient = b.exact ? x / b.s : x * b.inv;
+    float r = rintf(quotient);
+    if (fabsf(quotient - r) > 0.5f - kTieMargin) r = rintf(x / b.s);
+    if (r != r) return 0;
+    return static_cast<int>(fminf(fmaxf(r, -127.0f), 127.0f));
+}
+
+__device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+
+/// Load the kPer elements of this lane (zero beyond `count`).
+template <typename T, bool kVec>
+__device__ __forceinline__ void load_lane(const T* __restrict__ x, int64_t e, int64_t count,
+                                          float* v) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    if (kVec && e + kPer <= count) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(x + e);
+        unpack16<T>(raw, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) v[i] = (e + i < count) ? Storage<T>::load(x + e + i) : 0.0f;
+    }
+}
+
+/// Shared body of quantise and fake-quantise. kMode 0 writes codes + scales,
+/// kMode 1 writes q * s in T.
+template <typename T, bool kVec, int kMode>
+__device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __restrict__ q,
+                                           float* __restrict__ scales, T* __restrict__ y,
+                                           int64_t count) {
+    constexpr int kPer = Storage<T>::kPerVec;                  // 4 (fp32) or 8 (16-bit)
+    constexpr int kLanesPerBlock = kQuantBlockSize / kPer;     // 16 or 8
+    constexpr int kBlocksPerStep = kWaveSize / kLanesPerBlock; // 4 or 8
+
+    const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveSize) +
+                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
+    const int64_t base_block = wave * (kBlocksPerStep * kUnroll);
+    const int sub = lane / kLanesPerBlock;
+    const int part = lane % kLanesPerBlock;
+
+    float v[kUnroll][kPer];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t block = base_block + u * kBlocksPerStep + sub;
+        load_lane<T, kVec>(x, block * kQuantBlockSize + part * kPer, count, v[u]);
+    }
+
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const uint32_t a = abs_bits(v[u][i]);
+            m = a > m ? a : m;
+        }
+        m = group_reduce_u32<kLanesPerBlock, MaxU32>(m);
+        const BlockScale b = block_scale(m);
+
+        const int64_t block = base_block + u * kBlocksPerStep + sub;
+        const int64_t e = block * kQuantBlockSize + part * kPer;
+        if (e >= count) continue;
+
+        int codes[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) codes[i] = quant_code(v[u][i], b);
+
+        if constexpr (kMode == 0) {
+            if (part == 0) scales[block] = b.s;
+            if (kVec && e + kPer <= count) {
+                uint32_t w[kPer / 4];
+#pragma unroll
+                for (int j = 0; j < kPer / 4; ++j) {
+                    w[j] = (static_cast<uint32_t>(codes[4 * j]) & 0xFFu) |
+                           ((static_cast<uint32_t>(codes[4 * j + 1]) & 0xFFu) << 8) |
+                           ((static_cast<uint32_t>(codes[4 * j + 2]) & 0xFFu) << 16) |
+                           ((static_cast<uint32_t>(codes[4 * j + 3]) & 0xFFu) << 24);
+                }
+                if constexpr (kPer == 4) {
+                    *reinterpret_cast<uint32_t*>(q + e) = w[0];
+                } else {
+                    *reinterpret_cast<uint2*>(q + e) = make_uint2(w[0], w[1]);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) {
+                    if (e + i < count) q[e + i] = static_cast<int8_t>(codes[i]);
+                }
+            }
+        } else {
+            float out[kPer];
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) out[i] = static_cast<float>(codes[i]) * b.s;
+            if (kVec && e + kPer <= count) {
+                *reinterpret_cast<uint4*>(y + e) = pack16<T>(out);
+            } else {
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) {
+                    if (e + i < count) Storage<T>::store(y + e + i, out[i]);
+                }
+            }
+        }
+    }
+}
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(kDefaultBlockSize) void quantize_kernel(const T* __restrict__ x,
+                                                                     int8_t* __restrict__ q,
+                                                                     float* __restrict__ scales,
+                                                                     int64_t count) {
+    quant_body<T, kVec, 0>(x, q, scales, nullptr, count);
+}
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(kDefaultBlockSize) void fake_quant_kernel(const T* __restrict__ x,
+                                                                       T* __restrict__ y,
+                                                                       int64_t count) {
+    quant_body<T, kVec, 1>(x, nullptr, nullptr, y, count);
+}
+
+/// y = float(q) * s, one multiply, rounded to Tout. Each lane owns kPer
+/// consecutive elements (always inside one block); a wave stores 1 KiB per
+/// step with 16-byte stores.
+template <typename Tout, bool kVec>
+__global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
+    const int8_t* __restrict__ q, const float* __restrict__ scales, Tout* __restrict__ y,
+    int64_t count) {
+    constexpr int kPer = Storage<Tout>::kPerVec;
+    constexpr int64_t kStep = static_cast<int64_t>(kWaveSize) * kPer;
+    const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveSize) +
+                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
+    const int64_t base = wave * kStep * kUnroll + static_cast<int64_t>(lane) * kPer;
+
+    int codes[kUnroll][kPer];
+    float scale[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t e = base + u * kStep;
+        scale[u] = e < count ? scales[e / kQuantBlockSize] : 0.0f;
+        if (kVec && e + kPer <= count) {
+            if constexpr (kPer == 4) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(q + e);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) codes[u][i] = static_cast<int8_t>((w >> (8 * i)) & 0xFFu);
+            } else {
+                const uint2 w = *reinterpret_cast<const uint2*>(q + e);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    codes[u][i] = static_cast<int8_t>((w.x >> (8 * i)) & 0xFFu);
+                    codes[u][4 + i] = static_cast<int8_t>((w.y >> (8 * i)) & 0xFFu);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) codes[u][i] = (e + i < count) ? q[e + i] : 0;
+        }
+    }
+
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t e = base + u * kStep;
+        if (e >= count) continue;
+        float out[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) out[i] = static_cast<float>(codes[u][i]) * scale[u];
+        if (kVec && e + kPer <= count) {
+            *reinterpret_cast<uint4*>(y + e) = pack16<Tout>(out);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                if (e + i < count) Storage<Tout>::store(y + e + i, out[i]);
+            }
+        }
+    }
+}
+
+/// Workgroups needed so that every block (or element step) has a wave.
+template <typename T>
+int64_t quant_grid(int64_t count) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    constexpr int64_t kBlocksPerWave = (kWaveSize / (kQuantBlockSize / kPer)) * kUnroll;
+    const int64_t blocks = ceil_div<int64_t>(count, kQuantBlockSize);
+    const int64_t waves = ceil_div<int64_t>(blocks, kBlocksPerWave);
+    return ceil_div<int64_t>(waves, kDefaultBlockSize / kWaveSize);
+}
+
+template <typename T>
+int64_t dequant_grid(int64_t count) {
+    constexpr int64_t kPerWave = static_cast<int64_t>(kWaveSize) * Storage<T>::kPerVec * kUnroll;
+    const int64_t waves = ceil_div<int64_t>(count, kPerWave);
+    return ceil_div<int64_t>(waves, kDefaultBlockSize / kWaveSize);
+}
+
+constexpr int64_t kMaxGrid = 2147483647;
+
+template <typename T>
+cf_status launch_quantize(const void* x, int8_t* q, float* scales, int64_t count,
+                          hipStream_t stream) {
+    const int64_t grid = quant_grid<T>(count);
+    CF_REQUIRE(grid <= kMaxGrid, "cf_quantize_int8: %lld elements exceed the launch limit",
+               static_cast<long long>(count));
+    constexpr int kPer = Storage<T>::kPerVec;
+    const bool vec = host_aligned(x, 16) && host_aligned(q, kPer);
+    if (vec) {
+        quantize_kernel<T, true><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const T*>(x), q, scales, count);
+    } else {
+        quantize_kernel<T, false><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const T*>(x), q, scales, count);
+    }
+    return check_launch("launching quantize_int8", stream);
+}
+
+template <typename T>
+cf_status launch_fake_quant(const void* x, void* y, int64_t count, hipStream_t stream) {
+    const int64_t grid = quant_grid<T>(count);
+    CF_REQUIRE(grid <= kMaxGrid, "cf_quantize_dequantize: %lld elements exceed the launch limit",
+               static_cast<long long>(count));
+    const bool vec = host_aligned(x, 16) && host_aligned(y, 16);
+    if (vec) {
+        fake_quant_kernel<T, true><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const T*>(x), static_cast<T*>(y), count);
+    } else {
+        fake_quant_kernel<T, false><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const T*>(x), static_cast<T*>(y), count);
+    }
+    return check_launch("launching quantize_dequantize", stream);
+}
+
+template <typename T>
+cf_status launch_dequantize(const int8_t* q, const float* scales, void* y, int64_t count,
+                            hipStream_t stream) {
+    const int64_t grid = dequant_grid<T>(count);
+    CF_REQUIRE(grid <= kMaxGrid, "cf_dequantize_int8: %lld elements exceed the launch limit",
+               static_cast<long long>(count));
+    constexpr int kPer = Storage<T>::kPerVec;
+    const bool vec = host_aligned(q, kPer) && host_aligned(y, 16);
+    if (vec) {
+        dequantize_kernel<T, true><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            q, scales, static_cast<T*>(y), count);
+    } else {
+        dequantize_kernel<T, false><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            q, scales, static_cast<T*>(y), count);
+    }
+    return check_launch("launching dequantize_int8", stream);
+}
+
+}  // namespace
+}  // namespace cf
+
+extern "C" {
+
+int64_t cf_quant_scale_count(int64_t count) {
+    return count <= 0 ? 0 : cf::ceil_div<int64_t>(count, cf::kQuantBlockSize);
+}
+
+cf_status cf_quantize_int8(const void* x, cf_dtype x_dtype, int8_t* q, float* scales,
+                           int64_t count, void* stream) {
+    if (count <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && q != nullptr && scales != nullptr,
+               "cf_quantize_int8: null pointer (x=%p q=%p scales=%p)", x,
+               static_cast<void*>(q), static_cast<void*>(scales));
+    auto s = static_cast<hipStream_t>(stream);
+    switch (x_dtype) {
+        case CF_F32:
+            return cf::launch_quantize<float>(x, q, scales, count, s);
+        case CF_BF16:
+            return cf::launch_quantize<cf::bf16_t>(x, q, scales, count, s);
+        case CF_F16:
+            return cf::launch_quantize<cf::f16_t>(x, q, scales, count, s);
+    }
+    return cf::fail(CF_ERR_UNSUPPORTED, "cf_quantize_int8: unknown input dtype %d",
+                    static_cast<int>(x_dtype));
+}
+
+cf_status cf_dequantize_int8(const int8_t* q, const float* scales, void* y, cf_dtype y_dtype,
+                             int64_t count, void* stream) {
+    if (count <= 0) return CF_OK;
+    CF_REQUIRE(q != nullptr && scales != nullptr && y != nullptr,
+               "cf_dequantize_int8: null pointer");
+    auto s = static_cast<hipStream_t>(stream);
+    switch (y_dtype) {
+        case CF_F32:
+            return cf::launch_dequantize<float>(q, scales, y, count, s);
+        case CF_BF16:
+            return cf::launch_dequantize<cf::bf16_t>(q, scales, y, count, s);
+        case CF_F16:
+            return cf::launch_dequantize<cf::f16_t>(q, scales, y, count, s);
+    }
+    return cf::fail(CF_ERR_UNSUPPORTED, "cf_dequantize_int8: unknown output dtype %d",
+                    static_cast<int>(y_dtype));
+}
+
+cf_status cf_quantize_dequantize(const void* x, void* y, cf_dtype dtype, int64_t count,
+                                 void* stream) {
+    if (count <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && y != nullptr, "cf_quantize_dequantize: null pointer");
+    auto s = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case CF_F32:
+            return cf::launch_fake_quant<float>(x, y, count, s);
+        case CF_BF16:
+            return cf::launch_fake_quant<cf::bf16_t>(x, y, count, s);
+        case CF_F16:
+            return cf::launch_fake_quant<cf::f16_t>(x, y, count, s);
+    }
+    return cf::fail(CF_ERR_UNSUPPORTED, "cf_quantize_dequantize: unknown dtype %d",
+                    static_cast<int>(dtype));
+}
+
+}  // extern "C"

@@ -1,0 +1,188 @@
+// Whole-array sum and per-row sums for gfx950.
+//
+// The reference's bound sum kernel (reduce_sum_warp, cuda/src/reduction.cu:60-89)
+// ends with one global atomicAdd per block, so its result depends on block
+// completion order. Here the sum is a fixed two-stage tree:
+//
+//   stage 1: G workgroups, each reducing one contiguous chunk with 16-byte
+//            loads (four independent accumulators per lane), a DPP wave
+//            reduction and a 4-slot LDS exchange, into partial[G];
+//   stage 2: one workgroup reduces partial[0..G) in a fixed order and writes
+//            (or adds into) *out.
+//
+// G and the chunk size are functions of `count` only, so the same input gives
+// the same bits on any device and on every run.
+#include "cf_common.hpp"
+
+namespace cf {
+namespace {
+
+constexpr int kWavesPerBlock = kDefaultBlockSize / kWaveSize;
+constexpr int64_t kMaxPartials = 2048;
+constexpr int64_t kMinChunk = 8192;
+
+/// Number of stage-1 workgroups for `count` elements.
+int64_t partial_count(int64_t count) {
+    const int64_t wanted = ceil_div<int64_t>(count, kMinChunk);
+    return wanted < kMaxPartials ? (wanted < 1 ? 1 : wanted) : kMaxPartials;
+}
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(kDefaultBlockSize) void sum_stage1_kernel(const T* __restrict__ x,
+                                                                       float* __restrict__ partial,
+                                                                       int64_t count,
+                                                                       int64_t chunk) {
+    __shared__ float slot[kWavesPerBlock];
+    constexpr int kPer = Storage<T>::kPerVec;
+    const int64_t begin = static_cast<int64_t>(blockIdx.x) * chunk;
+    const int64_t end = begin + chunk < count ? begin + chunk : count;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (kVec) {
+        // chunk is a multiple of kPer * blockDim, so every vector is aligned
+        // and lies entirely before `end` unless it straddles `count`.
+        const int64_t step = static_cast<int64_t>(blockDim.x) * kPer;
+        int64_t e = begin + static_cast<int64_t>(threadIdx.x) * kPer;
+        for (; e + kPer <= end; e += step) {
+            float v[kPer];
+            unpack16<T>(*reinterpret_cast<const uint4*>(x + e), v);
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) acc[i & 3] += v[i];
+        }
+        for (int i = 0; i < kPer; ++i) {
+            if (e + i < end) acc[0] += Storage<T>::load(x + e + i);
+        }
+    } else {
+        for (int64_t e = begin + threadIdx.x; e < end; e += blockDim.x) {
+            acc[0] += Storage<T>::load(x + e);
+        }
+    }
+    const float total =
+        block_reduce_f32<kWavesPerBlock, AddF32>((acc[0] + acc[1]) + (acc[2] + acc[3]), slot);
+    if (threadIdx.x == 0) partial[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(kDefaultBlockSize) void sum_stage2_kernel(
+    const float* __restrict__ partial, int64_t partials, float* __restrict__ out, int accumulate) {
+    __shared__ float slot[kWavesPerBlock];
+    float acc = 0.0f;
+    for (int64_t i = threadIdx.x; i < partials; i += blockDim.x) acc += partial[i];
+    const float total = block_reduce_f32<kWavesPerBlock, AddF32>(acc, slot);
+    if (threadIdx.x == 0) *out = accumulate ? *out + total : total;
+}
+
+/// One wave per row; each lane strides the row with 16-byte vectors.
+template <typename T, bool kVec>
+__global__ __launch_bounds__(kDefaultBlockSize) void row_sum_kernel(const T* __restrict__ x,
+                                                                    float* __restrict__ out,
+                                                                    int64_t rows, int64_t cols) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
+                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    for (int64_t row = wave; row < rows; row += waves) {
+        const T* xr = x + row * cols;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (kVec) {
+            for (int64_t e = static_cast<int64_t>(lane) * kPer; e < cols;
+                 e += static_cast<int64_t>(kWaveSize) * kPer) {
+                float v[kPer];
+                unpack16<T>(*reinterpret_cast<const uint4*>(xr + e), v);
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) acc[i & 3] += v[i];
+            }
+        } else {
+            for (int64_t e = lane; e < cols; e += kWaveSize) acc[0] += Storage<T>::load(xr + e);
+        }
+        const float total = wave_reduce_f32<AddF32>((acc[0] + acc[1]) + (acc[2] + acc[3]));
+        if (lane == 0) out[row] = total;
+    }
+}
+
+template <typename T>
+cf_status launch_sum(const void* x, float* out, int64_t count, void* workspace,
+                     int accumulate, hipStream_t stream) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    const int64_t partials = partial_count(count);
+    // Chunk rounded up to whole workgroup strides so every vector stays aligned.
+    const int64_t stride = static_cast<int64_t>(kDefaultBlockSize) * kPer;
+    const int64_t chunk = ceil_div<int64_t>(ceil_div<int64_t>(count, partials), stride) * stride;
+    const int64_t grid = ceil_div<int64_t>(count, chunk);
+    float* partial = static_cast<float*>(workspace);
+    if (host_aligned(x, 16)) {
+        sum_stage1_kernel<T, true><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const T*>(x), partial, count, chunk);
+    } else {
+        sum_stage1_kernel<T, false><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const T*>(x), partial, count, chunk);
+    }
+    sum_stage2_kernel<<<1, kDefaultBlockSize, 0, stream>>>(partial, grid, out, accumulate);
+    return check_launch("launching reduce_sum", stream);
+}
+
+template <typename T>
+cf_status launch_row_sum(const void* x, float* out, int64_t rows, int64_t cols,
+                         hipStream_t stream) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    const int64_t max_waves = static_cast<int64_t>(cu_count()) * 16;
+    const int64_t waves = rows < max_waves ? rows : max_waves;
+    const int64_t grid = ceil_div<int64_t>(waves, kWavesPerBlock);
+    if (cols % kPer == 0 && host_aligned(x, 16)) {
+        row_sum_kernel<T, true><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const T*>(x), out, rows, cols);
+    } else {
+        row_sum_kernel<T, false><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const T*>(x), out, rows, cols);
+    }
+    return check_launch("launching row_sum", stream);
+}
+
+}  // namespace
+}  // namespace cf
+
+extern "C" {
+
+size_t cf_reduce_sum_workspace_bytes(int64_t count) {
+    if (count <= 0) return 0;
+    return static_cast<size_t>(cf::partial_count(count)) * sizeof(float);
+}
+
+cf_status cf_reduce_sum(const void* x, cf_dtype x_dtype, float* out, int64_t count,
+                        void* workspace, size_t workspace_bytes, int accumulate, void* stream) {
+    if (count <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && out != nullptr, "cf_reduce_sum: null pointer");
+    const size_t needed = cf_reduce_sum_workspace_bytes(count);
+    CF_REQUIRE(workspace != nullptr && workspace_bytes >= needed,
+               "cf_reduce_sum: workspace of %zu bytes given, %zu needed", workspace_bytes, needed);
+    CF_REQUIRE(cf::host_aligned(workspace, 4), "cf_reduce_sum: workspace must be 4-byte aligned");
+    auto s = static_cast<hipStream_t>(stream);
+    switch (x_dtype) {
+        case CF_F32:
+            return cf::launch_sum<float>(x, out, count, workspace, accumulate, s);
+        case CF_BF16:
+            return cf::launch_sum<cf::bf16_t>(x, out, count, workspace, accumulate, s);
+        case CF_F16:
+            return cf::launch_sum<cf::f16_t>(x, out, count, workspace, accumulate, s);
+    }
+    return cf::fail(CF_ERR_UNSUPPORTED, "cf_reduce_sum: unknown dtype %d",
+                    static_cast<int>(x_dtype));
+}
+
+cf_status cf_row_sum(const void* x, cf_dtype x_dtype, float* out, int64_t rows, int64_t cols,
+                     void* stream) {
+    if (rows <= 0 || cols <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && out != nullptr, "cf_row_sum: null pointer");
+    auto s = static_cast<hipStream_t>(stream);
+    switch (x_dtype) {
+        case CF_F32:
+            return cf::launch_row_sum<float>(x, out, rows, cols, s);
+        case CF_BF16:
+            return cf::launch_row_sum<cf::bf16_t>(x, out, rows, cols, s);
+        case CF_F16:
+            return cf::launch_row_sum<cf::f16_t>(x, out, rows, cols, s);
+    }
+    return cf::fail(CF_ERR_UNSUPPORTED, "cf_row_sum: unknown dtype %d",
+                    static_cast<int>(x_dtype));
+}
+
+}  // extern "C"

@@ -1,0 +1,152 @@
+// Error plumbing, device facts and the byte-copy calibration kernel.
+//
+// The reference reports failures by throwing cudaforge::CudaError from
+// CUDAFORGE_CHECK / CUDAFORGE_CHECK_LAUNCH
+// (cuda/include/cudaforge/cuda_error.cuh:15-96). A C ABI cannot throw, so each
+// entry point returns a cf_status and leaves its message in a thread-local
+// slot; CUDAFORGE_DEBUG_SYNC keeps its meaning, but is read from the
+// environment at run time rather than fixed at compile time.
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+
+#include "cf_common.hpp"
+
+namespace cf {
+namespace {
+
+thread_local char g_last_error[512] = "no error";
+thread_local int g_last_hip_error = 0;
+
+bool debug_sync_enabled() {
+    static const bool enabled = [] {
+        const char* value = std::getenv("CUDAFORGE_DEBUG_SYNC");
+        return value != nullptr && value[0] != '\0' && value[0] != '0';
+    }();
+    return enabled;
+}
+
+}  // namespace
+
+cf_status fail(cf_status status, const char* format, ...) {
+    va_list args;
+    va_start(args, format);
+    std::vsnprintf(g_last_error, sizeof(g_last_error), format, args);
+    va_end(args);
+    g_last_hip_error = 0;
+    return status;
+}
+
+cf_status fail_hip(hipError_t error, const char* what) {
+    std::snprintf(g_last_error, sizeof(g_last_error), "HIP error %d (%s): %s while %s",
+                  static_cast<int>(error), hipGetErrorName(error), hipGetErrorString(error), what);
+    g_last_hip_error = static_cast<int>(error);
+    return CF_ERR_HIP;
+}
+
+cf_status check_launch(const char* what, hipStream_t stream) {
+    const hipError_t launch = hipGetLastError();
+    if (launch != hipSuccess) return fail_hip(launch, what);
+    if (debug_sync_enabled()) {
+        const hipError_t done = hipStreamSynchronize(stream);
+        if (done != hipSuccess) return fail_hip(done, what);
+    }
+    return CF_OK;
+}
+
+int cu_count() {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mutex;
+    static int cached[kMaxDevices] = {};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return 256;
+    std::lock_guard<std::mutex> lock(mutex);
+    if (cached[device] == 0) {
+        int count = 0;
+        if (hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) !=
+                hipSuccess ||
+            count <= 0) {
+            count = 256;
+        }
+        cached[device] = count;
+    }
+    return cached[device];
+}
+
+namespace {
+
+/// Streaming copy: each lane moves 16-byte vectors, four in flight.
+__global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ src,
+                                                     uint4* __restrict__ dst, int64_t vectors) {
+    constexpr int kUnroll = 4;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (; i + (kUnroll - 1) * stride < vectors; i += kUnroll * stride) {
+        uint4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) v[u] = src[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) dst[i + u * stride] = v[u];
+    }
+    for (; i < vectors; i += stride) dst[i] = src[i];
+}
+
+__global__ void copy_tail_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                 int64_t bytes) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes;
+         i += stride) {
+        dst[i] = src[i];
+    }
+}
+
+}  // namespace
+}  // namespace cf
+
+extern "C" {
+
+const char* cf_last_error(void) { return cf::g_last_error; }
+
+int cf_last_hip_error(void) { return cf::g_last_hip_error; }
+
+int cf_hip_error_is_sticky(int hip_error) {
+    switch (static_cast<hipError_t>(hip_error)) {
+        case hipErrorIllegalAddress:
+        case hipErrorLaunchFailure:
+        case hipErrorLaunchTimeOut:
+        case hipErrorIllegalState:
+        case hipErrorAssert:
+        case hipErrorECCNotCorrectable:
+            return 1;
+        default:
+            return 0;
+    }
+}
+
+int cf_abi_version(void) { return 1; }
+
+cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream) {
+    if (bytes <= 0) return CF_OK;
+    CF_REQUIRE(src != nullptr && dst != nullptr, "cf_copy_bytes: null pointer");
+    auto s = static_cast<hipStream_t>(stream);
+    const bool vec = cf::host_aligned(src, 16) && cf::host_aligned(dst, 16);
+    const int64_t vectors = vec ? bytes / 16 : 0;
+    if (vectors > 0) {
+        const int64_t wanted = cf::ceil_div<int64_t>(vectors, 256 * 4);
+        const int grid = static_cast<int>(wanted < 65536 ? wanted : 65536);
+        cf::copy16_kernel<<<grid, 256, 0, s>>>(static_cast<const uint4*>(src),
+                                               static_cast<uint4*>(dst), vectors);
+    }
+    const int64_t done = vectors * 16;
+    const int64_t rest = bytes - done;
+    if (rest > 0) {
+        const int64_t wanted = cf::ceil_div<int64_t>(rest, 256);
+        const int grid = static_cast<int>(wanted < 65536 ? wanted : 65536);
+        cf::copy_tail_kernel<<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(src) + done,
+                                                  static_cast<uint8_t*>(dst) + done, rest);
+    }
+    return cf::check_launch("launching the byte copy", s);
+}
+
+}  // extern "C"

@@ -1,0 +1,209 @@
+// Row softmax for gfx950.
+//
+// Semantics: torch.softmax(x, dim=-1) (python/cudaforge/ops.py:174-175): fp32
+// arithmetic for every storage type, y = exp(x - max) * (1 / sum), which is
+// the order ATen's vectorised CPU softmax uses. A row whose entries are all
+// -inf yields NaN, as torch does; the causal-masked configuration always has a
+// finite entry in column 0.
+//
+// Design (fast path): one wavefront per row with the row held in registers:
+// one 16-byte-vector read, a DPP max reduction, exp and a DPP sum reduction
+// from registers, then one write - one HBM read and one write per element.
+// The reference's bound kernel is the online variant that reads the row twice
+// (cuda/src/softmax.cu:102-138); the register tile makes the second read and
+// the online rescaling unnecessary. Input and output may have different
+// storage types (bf16 logits -> fp32 probabilities) and may alias when equal:
+// a wave reads its whole row before it writes any of it.
+//
+// Fallback: long rows, unaligned pointers or ragged widths use a workgroup per
+// row with three passes over the row (max, sum, normalise).
+#include "cf_common.hpp"
+
+namespace cf {
+namespace {
+
+constexpr int kWavesPerBlock = kDefaultBlockSize / kWaveSize;
+
+/// Store `n` (4 or 8) floats as Tout at `p` with 16- or 8-byte stores.
+template <typename Tout, int kN>
+__device__ __forceinline__ void store_vec(Tout* p, const float* v) {
+    constexpr int kOutPer = Storage<Tout>::kPerVec;
+    if constexpr (kN == kOutPer) {
+        *reinterpret_cast<uint4*>(p) = pack16<Tout>(v);
+    } else if constexpr (kN == 2 * kOutPer) {
+        reinterpret_cast<uint4*>(p)[0] = pack16<Tout>(v);
+        reinterpret_cast<uint4*>(p)[1] = pack16<Tout>(v + kOutPer);
+    } else {
+        // 4 values into a 16-bit type: one 8-byte store.
+        static_assert(kN == 4 && kOutPer == 8, "unsupported store width");
+        uint2 w;
+        w.x = Storage<Tout>::to_bits(v[0]) | (Storage<Tout>::to_bits(v[1]) << 16);
+        w.y = Storage<Tout>::to_bits(v[2]) | (Storage<Tout>::to_bits(v[3]) << 16);
+        *reinterpret_cast<uint2*>(p) = w;
+    }
+}
+
+template <typename Tin, typename Tout, int kVecs>
+__global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const Tin* x, Tout* y,
+                                                                         int64_t rows,
+                                                                         int64_t cols) {
+    constexpr int kPer = Storage<Tin>::kPerVec;
+    const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
+    const int64_t vec_cols = cols / kPer;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
+                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    const float neg_inf = -__builtin_inff();
+
+    for (int64_t row = wave; row < rows; row += waves) {
+        const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
+        float v[kVecs][kPer];
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t idx = static_cast<int64_t>(j) * kWaveSize + lane;
+            if (idx < vec_cols) {
+                unpack16<Tin>(xr[idx], v[j]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) v[j][i] = neg_inf;
+            }
+        }
+
+        float local_max = neg_inf;
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) local_max = fmaxf(local_max, v[j][i]);
+        }
+        const float row_max = wave_reduce_f32<MaxF32>(local_max);
+
+        float partial[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                v[j][i] = expf(v[j][i] - row_max);
+                partial[i & 1] += v[j][i];
+            }
+        }
+        const float row_sum = wave_reduce_f32<AddF32>(partial[0] + partial[1]);
+        const float inv_sum = 1.0f / row_sum;
+
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t idx = static_cast<int64_t>(j) * kWaveSize + lane;
+            if (idx < vec_cols) {
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) v[j][i] = v[j][i] * inv_sum;
+                store_vec<Tout, kPer>(y + row * cols + idx * kPer, v[j]);
+            }
+        }
+    }
+}
+
+/// Any shape: one workgroup per row, three passes.
+template <typename Tin, typename Tout>
+__global__ __launch_bounds__(kDefaultBlockSize) void softmax_block_kernel(const Tin* x, Tout* y,
+                                                                          int64_t rows,
+                                                                          int64_t cols) {
+    __shared__ float slot[kWavesPerBlock];
+    const float neg_inf = -__builtin_inff();
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const Tin* xr = x + row * cols;
+        float local_max = neg_inf;
+        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+            local_max = fmaxf(local_max, Storage<Tin>::load(xr + c));
+        }
+        const float row_max = block_reduce_f32<kWavesPerBlock, MaxF32>(local_max, slot);
+        float local_sum = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+            local_sum += expf(Storage<Tin>::load(xr + c) - row_max);
+        }
+        const float inv_sum = 1.0f / block_reduce_f32<kWavesPerBlock, AddF32>(local_sum, slot);
+        // When x and y alias, every thread must finish reading before any
+        // writes: the reductions above end in a barrier, and this pass reads
+        // and writes the same element in the same thread.
+        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+            const float e = expf(Storage<Tin>::load(xr + c) - row_max);
+            Storage<Tout>::store(y + row * cols + c, e * inv_sum);
+        }
+    }
+}
+
+template <typename Tin, typename Tout, int kVecs>
+void launch_wave(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t stream) {
+    const int64_t max_waves = static_cast<int64_t>(cu_count()) * 16;
+    const int64_t waves = rows < max_waves ? rows : max_waves;
+    const int64_t grid = ceil_div<int64_t>(waves, kWavesPerBlock);
+    softmax_wave_kernel<Tin, Tout, kVecs>
+        <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+            static_cast<const Tin*>(x), static_cast<Tout*>(y), rows, cols);
+}
+
+template <typename Tin, typename Tout>
+cf_status dispatch(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t stream) {
+    constexpr int kPer = Storage<Tin>::kPerVec;
+    const bool vec = cols % kPer == 0 && host_aligned(x, 16) && host_aligned(y, 16);
+    const int64_t vectors_per_lane = ceil_div<int64_t>(cols / kPer, kWaveSize);
+    if (vec && vectors_per_lane <= 16) {
+        if (vectors_per_lane <= 1) {
+            launch_wave<Tin, Tout, 1>(x, y, rows, cols, stream);
+        } else if (vectors_per_lane <= 2) {
+            launch_wave<Tin, Tout, 2>(x, y, rows, cols, stream);
+        } else if (vectors_per_lane <= 4) {
+            launch_wave<Tin, Tout, 4>(x, y, rows, cols, stream);
+        } else if (vectors_per_lane <= 8) {
+            launch_wave<Tin, Tout, 8>(x, y, rows, cols, stream);
+        } else {
+            launch_wave<Tin, Tout, 16>(x, y, rows, cols, stream);
+        }
+    } else {
+        const int64_t max_blocks = static_cast<int64_t>(cu_count()) * 8;
+        const int64_t grid = rows < max_blocks ? rows : max_blocks;
+        softmax_block_kernel<Tin, Tout><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0,
+                                          stream>>>(static_cast<const Tin*>(x),
+                                                    static_cast<Tout*>(y), rows, cols);
+    }
+    return check_launch("launching softmax", stream);
+}
+
+template <typename Tin>
+cf_status dispatch_out(const void* x, void* y, cf_dtype y_dtype, int64_t rows, int64_t cols,
+                       hipStream_t stream) {
+    switch (y_dtype) {
+        case CF_F32:
+            return dispatch<Tin, float>(x, y, rows, cols, stream);
+        case CF_BF16:
+            return dispatch<Tin, bf16_t>(x, y, rows, cols, stream);
+        case CF_F16:
+            return dispatch<Tin, f16_t>(x, y, rows, cols, stream);
+    }
+    return fail(CF_ERR_UNSUPPORTED, "cf_softmax: unknown output dtype %d",
+                static_cast<int>(y_dtype));
+}
+
+}  // namespace
+}  // namespace cf
+
+extern "C" {
+
+cf_status cf_softmax(const void* x, cf_dtype x_dtype, void* y, cf_dtype y_dtype, int64_t rows,
+                     int64_t cols, void* stream) {
+    if (rows <= 0 || cols <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && y != nullptr, "cf_softmax: null pointer");
+    CF_REQUIRE(x != y || x_dtype == y_dtype,
+               "cf_softmax: input and output may alias only when their dtypes match");
+    auto s = static_cast<hipStream_t>(stream);
+    switch (x_dtype) {
+        case CF_F32:
+            return cf::dispatch_out<float>(x, y, y_dtype, rows, cols, s);
+        case CF_BF16:
+            return cf::dispatch_out<cf::bf16_t>(x, y, y_dtype, rows, cols, s);
+        case CF_F16:
+            return cf::dispatch_out<cf::f16_t>(x, y, y_dtype, rows, cols, s);
+    }
+    return cf::fail(CF_ERR_UNSUPPORTED, "cf_softmax: unknown input dtype %d",
+                    static_cast<int>(x_dtype));
+}
+
+}  // extern "C"

@@ -1,0 +1,234 @@
+/*
+ * cudaforge_hip.h - C ABI of the MI355X (gfx950) custom-op library
+ * `libcudaforge_hip.so`.
+ *
+ * This is the drop-in boundary for CudaForge's custom-op hot path. Every entry
+ * point replaces one host launcher of the reference's CUDA library
+ * (the headers under cuda/include/cudaforge/) and keeps its argument meaning, but with a
+ * plain C signature that any FFI can bind (ctypes, cgo, JNI, N-API):
+ *
+ *   - raw device pointers and element counts (int64_t instead of the
+ *     reference's `int count`, so tensors above 2^31 elements are legal);
+ *   - an explicit dtype tag where the reference had one function per storage
+ *     type (launch_rmsnorm / launch_rmsnorm_half / launch_rmsnorm_bf16);
+ *   - `stream` is a hipStream_t passed as `void*` (NULL = the null stream), so
+ *     this header needs no HIP include. Every launch is asynchronous on that
+ *     stream and nothing here synchronises, except when the environment
+ *     variable CUDAFORGE_DEBUG_SYNC is set (then every entry point waits for
+ *     its stream and reports kernel faults synchronously);
+ *   - no exceptions cross the ABI: each entry point returns a cf_status and
+ *     leaves a message for cf_last_error() (thread-local). The reference threw
+ *     cudaforge::CudaError (cuda/include/cudaforge/cuda_error.cuh:15-69) and
+ *     std::invalid_argument (cuda/src/lora_linear.cu:263-265).
+ *
+ * Empty inputs (count <= 0, rows <= 0 or cols <= 0) return CF_OK without
+ * launching anything, as every reference launcher does.
+ *
+ * Nothing in this library allocates device memory. Entry points that need
+ * scratch space take a caller-provided `workspace` and publish its size through
+ * a *_workspace_bytes() query, like the reference's lora_workspace_bytes
+ * (cuda/include/cudaforge/lora_linear.cuh:62).
+ */
+#ifndef CUDAFORGE_HIP_H
+#define CUDAFORGE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status, dtypes, library facts ------------------------------------ */
+
+typedef enum cf_status {
+    CF_OK = 0,
+    CF_ERR_INVALID_ARGUMENT = 1, /* shape, pointer, alignment or size error  */
+    CF_ERR_UNSUPPORTED = 2,      /* dtype or shape combination with no kernel */
+    CF_ERR_HIP = 3,              /* the HIP runtime reported an error         */
+} cf_status;
+
+typedef enum cf_dtype {
+    CF_F32 = 0,
+    CF_F16 = 1,
+    CF_BF16 = 2,
+} cf_dtype;
+
+/* Elements per quantisation block. Same value as kQuantBlockSize
+ * (cuda/include/cudaforge/quantization.cuh:18) and QUANT_BLOCK_SIZE
+ * (python/cudaforge/ops.py:41). */
+#define CF_QUANT_BLOCK_SIZE 64
+
+/* Message describing the most recent failure on the calling thread; the text
+ * the reference put in CudaError::what() (cuda/include/cudaforge/cuda_error.cuh:44-51). */
+const char* cf_last_error(void);
+
+/* hipError_t value behind the most recent CF_ERR_HIP on this thread (0 if the
+ * last failure was not a HIP error). Replaces CudaError::status()
+ * (cuda/include/cudaforge/cuda_error.cuh:21). */
+int cf_last_hip_error(void);
+
+/* True when the hipError_t names a fault that has poisoned the context
+ * (illegal address, launch failure, ...). Replaces CudaError::is_sticky()
+ * (cuda/include/cudaforge/cuda_error.cuh:25-39). */
+int cf_hip_error_is_sticky(int hip_error);
+
+/* ABI version of this header; bumped on any incompatible change. It has no
+ * counterpart in the reference (a C++ API needs none). */
+int cf_abi_version(void);
+
+/* ---- block-wise INT8 quantisation -------------------------------------- */
+
+/* Number of block scales `count` elements need: ceil(count / 64), 0 for
+ * count <= 0. Replaces quant_scale_count (cuda/include/cudaforge/quantization.cuh:54,
+ * cuda/src/quantization.cu:80-82). */
+int64_t cf_quant_scale_count(int64_t count);
+
+/* Symmetric absmax INT8 quantisation over 64-element blocks of the flattened
+ * input:  s_b = absmax_b / 127 (IEEE fp32 divide; 1 when that is not > 0),
+ *         q_i = clamp(rint(x_i / s_b), -127, 127)  (round half to even;
+ *               NaN codes to 0).
+ * `x` is fp32, fp16 or bf16 (`x_dtype`); half inputs are widened exactly to
+ * fp32 first. `q` holds `count` int8 codes, `scales` cf_quant_scale_count(count)
+ * fp32 scales. Bit-identical to the reference's CPU semantics
+ * (python/cudaforge/ops.py:215-229, cpp/src/bindings.cpp:298-318).
+ * Replaces launch_quantize_int8 (cuda/include/cudaforge/quantization.cuh:40-41). */
+cf_status cf_quantize_int8(const void* x, cf_dtype x_dtype, int8_t* q, float* scales,
+                           int64_t count, void* stream);
+
+/* y_i = (fp32)q_i * s_{i/64}, one IEEE multiply, then rounded to `y_dtype`
+ * (round to nearest even) when that is fp16/bf16.
+ * Replaces launch_dequantize_int8 (cuda/include/cudaforge/quantization.cuh:45-46);
+ * fp32 output is the reference's dequantize_int8 (python/cudaforge/ops.py:232-240),
+ * half output equals that followed by `.to(dtype)`. */
+cf_status cf_dequantize_int8(const int8_t* q, const float* scales, void* y, cf_dtype y_dtype,
+                             int64_t count, void* stream);
+
+/* Quantise then dequantise in registers ("fake quantisation"); `y` has the
+ * dtype of `x`. Equals cf_quantize_int8 followed by cf_dequantize_int8.
+ * Replaces launch_quantize_dequantize (cuda/include/cudaforge/quantization.cuh:51). */
+cf_status cf_quantize_dequantize(const void* x, void* y, cf_dtype dtype, int64_t count,
+                                 void* stream);
+
+/* ---- RMSNorm ------------------------------------------------------------ */
+
+/* y = (x * rsqrt(mean(x^2) + eps)) * w per row of a row-major [rows, cols]
+ * matrix; fp32 arithmetic for every storage dtype; eps inside the sqrt.
+ * `x`, `w`, `y` share `dtype`. Replaces launch_rmsnorm / launch_rmsnorm_half /
+ * launch_rmsnorm_bf16 (cuda/include/cudaforge/rmsnorm.cuh:35-62); semantics of
+ * _rmsnorm_reference (python/cudaforge/ops.py:164-171). */
+cf_status cf_rmsnorm(const void* x, const void* w, void* y, cf_dtype dtype, int64_t rows,
+                     int64_t cols, float eps, void* stream);
+
+/* r = x + residual; y = rmsnorm(r) * w. Writes both `y` and `residual_out`.
+ * Replaces launch_fused_residual_rmsnorm (cuda/include/cudaforge/fused_norm.cuh:38-40);
+ * semantics of _fused_residual_rmsnorm_reference (python/cudaforge/ops.py:188-192). */
+cf_status cf_fused_residual_rmsnorm(const void* x, const void* residual, const void* w, void* y,
+                                    void* residual_out, cf_dtype dtype, int64_t rows,
+                                    int64_t cols, float eps, void* stream);
+
+/* ---- softmax ------------------------------------------------------------ */
+
+/* Numerically stable softmax over the last dim of a row-major [rows, cols]
+ * matrix, fp32 arithmetic: y = exp(x - max) * (1 / sum exp(x - max)).
+ * `y_dtype` may differ from `x_dtype` (e.g. bf16 logits -> fp32 probabilities).
+ * `x` and `y` may alias when the dtypes match. Replaces launch_softmax /
+ * launch_softmax_half / launch_softmax_bf16 (cuda/include/cudaforge/softmax.cuh:43-65);
+ * semantics of torch.softmax(x, -1) (python/cudaforge/ops.py:174-175). */
+cf_status cf_softmax(const void* x, cf_dtype x_dtype, void* y, cf_dtype y_dtype, int64_t rows,
+                     int64_t cols, void* stream);
+
+/* ---- reductions --------------------------------------------------------- */
+
+/* Bytes of workspace cf_reduce_sum needs for `count` elements (the stage-1
+ * partial sums). The reference needs none because it reduces with atomics
+ * into the zeroed output (cuda/src/reduction.cu:60-89). */
+size_t cf_reduce_sum_workspace_bytes(int64_t count);
+
+/* Sum of `count` elements (fp32 accumulation) into the single fp32 `*out`.
+ * With accumulate != 0 the sum is added to `*out` (the reference launcher's
+ * contract: cuda/include/cudaforge/reduction.cuh:36-42); with 0 it overwrites.
+ * Deterministic: a fixed two-stage tree whose shape depends only on `count`.
+ * Replaces launch_reduce_sum (cuda/include/cudaforge/reduction.cuh:43-44). */
+cf_status cf_reduce_sum(const void* x, cf_dtype x_dtype, float* out, int64_t count,
+                        void* workspace, size_t workspace_bytes, int accumulate, void* stream);
+
+/* Per-row sums of a row-major [rows, cols] matrix into fp32 `out[rows]`.
+ * Replaces launch_row_sum (cuda/include/cudaforge/reduction.cuh:48). */
+cf_status cf_row_sum(const void* x, cf_dtype x_dtype, float* out, int64_t rows, int64_t cols,
+                     void* stream);
+
+/* ---- LoRA linear -------------------------------------------------------- */
+
+/* Bytes of workspace cf_lora_linear needs: the batch x rank adapter
+ * intermediate (fp32). Replaces lora_workspace_bytes
+ * (cuda/include/cudaforge/lora_linear.cuh:62). */
+size_t cf_lora_workspace_bytes(int64_t batch, int64_t rank);
+
+/* y = x @ w + scale * ((x @ a) @ b), the reference's operator layout
+ * (cuda/include/cudaforge/lora_linear.cuh:26-31, python/cudaforge/ops.py:289-332):
+ *   x [batch, in]   w [in, out]   a [in, rank]   b [rank, out]   y [batch, out]
+ * all row-major and of one dtype (fp32 or bf16). fp32 accumulation; for bf16 the
+ * adapter intermediate x @ a is rounded to bf16 before the up-projection, as the
+ * reference's ATen path does. When `xa_out` is non-NULL the fp32 adapter
+ * intermediate x @ a ([batch, rank], before that rounding) is also written
+ * there (the autograd path keeps it for the backward). rank <= 64.
+ * Replaces launch_lora_linear (cuda/include/cudaforge/lora_linear.cuh:49-51). */
+cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void* b, void* y,
+                         float* xa_out, cf_dtype dtype, int64_t batch, int64_t in_features,
+                         int64_t out_features, int64_t rank, float scale, void* stream);
+
+/* c[m, n] = a[m, k] @ b[k, n], row-major, one dtype (fp32 or bf16), fp32
+ * accumulation. Replaces launch_matmul (cuda/include/cudaforge/lora_linear.cuh:57-58). */
+cf_status cf_matmul(const void* a, const void* b, void* c, cf_dtype dtype, int64_t m, int64_t n,
+                    int64_t k, void* stream);
+
+/* Bytes of workspace cf_lora_backward needs. The reference has no backward
+ * kernel to size (cpp/src/bindings.cpp:369-377 guards the operator instead). */
+size_t cf_lora_backward_workspace_bytes(int64_t batch, int64_t in_features, int64_t out_features,
+                                        int64_t rank);
+
+/* Adapter gradients of y = x @ w + scale * (x @ a) @ b, op layout:
+ *   grad_a [in, rank]  = scale * x^T (dy @ b^T)
+ *   grad_b [rank, out] = scale * (x @ a)^T dy
+ * `xa` is the fp32 adapter intermediate x @ a [batch, rank] from the forward
+ * (cf_lora_linear's xa_out); the bf16 path rounds it to bf16 first, as the
+ * reference's ATen autograd sees the bf16 tensor. Gradients are written in
+ * `dtype` (fp32 or bf16) after fp32 accumulation. These are the derivatives
+ * ATen autograd produces for _lora_linear_reference (python/cudaforge/ops.py:178-185,
+ * tests/python/test_autograd.py:81-91); the reference has no backward kernel
+ * and guards the operator instead (cpp/src/bindings.cpp:369-377). */
+cf_status cf_lora_backward(const void* x, const void* dy, const void* b, const float* xa,
+                           void* grad_a, void* grad_b, cf_dtype dtype, int64_t batch,
+                           int64_t in_features, int64_t out_features, int64_t rank, float scale,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- elementwise activations ------------------------------------------- */
+
+/* silu(x) = x * sigmoid(x), fp32 arithmetic for every dtype.
+ * Replaces launch_silu (cuda/include/cudaforge/activations.cuh:25). */
+cf_status cf_silu(const void* x, void* y, cf_dtype dtype, int64_t count, void* stream);
+
+/* GELU, tanh approximation, fp32 arithmetic.
+ * Replaces launch_gelu (cuda/include/cudaforge/activations.cuh:77). */
+cf_status cf_gelu(const void* x, void* y, cf_dtype dtype, int64_t count, void* stream);
+
+/* silu(gate) * up, fp32 arithmetic, one rounding to the storage type.
+ * Replaces launch_swiglu / launch_swiglu_half / launch_swiglu_bf16
+ * (cuda/include/cudaforge/activations.cuh:47-70). */
+cf_status cf_swiglu(const void* gate, const void* up, void* y, cf_dtype dtype, int64_t count,
+                    void* stream);
+
+/* ---- measurement helper ------------------------------------------------- */
+
+/* Plain device-to-device copy of `bytes` bytes through a streaming kernel
+ * (16-byte loads and stores). It has no counterpart in the reference: it is
+ * the known-size kernel used to calibrate hardware byte counters and to
+ * measure the achievable HBM bandwidth next to the ops above. */
+cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUDAFORGE_HIP_H */

@@ -1,0 +1,117 @@
+"""float64 restatements of the floating-point ops (test infrastructure only).
+
+Each function takes the values the kernel receives (16-bit inputs already
+widened from their stored bits) and returns the float64 result before the
+final rounding to the output type, so a test can apply its tolerance - or,
+for bf16 outputs, compare against the same value rounded once. Citations are
+to the reference semantics each follows.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even, NaN -> 0x7FC0."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    return np.where(nan, np.uint16(0x7FC0), rounded).astype(np.uint16)
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """Round (via fp32) to the nearest bf16 value; returned as float64."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(x, dtype=np.float32))).astype(np.float64)
+
+
+def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """(x * rsqrt(mean(x^2) + eps)) * w per row (python/cudaforge/ops.py:164-171).
+
+    eps is added in fp32 by the reference (variance + eps on a float32
+    tensor); it is taken here as the fp32 value of eps."""
+    x64 = np.asarray(x, dtype=np.float64)
+    mean = np.mean(x64 * x64, axis=-1, keepdims=True)
+    inv = 1.0 / np.sqrt(mean + float(np.float32(eps)))
+    return (x64 * inv) * np.asarray(weight, dtype=np.float64)
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    """exp(x - max) / sum per row (torch.softmax, python/cudaforge/ops.py:174-175)."""
+    x64 = np.asarray(x, dtype=np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        shifted = x64 - np.max(x64, axis=-1, keepdims=True)
+        e = np.exp(shifted)
+        return e / np.sum(e, axis=-1, keepdims=True)
+
+
+def sum_exact(x: np.ndarray) -> float:
+    """Correctly rounded sum of the values (math.fsum)."""
+    return math.fsum(np.asarray(x, dtype=np.float64).reshape(-1).tolist())
+
+
+def lora_linear(
+    x: np.ndarray,
+    w: np.ndarray,
+    a: np.ndarray,
+    b: np.ndarray,
+    scale: float,
+    round_intermediate: bool,
+) -> np.ndarray:
+    """x @ w + scale * ((x @ a) @ b), op layout (python/cudaforge/ops.py:178-185).
+
+    With round_intermediate the adapter intermediate x @ a is rounded to bf16
+    first, as the reference's bf16 ATen path materialises it as a bf16 tensor."""
+    x64 = np.asarray(x, dtype=np.float64)
+    xa = x64 @ np.asarray(a, dtype=np.float64)
+    if round_intermediate:
+        xa = round_bf16(xa)
+    return x64 @ np.asarray(w, dtype=np.float64) + scale * (xa @ np.asarray(b, dtype=np.float64))
+
+
+def lora_backward(
+    x: np.ndarray,
+    dy: np.ndarray,
+    b: np.ndarray,
+    xa: np.ndarray,
+    scale: float,
+    round_intermediate: bool,
+) -> tuple[np.ndarray, np.ndarray]:
+    """Adapter gradients of x @ w + s * (x @ a) @ b in op layout:
+    grad_a = s * x^T (dy @ b^T), grad_b = s * (x @ a)^T dy
+    (tests/python/test_autograd.py:81-91 checks the reference produces them).
+
+    With round_intermediate, dy @ b^T and x @ a are rounded to bf16, the
+    tensors ATen's bf16 autograd sees."""
+    x64 = np.asarray(x, dtype=np.float64)
+    dy64 = np.asarray(dy, dtype=np.float64)
+    g = dy64 @ np.asarray(b, dtype=np.float64).T
+    p = np.asarray(xa, dtype=np.float64)
+    if round_intermediate:
+        g = round_bf16(g)
+        p = round_bf16(p)
+    return scale * (x64.T @ g), scale * (p.T @ dy64)
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    """x * sigmoid(x) (python/cudaforge/ops.py:195-196)."""
+    x64 = np.asarray(x, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return x64 / (1.0 + np.exp(-x64))
+
+
+def gelu_tanh(x: np.ndarray) -> np.ndarray:
+    """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) (python/cudaforge/ops.py:208-212)."""
+    x64 = np.asarray(x, dtype=np.float64)
+    return 0.5 * x64 * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (x64 + 0.044715 * x64**3)))
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """silu(gate) * up (python/cudaforge/ops.py:199-205)."""
+    return silu(gate) * np.asarray(up, dtype=np.float64)

@@ -1,0 +1,107 @@
+"""The C ABI library: loads, exports every declared symbol, host-only logic.
+
+No compute calls here (no GPU on the CPU test host): only entry points that
+return before touching HIP - size queries, argument validation, empty inputs.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from cuda_force_amd import _lib
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_every_declared_function_is_exported_and_bound(lib):
+    declared = _lib.declared_functions()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/cudaforge_hip.h but not exported"
+    assert set(declared) == set(_lib.SIGNATURES), "ctypes signatures out of step with the header"
+
+
+def test_every_header_function_cites_a_reference_interface_or_says_it_has_none():
+    text = _lib.HEADER.read_text(encoding="utf-8")
+    for name in _lib.declared_functions():
+        decl = re.search(rf"^[a-z_0-9 ]+\**\s*{name}\(", text, re.M).start()
+        comment = text[max(0, text.rfind("/*", 0, decl)) : decl]
+        flat = " ".join(comment.replace("*", " ").split())
+        assert re.search(r"\.(cuh|cu|cpp|py|hpp):\d+|no counterpart in the reference", flat), (
+            f"{name} has no reference citation"
+        )
+
+
+def test_the_block_size_and_scale_count(lib):
+    text = _lib.HEADER.read_text(encoding="utf-8")
+    assert re.search(r"#define CF_QUANT_BLOCK_SIZE 64\b", text)
+    assert [lib.cf_quant_scale_count(n) for n in (-5, 0, 1, 64, 65, 4096 * 4096)] == [0, 0, 1, 1, 2, 262144]
+
+
+def test_workspace_queries(lib):
+    assert lib.cf_lora_workspace_bytes(8, 16) == 8 * 16 * 4
+    assert lib.cf_lora_workspace_bytes(0, 16) == 0
+    assert lib.cf_reduce_sum_workspace_bytes(0) == 0
+    assert lib.cf_reduce_sum_workspace_bytes(1) == 4
+    assert lib.cf_reduce_sum_workspace_bytes(1 << 30) == 2048 * 4
+    assert lib.cf_lora_backward_workspace_bytes(8192, 4096, 4096, 16) >= 8192 * 16 * 4
+    assert lib.cf_abi_version() == 1
+
+
+def test_empty_inputs_return_ok_without_touching_the_device(lib):
+    null = ctypes.c_void_p(0)
+    assert lib.cf_quantize_int8(null, _lib.CF_F32, null, null, 0, null) == _lib.CF_OK
+    assert lib.cf_dequantize_int8(null, null, null, _lib.CF_F32, -1, null) == _lib.CF_OK
+    assert lib.cf_rmsnorm(null, null, null, _lib.CF_BF16, 0, 4096, 1e-6, null) == _lib.CF_OK
+    assert lib.cf_softmax(null, _lib.CF_F32, null, _lib.CF_F32, 5, 0, null) == _lib.CF_OK
+    assert lib.cf_lora_linear(null, null, null, null, null, null, _lib.CF_BF16, 0, 8, 8, 2, 1.0, null) == _lib.CF_OK
+
+
+def test_invalid_arguments_are_reported_not_thrown(lib):
+    null = ctypes.c_void_p(0)
+    status = lib.cf_quantize_int8(null, _lib.CF_F32, null, null, 10, null)
+    assert status == _lib.CF_ERR_INVALID_ARGUMENT
+    assert b"null pointer" in lib.cf_last_error()
+    status = lib.cf_lora_linear(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                ctypes.c_void_p(16), ctypes.c_void_p(16), null, _lib.CF_BF16,
+                                8, 8, 8, 65, 1.0, null)
+    assert status == _lib.CF_ERR_INVALID_ARGUMENT
+    assert b"rank 65" in lib.cf_last_error()
+    status = lib.cf_lora_linear(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                ctypes.c_void_p(16), ctypes.c_void_p(16), null, _lib.CF_F16,
+                                8, 8, 8, 4, 1.0, null)
+    assert status == _lib.CF_ERR_INVALID_ARGUMENT
+    assert b"float16" in lib.cf_last_error()
+    status = lib.cf_reduce_sum(ctypes.c_void_p(16), _lib.CF_F32, ctypes.c_void_p(16), 1000,
+                               null, 0, 0, null)
+    assert status == _lib.CF_ERR_INVALID_ARGUMENT
+    assert b"workspace" in lib.cf_last_error()
+
+
+def test_sticky_error_classification(lib):
+    # hipErrorIllegalAddress (700) poisons the context; hipErrorInvalidValue (1) does not.
+    assert lib.cf_hip_error_is_sticky(700) == 1
+    assert lib.cf_hip_error_is_sticky(1) == 0
+
+
+def test_the_error_slot_is_per_thread(lib):
+    import threading
+
+    null = ctypes.c_void_p(0)
+    lib.cf_quantize_int8(null, _lib.CF_F32, null, null, 10, null)
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.cf_last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == b"no error"
+    assert b"null pointer" in lib.cf_last_error()

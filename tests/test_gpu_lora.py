@@ -1,0 +1,180 @@
+"""GPU parity of the LoRA linear (forward, adapter backward) and matmul.
+
+Tolerances: fp32 outputs |got - exact| <= 1e-4 |exact| + 1e-4 max|exact|
+(the reference's CUDA tests allow 1e-3 against a double host reference,
+tests/cuda/test_lora.cu:220-222); bf16 outputs
+|got - exact| <= 1e-2 |exact| + 1e-3 max|exact| - 1e-2 relative with an
+absolute floor at 0.1% of the output's scale for entries near zero, where a
+bf16 GEMM's rounding of the accumulator (2^-9 of |y|) and of the adapter
+intermediate dominate. `exact` is the float64 oracle on the same bf16 inputs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import gpu_util as g
+from tests.conftest import load_golden, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_gemm_close(got_stored: np.ndarray, exact: np.ndarray, dtype: str, what: str) -> None:
+    got = g.host_values(got_stored, dtype).astype(np.float64)
+    rel, floor = (1e-4, 1e-4) if dtype == "f32" else (1e-2, 1e-3)
+    scale = np.max(np.abs(exact)) if exact.size else 0.0
+    err = np.abs(got - exact)
+    bad = np.flatnonzero((err > rel * np.abs(exact) + floor * scale).reshape(-1))
+    assert bad.size == 0, f"{what}: {bad.size} out of tolerance, max err {err.max():.3e} (scale {scale:.3e})"
+
+
+def make_operands(m: int, k: int, n: int, r: int, dtype: str, seed: int):
+    gen = rng(seed)
+    x = g.storage_bits(gen.standard_normal((m, k)).astype(np.float32), dtype)
+    w = g.storage_bits((0.02 * gen.standard_normal((k, n))).astype(np.float32), dtype)
+    a = g.storage_bits((gen.standard_normal((k, r)) / 64).astype(np.float32), dtype)
+    b = g.storage_bits((0.02 * gen.standard_normal((r, n))).astype(np.float32), dtype)
+    return x, w, a, b
+
+
+def run_lora(x, w, a, b, dtype: str, scale: float, want_xa: bool = True):
+    m, k = x.shape
+    n = w.shape[1]
+    r = a.shape[1]
+    xg, wg, ag, bg = (g.to_gpu(t, dtype) for t in (x, w, a, b))
+    yg = g.empty((m, n), g.torch_dtype(dtype))
+    xa = g.empty((m, max(r, 1)), torch.float32)
+    g.call("cf_lora_linear", xg.data_ptr(), wg.data_ptr(), ag.data_ptr(), bg.data_ptr(), yg.data_ptr(),
+           xa.data_ptr() if want_xa else 0, g.cf(dtype), m, k, n, r, scale, g.stream())
+    torch.cuda.synchronize()
+    return g.to_host(yg), g.to_host(xa)
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 4, 2), (4, 64, 32, 8), (7, 129, 65, 3), (16, 256, 256, 16), (33, 100, 50, 4)])
+def test_fp32_reference_shapes(shape):
+    m, k, n, r = shape
+    gen = rng(sum(shape))
+    x, w, a, b = (gen.standard_normal(s).astype(np.float32) for s in ((m, k), (k, n), (k, r), (r, n)))
+    y, _ = run_lora(x, w, a, b, "f32", 0.25)
+    assert_gemm_close(y, oracle.lora_linear(x, w, a, b, 0.25, False), "f32", f"fp32 {shape}")
+
+
+def test_fp32_golden_cases():
+    for case, d in load_golden("lora.npz").items():
+        if not case.startswith("f32"):
+            continue
+        y, _ = run_lora(d["x"], d["w"], d["a"], d["b"], "f32", 0.25)
+        assert_gemm_close(y, oracle.lora_linear(d["x"], d["w"], d["a"], d["b"], 0.25, False), "f32", case)
+
+
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (256, 256, 256, 16),    # one tile
+        (512, 1024, 768, 16),   # several tiles, K loop
+        (300, 512, 264, 16),    # ragged M and N (N a multiple of 8 only)
+        (256, 512, 256, 8),     # rank below 16
+        (64, 128, 512, 3),      # odd rank
+        (1024, 4096, 1024, 16), # long K
+    ],
+)
+def test_fused_bf16_matches_the_oracle(shape):
+    m, k, n, r = shape
+    x, w, a, b = make_operands(m, k, n, r, "bf16", seed=m + k + n + r)
+    y, xa = run_lora(x, w, a, b, "bf16", 2.0)
+    xv, wv, av, bv = (g.host_values(t, "bf16") for t in (x, w, a, b))
+    assert_gemm_close(y, oracle.lora_linear(xv, wv, av, bv, 2.0, True), "bf16", f"bf16 {shape}")
+    np.testing.assert_allclose(xa[:, :r], xv.astype(np.float64) @ av, rtol=1e-4, atol=1e-4)
+
+
+def test_bf16_golden_case():
+    d = load_golden("lora.npz")["bf16_64x256x128r16"]
+    y, _ = run_lora(d["x"], d["w"], d["a"], d["b"], "bf16", 2.0)
+    vals = [g.host_values(d[k], "bf16") for k in "xwab"]
+    assert_gemm_close(y, oracle.lora_linear(*vals, 2.0, True), "bf16", "golden bf16")
+
+
+def test_bf16_unfused_shapes_take_the_generic_path():
+    # K not a multiple of 64 and rank above 16 cannot take the fused kernel.
+    for shape in ((33, 100, 48, 4), (64, 256, 128, 32)):
+        m, k, n, r = shape
+        x, w, a, b = make_operands(m, k, n, r, "bf16", seed=sum(shape))
+        y, _ = run_lora(x, w, a, b, "bf16", 2.0)
+        vals = [g.host_values(t, "bf16") for t in (x, w, a, b)]
+        assert_gemm_close(y, oracle.lora_linear(*vals, 2.0, True), "bf16", f"generic {shape}")
+
+
+def test_zero_b_reduces_to_the_base_layer_and_scale_is_linear():
+    x, w, a, b = make_operands(256, 512, 256, 16, "bf16", seed=5)
+    zero_b = np.zeros_like(b)
+    y0, _ = run_lora(x, w, a, zero_b, "bf16", 2.0)
+    xv, wv = g.host_values(x, "bf16"), g.host_values(w, "bf16")
+    assert_gemm_close(y0, xv.astype(np.float64) @ wv, "bf16", "B = 0")
+    zero_w = np.zeros_like(w)
+    y1, _ = run_lora(x, zero_w, a, b, "bf16", 1.0)
+    y2, _ = run_lora(x, zero_w, a, b, "bf16", 2.0)
+    # Doubling a power-of-two scale doubles every bf16 output exactly.
+    np.testing.assert_array_equal(g.host_values(y2, "bf16"), 2 * g.host_values(y1, "bf16"))
+
+
+def test_config3_full_size():
+    g.announce("config 3: fused LoRA bf16 8192x4096x4096 r16")
+    gen = rng(3003)
+    m, k, n, r = 8192, 4096, 4096, 16
+    # PEFT layout, then the operator layout the reference's test maps it to
+    # (tests/python/test_lora.py:54-70): op(x, W^T, A^T, B^T, alpha / r).
+    x = oracle.f32_to_bf16_bits(gen.standard_normal((m, k), dtype=np.float32))
+    W = oracle.f32_to_bf16_bits((0.02 * gen.standard_normal((n, k), dtype=np.float32)))
+    A = oracle.f32_to_bf16_bits((gen.standard_normal((r, k), dtype=np.float32) / 64))
+    B = oracle.f32_to_bf16_bits((0.02 * gen.standard_normal((n, r), dtype=np.float32)))
+    w, a, b = (np.ascontiguousarray(t.T) for t in (W, A, B))
+    y, xa = run_lora(x, w, a, b, "bf16", 32 / 16)
+    rows = rng(3004).choice(m, size=48, replace=False)
+    xv = g.host_values(x[rows], "bf16")
+    wv, av, bv = (g.host_values(t, "bf16") for t in (w, a, b))
+    assert_gemm_close(y[rows], oracle.lora_linear(xv, wv, av, bv, 2.0, True), "bf16", "config 3 (48 rows)")
+    np.testing.assert_allclose(xa[rows], xv.astype(np.float64) @ av, rtol=1e-3, atol=1e-3)
+    assert np.isfinite(g.host_values(y, "bf16")).all()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(64, 96, 80, 4), (300, 256, 520, 16), (8192, 512, 384, 16), (1000, 130, 70, 24)])
+def test_adapter_backward(dtype, shape):
+    m, k, n, r = shape
+    gen = rng(sum(shape) + 1)
+    x = g.storage_bits(gen.standard_normal((m, k)).astype(np.float32), dtype)
+    dy = g.storage_bits(gen.standard_normal((m, n)).astype(np.float32), dtype)
+    b = g.storage_bits((0.02 * gen.standard_normal((r, n))).astype(np.float32), dtype)
+    xa = (gen.standard_normal((m, r)) * 0.5).astype(np.float32)
+    xg, dyg, bg = g.to_gpu(x, dtype), g.to_gpu(dy, dtype), g.to_gpu(b, dtype)
+    xag = g.to_gpu(xa)
+    ga = g.empty((k, r), g.torch_dtype(dtype))
+    gb = g.empty((r, n), g.torch_dtype(dtype))
+    nbytes = g.lib().cf_lora_backward_workspace_bytes(m, k, n, r)
+    ws = g.empty(nbytes, torch.uint8)
+    g.call("cf_lora_backward", xg.data_ptr(), dyg.data_ptr(), bg.data_ptr(), xag.data_ptr(), ga.data_ptr(),
+           gb.data_ptr(), g.cf(dtype), m, k, n, r, 2.0, ws.data_ptr(), nbytes, g.stream())
+    torch.cuda.synchronize()
+    exact_a, exact_b = oracle.lora_backward(
+        g.host_values(x, dtype), g.host_values(dy, dtype), g.host_values(b, dtype), xa, 2.0, dtype == "bf16"
+    )
+    assert_gemm_close(g.to_host(ga), exact_a, dtype, f"grad_a {dtype} {shape}")
+    assert_gemm_close(g.to_host(gb), exact_b, dtype, f"grad_b {dtype} {shape}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(1, 8, 4, 2), (7, 129, 65, 3), (128, 256, 256, 16)])
+def test_matmul(dtype, shape):
+    m, k, n, _ = shape
+    gen = rng(m * k + n)
+    a = g.storage_bits(gen.standard_normal((m, k)).astype(np.float32), dtype)
+    b = g.storage_bits(gen.standard_normal((k, n)).astype(np.float32), dtype)
+    ag, bg = g.to_gpu(a, dtype), g.to_gpu(b, dtype)
+    cg = g.empty((m, n), g.torch_dtype(dtype))
+    g.call("cf_matmul", ag.data_ptr(), bg.data_ptr(), cg.data_ptr(), g.cf(dtype), m, n, k, g.stream())
+    torch.cuda.synchronize()
+    exact = g.host_values(a, dtype).astype(np.float64) @ g.host_values(b, dtype)
+    assert_gemm_close(g.to_host(cg), exact, dtype, f"matmul {dtype} {shape}")

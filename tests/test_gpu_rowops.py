@@ -1,0 +1,272 @@
+"""GPU parity of RMSNorm, residual+RMSNorm, softmax, the sums and the activations.
+
+Tolerances (stated per BASELINE): fp32 outputs within 1e-5 relative of the
+float64 oracle (elementwise |got - exact| <= 1e-5 |exact| + 1e-7); bf16/fp16
+outputs within 1e-2 relative (|got - exact| <= 1e-2 |exact| + 1e-6) - in
+practice one rounding of the fp32 result, <= 2^-9 relative. Sums: the
+reference's |got - exact| <= max(|exact|, 1) * 1e-5 * sqrt(N)
+(tests/cuda/test_reduction.cu:18-20), exact for integer-valued inputs.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import gpu_util as g
+from tests.conftest import load_golden, rng
+
+pytestmark = pytest.mark.gpu
+
+RTOL = {"f32": 1e-5, "bf16": 1e-2, "f16": 1e-2}
+ATOL = {"f32": 1e-7, "bf16": 1e-6, "f16": 1e-6}
+
+
+def assert_close(got_stored: np.ndarray, exact: np.ndarray, dtype: str, what: str) -> None:
+    got = g.host_values(got_stored, dtype).astype(np.float64)
+    err = np.abs(got - exact)
+    bound = RTOL[dtype] * np.abs(exact) + ATOL[dtype]
+    bad = np.flatnonzero((err > bound).reshape(-1))
+    assert bad.size == 0, (
+        f"{what}: {bad.size} elements out of tolerance; worst rel "
+        f"{np.max(err / (np.abs(exact) + 1e-30)):.3e} at {bad[:5]}"
+    )
+
+
+def run_rmsnorm(x: np.ndarray, w: np.ndarray, dtype: str, eps: float, offset: int = 0) -> np.ndarray:
+    rows, cols = x.shape
+    flat = np.concatenate([np.zeros(offset, x.dtype), x.reshape(-1)])
+    xg = g.to_gpu(flat, dtype)
+    wg = g.to_gpu(w, dtype)
+    yg = torch.empty_like(xg)
+    es = xg.element_size()
+    g.call("cf_rmsnorm", xg.data_ptr() + offset * es, wg.data_ptr(), yg.data_ptr() + offset * es,
+           g.cf(dtype), rows, cols, eps, g.stream())
+    torch.cuda.synchronize()
+    return g.to_host(yg)[offset:].reshape(rows, cols)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize(
+    "shape", [(1, 1), (1, 64), (3, 17), (8, 128), (33, 1023), (16, 4096), (3, 2049), (4, 16384), (2, 40000)]
+)
+def test_rmsnorm_matches_the_oracle(dtype, shape):
+    rows, cols = shape
+    r = rng(rows * 131 + cols)
+    x = g.storage_bits(r.standard_normal((rows, cols)).astype(np.float32), dtype)
+    w = g.storage_bits((1 + 0.1 * r.standard_normal(cols)).astype(np.float32), dtype)
+    y = run_rmsnorm(x, w, dtype, 1e-6)
+    exact = oracle.rmsnorm(g.host_values(x, dtype), g.host_values(w, dtype), 1e-6)
+    assert_close(y, exact, dtype, f"rmsnorm {dtype} {shape}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_rmsnorm_misaligned_rows_take_the_fallback(dtype):
+    r = rng(3)
+    x = g.storage_bits(r.standard_normal((5, 256)).astype(np.float32), dtype)
+    w = g.storage_bits(r.standard_normal(256).astype(np.float32), dtype)
+    y = run_rmsnorm(x, w, dtype, 1e-6, offset=1)
+    exact = oracle.rmsnorm(g.host_values(x, dtype), g.host_values(w, dtype), 1e-6)
+    assert_close(y, exact, dtype, "rmsnorm misaligned")
+
+
+def test_rmsnorm_golden_cases():
+    for case, d in load_golden("rmsnorm.npz").items():
+        dtype = "bf16" if case.startswith("bf16") else "f32"
+        y = run_rmsnorm(d["x"], d["w"], dtype, 1e-6)
+        exact = oracle.rmsnorm(g.host_values(d["x"], dtype), g.host_values(d["w"], dtype), 1e-6)
+        assert_close(y, exact, dtype, case)
+
+
+def test_rmsnorm_unit_input_returns_the_weight_and_is_scale_invariant():
+    x = np.ones((4, 256), np.float32)
+    w = np.ones(256, np.float32)
+    np.testing.assert_allclose(run_rmsnorm(x, w, "f32", 0.0), 1.0, rtol=1e-6)
+    z = rng(4).standard_normal((4, 512)).astype(np.float32)
+    a = run_rmsnorm(z, np.ones(512, np.float32), "f32", 1e-12)
+    b = run_rmsnorm(z * 10, np.ones(512, np.float32), "f32", 1e-12)
+    np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
+
+
+def test_config2_rmsnorm_full_size():
+    g.announce("config 2: rmsnorm bf16 [16384, 4096]")
+    r = rng(2002)
+    x = oracle.f32_to_bf16_bits(r.standard_normal((16384, 4096), dtype=np.float32))
+    w = oracle.f32_to_bf16_bits((1 + 0.02 * r.standard_normal(4096)).astype(np.float32))
+    y = run_rmsnorm(x, w, "bf16", 1e-6)
+    rows = rng(2003).choice(16384, size=512, replace=False)
+    exact = oracle.rmsnorm(g.host_values(x[rows], "bf16"), g.host_values(w, "bf16"), 1e-6)
+    assert_close(y[rows], exact, "bf16", "config 2 rmsnorm (512 sampled rows)")
+    # Every row: the output's RMS is the weight's RMS to bf16 precision.
+    yv = g.host_values(y, "bf16").astype(np.float64) / g.host_values(w, "bf16")
+    rms = np.sqrt(np.mean(yv * yv, axis=1))
+    assert np.all(np.abs(rms - 1.0) < 1e-2)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(4, 17), (8, 512), (33, 4096)])
+def test_fused_residual_rmsnorm(dtype, shape):
+    r = rng(shape[0] + shape[1])
+    x = g.storage_bits(r.standard_normal(shape).astype(np.float32), dtype)
+    res = g.storage_bits(r.standard_normal(shape).astype(np.float32), dtype)
+    w = g.storage_bits(r.standard_normal(shape[1]).astype(np.float32), dtype)
+    xg, rg, wg = g.to_gpu(x, dtype), g.to_gpu(res, dtype), g.to_gpu(w, dtype)
+    yg, sg = torch.empty_like(xg), torch.empty_like(xg)
+    g.call("cf_fused_residual_rmsnorm", xg.data_ptr(), rg.data_ptr(), wg.data_ptr(), yg.data_ptr(),
+           sg.data_ptr(), g.cf(dtype), shape[0], shape[1], 1e-6, g.stream())
+    torch.cuda.synchronize()
+    summed = g.storage_bits(g.host_values(x, dtype) + g.host_values(res, dtype), dtype)
+    got_sum = g.to_host(sg)
+    np.testing.assert_array_equal(got_sum.view(np.uint32) if dtype == "f32" else got_sum,
+                                  summed.view(np.uint32) if dtype == "f32" else summed)
+    exact = oracle.rmsnorm(g.host_values(summed, dtype), g.host_values(w, dtype), 1e-6)
+    assert_close(g.to_host(yg), exact, dtype, "fused residual rmsnorm")
+
+
+# ---------------------------------------------------------------------------
+# Softmax.
+# ---------------------------------------------------------------------------
+
+
+def run_softmax(x: np.ndarray, in_dtype: str, out_dtype: str, offset: int = 0) -> np.ndarray:
+    rows, cols = x.shape
+    flat = np.concatenate([np.zeros(offset, x.dtype), x.reshape(-1)])
+    xg = g.to_gpu(flat, in_dtype)
+    yg = g.empty(flat.size, g.torch_dtype(out_dtype))
+    g.call("cf_softmax", xg.data_ptr() + offset * xg.element_size(), g.cf(in_dtype),
+           yg.data_ptr() + offset * yg.element_size(), g.cf(out_dtype), rows, cols, g.stream())
+    torch.cuda.synchronize()
+    return g.to_host(yg)[offset:].reshape(rows, cols)
+
+
+def causal(rows: int, cols: int, seed: int) -> np.ndarray:
+    x = (rng(seed).standard_normal((rows, cols)) * 2.0).astype(np.float32)
+    col = np.arange(cols)[None, :]
+    row = (np.arange(rows) % cols)[:, None]
+    x[col > row] = -np.inf
+    return x
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", [(1, 1), (1, 32), (4, 17), (8, 256), (3, 1025), (64, 4096), (2, 32768)])
+def test_softmax_matches_the_oracle(dtype, shape):
+    x = g.storage_bits((rng(shape[0] * 31 + shape[1]).standard_normal(shape) * 2).astype(np.float32), dtype)
+    y = run_softmax(x, dtype, dtype)
+    assert_close(y, oracle.softmax(g.host_values(x, dtype)), dtype, f"softmax {dtype} {shape}")
+
+
+def test_softmax_golden_and_extreme_logits():
+    for case, d in load_golden("softmax.npz").items():
+        dtype = "bf16" if case.startswith("bf16") else "f32"
+        y = run_softmax(d["x"], dtype, dtype)
+        assert_close(y, oracle.softmax(g.host_values(d["x"], dtype)), dtype, case)
+    ext = load_golden("softmax.npz")["extreme"]["x"]
+    y = run_softmax(ext, "f32", "f32")
+    assert np.isfinite(y).all()
+    np.testing.assert_allclose(y[0], 0.25, rtol=1e-6)
+
+
+def test_softmax_bf16_logits_to_fp32_probabilities_and_misaligned():
+    x = oracle.f32_to_bf16_bits(causal(128, 512, 8))
+    y = run_softmax(x, "bf16", "f32")
+    assert_close(y, oracle.softmax(g.host_values(x, "bf16")), "f32", "bf16 -> f32 softmax")
+    z = rng(9).standard_normal((6, 128)).astype(np.float32)
+    assert_close(run_softmax(z, "f32", "f32", offset=1), oracle.softmax(z), "f32", "misaligned")
+
+
+def test_config2_softmax_full_size():
+    g.announce("config 2: causal softmax bf16 [1024, 2048]")
+    x = oracle.f32_to_bf16_bits(causal(1024, 2048, 2048))
+    y = run_softmax(x, "bf16", "bf16")
+    exact = oracle.softmax(g.host_values(x, "bf16"))
+    assert_close(y, exact, "bf16", "config 2 softmax")
+    masked = np.arange(2048)[None, :] > np.arange(1024)[:, None]
+    assert (g.host_values(y, "bf16")[masked] == 0).all()
+    np.testing.assert_allclose(g.host_values(y, "bf16").astype(np.float64).sum(axis=1), 1.0, atol=2e-2)
+
+
+def test_softmax_in_place():
+    x = rng(10).standard_normal((16, 1024)).astype(np.float32)
+    xg = g.to_gpu(x)
+    g.call("cf_softmax", xg.data_ptr(), g.cf("f32"), xg.data_ptr(), g.cf("f32"), 16, 1024, g.stream())
+    torch.cuda.synchronize()
+    assert_close(g.to_host(xg), oracle.softmax(x), "f32", "in place")
+
+
+# ---------------------------------------------------------------------------
+# Sums.
+# ---------------------------------------------------------------------------
+
+
+def run_sum(x: np.ndarray, dtype: str = "f32", accumulate_onto: float | None = None) -> float:
+    xg = g.to_gpu(x, dtype)
+    n = x.size
+    ws = g.empty(max(1, g.lib().cf_reduce_sum_workspace_bytes(n)), torch.uint8)
+    out = torch.full((1,), 0.0 if accumulate_onto is None else accumulate_onto, device=g.DEVICE)
+    g.call("cf_reduce_sum", xg.data_ptr(), g.cf(dtype), out.data_ptr(), n, ws.data_ptr(), ws.numel(),
+           0 if accumulate_onto is None else 1, g.stream())
+    torch.cuda.synchronize()
+    return float(out.item())
+
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 255, 256, 1000, 1 << 16, 1 << 20, (1 << 24) + 7])
+def test_sum_matches_the_exact_sum(n):
+    x = rng(n).standard_normal(n).astype(np.float32)
+    exact = oracle.sum_exact(x)
+    assert abs(run_sum(x) - exact) <= max(abs(exact), 1.0) * 1e-5 * math.sqrt(n)
+
+
+def test_sum_of_ones_is_exact_and_deterministic():
+    assert run_sum(np.ones(100_000, np.float32)) == 100_000.0
+    x = rng(11).standard_normal(3_000_001).astype(np.float32)
+    first = run_sum(x)
+    assert all(run_sum(x) == first for _ in range(3))
+
+
+def test_sum_accumulates_when_asked_and_handles_bf16():
+    x = np.ones(1000, np.float32)
+    assert run_sum(x, accumulate_onto=5.0) == 1005.0
+    xb = oracle.f32_to_bf16_bits(rng(12).standard_normal(50_000).astype(np.float32))
+    exact = oracle.sum_exact(g.host_values(xb, "bf16"))
+    assert abs(run_sum(xb, "bf16") - exact) <= max(abs(exact), 1.0) * 1e-5 * math.sqrt(50_000)
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (4, 17), (33, 1023), (128, 512), (3, 100_000)])
+def test_row_sums(shape):
+    x = rng(shape[0] * shape[1]).standard_normal(shape).astype(np.float32)
+    xg = g.to_gpu(x)
+    out = g.empty(shape[0], torch.float32)
+    g.call("cf_row_sum", xg.data_ptr(), g.cf("f32"), out.data_ptr(), shape[0], shape[1], g.stream())
+    torch.cuda.synchronize()
+    exact = x.astype(np.float64).sum(axis=1)
+    np.testing.assert_allclose(g.to_host(out), exact, rtol=1e-4, atol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# Activations.
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("n", [1, 64, 1023, 100_003])
+def test_activations(dtype, n):
+    r = rng(n)
+    x = g.storage_bits((r.standard_normal(n) * 4).astype(np.float32), dtype)
+    up = g.storage_bits(r.standard_normal(n).astype(np.float32), dtype)
+    xg, ug = g.to_gpu(x, dtype), g.to_gpu(up, dtype)
+    xv, uv = g.host_values(x, dtype), g.host_values(up, dtype)
+    for name, args, exact in (
+        ("cf_silu", (xg,), oracle.silu(xv)),
+        ("cf_gelu", (xg,), oracle.gelu_tanh(xv)),
+        ("cf_swiglu", (xg, ug), oracle.swiglu(xv, uv)),
+    ):
+        yg = torch.empty_like(xg)
+        g.call(name, *[a.data_ptr() for a in args], yg.data_ptr(), g.cf(dtype), n, g.stream())
+        torch.cuda.synchronize()
+        got = g.host_values(g.to_host(yg), dtype).astype(np.float64)
+        bound = (1e-5 if dtype == "f32" else 1e-2) * np.abs(exact) + (1e-6 if dtype == "f32" else 1e-3)
+        assert (np.abs(got - exact) <= bound).all(), name
