@@ -34,6 +34,7 @@ HIP_SOURCES = (
     "cf_reduce.hip",
     "cf_activations.hip",
     "cf_lora.hip",
+    "cf_lora_fused.hip",
 )
 
 HIP_LIBRARY = PACKAGE_DIR / "libcudaforge_hip.so"

@@ -263,6 +263,76 @@ __device__ __forceinline__ bool aligned16(const void* p) {
 }
 
 // ---------------------------------------------------------------------------
+// Device: streaming (nontemporal) loads and stores.
+//
+// Data that is touched exactly once goes through global_load/store with the
+// nontemporal hint, so it does not displace reused lines (weights, scales)
+// in L2 and the Infinity Cache. Measured on MI355X with one-shot grids: a
+// 256 MiB copy moves 5.97 TB/s with the hint on both sides against 5.54 TB/s
+// without it.
+// ---------------------------------------------------------------------------
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+    const u32x4_t v = __builtin_nontemporal_load(static_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void store_stream16(void* p, const uint4& v) {
+    const u32x4_t w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, static_cast<u32x4_t*>(p));
+}
+
+__device__ __forceinline__ uint2 load_stream8(const void* p) {
+    const u32x2_t v = __builtin_nontemporal_load(static_cast<const u32x2_t*>(p));
+    return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ void store_stream8(void* p, const uint2& v) {
+    const u32x2_t w = {v.x, v.y};
+    __builtin_nontemporal_store(w, static_cast<u32x2_t*>(p));
+}
+
+// ---------------------------------------------------------------------------
+// Device: buffer loads.
+//
+// A buffer resource (4 SGPRs: base, range in bytes, format word) lets a load
+// address memory with a 32-bit per-lane VGPR offset plus a uniform SGPR
+// offset, instead of a 64-bit VGPR address per load; loads whose lane offset
+// falls outside the range return zero without faulting. The GEMM kernels use
+// this to keep their prefetch addressing in a handful of registers.
+// ---------------------------------------------------------------------------
+
+/// Word 3 of a raw (untyped, unswizzled) buffer resource on gfx9-family parts.
+inline constexpr int kRawBufferFormat = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), kRawBufferFormat);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset,
+                                               uint32_t soffset) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint16_t buffer_load2(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset,
+                                                 uint32_t soffset) {
+    return __builtin_amdgcn_raw_buffer_load_b16(rsrc, voffset, soffset, 0);
+}
+
+__device__ __forceinline__ uint32_t load_stream4(const void* p) {
+    return __builtin_nontemporal_load(static_cast<const uint32_t*>(p));
+}
+
+__device__ __forceinline__ void store_stream4(void* p, uint32_t v) {
+    __builtin_nontemporal_store(v, static_cast<uint32_t*>(p));
+}
+
+// ---------------------------------------------------------------------------
 // Host: errors, launch checks, device facts.
 // ---------------------------------------------------------------------------
 

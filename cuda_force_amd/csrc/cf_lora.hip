@@ -5,30 +5,8 @@
 //   x [M, K]   w [K, N]   a [K, r]   b [r, N]   y [M, N]
 //   y = x @ w + scale * ((x @ a) @ b)
 //
-// Fast path (bf16, K % 64 == 0, N % 8 == 0, r <= 16, 16-byte aligned): one
-// fused kernel on the bf16 MFMA units.
-//   * 256x256 output tile per workgroup, 4 waves of 128x128, K-step 64,
-//     v_mfma_f32_32x32x16_bf16 with fp32 accumulators (256 per lane).
-//   * Operands are staged through LDS in a K-major layout with an XOR swizzle
-//     on 16-byte chunks (conflict-free fragment reads), double-buffered: the
-//     next K-tile's global loads are in flight while the current one feeds
-//     the MFMAs, one barrier per K-step.
-//   * w arrives N-major ([K, N] is what the reference's operator takes), so
-//     each thread loads an 8x8 bf16 block as eight 16-byte row segments and
-//     transposes it in registers with v_perm_b32 before the LDS store.
-//   * The adapter down-projection x @ a is accumulated in the same K-loop as
-//     16 extra output columns (v_mfma_f32_16x16x32_bf16 on the x tile already
-//     in LDS, about 6% more MFMA work), so x is read from HBM once.
-//   * Epilogue: x @ a is rounded to bf16 (as the reference's ATen path rounds
-//     the intermediate tensor), exchanged through LDS into MFMA A-operand
-//     layout, multiplied by b with one K=16 MFMA per 32x32 tile, scaled and
-//     added to the base accumulators, and the tile is stored as bf16. No
-//     second launch and no [M, r] round trip through HBM.
-//   * Workgroup ids are remapped so that the 64 tiles dispatched to one XCD
-//     (ids are dealt round-robin across the 8 XCDs) form a 4 x 16 band of
-//     output tiles sharing x row-panels in that XCD's L2.
-// The reference's fused kernel instead recomputes x @ a untiled in every
-// block (cuda/src/lora_linear.cu:138-203).
+// Fast path (bf16, K % 64 == 0, N % 8 == 0, r <= 16, 16-byte aligned): the
+// fused MFMA kernel in cf_lora_fused.hip, one launch.
 //
 // Generic path (fp32, or shapes the fast path does not take): x @ a into a
 // fp32 [M, r] workspace (one wave per row), then a 64x64-tiled fp32 FMA GEMM
@@ -41,13 +19,10 @@
 // The column reductions run in row chunks into an fp32 workspace and a second
 // kernel sums the chunks in a fixed order (deterministic).
 #include "cf_common.hpp"
+#include "cf_lora_fused.hpp"
 
 namespace cf {
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxRank = 64;
 
@@ -177,325 +152,6 @@ __global__ __launch_bounds__(kDefaultBlockSize) void tiled_gemm_kernel(
             Storage<T>::store(y + gm * N + gn, v);
         }
     }
-}
-
-// ---------------------------------------------------------------------------
-// Fast path: fused bf16 MFMA kernel.
-// ---------------------------------------------------------------------------
-
-constexpr int kBM = 256;
-constexpr int kBN = 256;
-constexpr int kBK = 64;
-constexpr int kLdsRow = kBK * 2;                    // bytes per K-major LDS row
-constexpr int kTileA = kBM * kLdsRow;               // 32 KiB
-constexpr int kTileB = kBN * kLdsRow;               // 32 KiB
-constexpr int kTileAdapter = 16 * kLdsRow;          // 2 KiB: a^T [16][64]
-constexpr int kStage = kTileA + kTileB + kTileAdapter;
-constexpr int kLdsBytes = 2 * kStage;               // 132 KiB
-constexpr int kFusedThreads = 256;
-
-/// Byte offset of 16-byte chunk `chunk` (0..7) of K-major row `row`. The XOR
-/// of both the low and the next three bits of the row spreads 8 consecutive
-/// rows (fragment reads) and rows 8 apart (transposed stores) over all banks.
-__device__ __forceinline__ int lds_offset(int row, int chunk) {
-    return row * kLdsRow + ((chunk ^ (row & 7) ^ ((row >> 3) & 7)) << 4);
-}
-
-/// Transpose an 8x8 block of bf16: in[r] holds row r (8 values, 2 per dword);
-/// out[j] receives column j (8 values).
-__device__ __forceinline__ void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const uint32_t lo_row[4] = {in[2 * e].x, in[2 * e].y, in[2 * e].z, in[2 * e].w};
-        const uint32_t hi_row[4] = {in[2 * e + 1].x, in[2 * e + 1].y, in[2 * e + 1].z,
-                                    in[2 * e + 1].w};
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const uint32_t even = __builtin_amdgcn_perm(hi_row[d], lo_row[d], 0x05040100u);
-            const uint32_t odd = __builtin_amdgcn_perm(hi_row[d], lo_row[d], 0x07060302u);
-            uint32_t* ce = reinterpret_cast<uint32_t*>(&out[2 * d]);
-            uint32_t* co = reinterpret_cast<uint32_t*>(&out[2 * d + 1]);
-            ce[e] = even;
-            co[e] = odd;
-        }
-    }
-}
-
-struct FusedArgs {
-    const uint16_t* x;
-    const uint16_t* w;
-    const uint16_t* a;
-    const uint16_t* b;
-    uint16_t* y;
-    float* xa_out;
-    int64_t M;
-    int64_t N;
-    int64_t K;
-    int64_t rank;
-    float scale;
-    int tiles_m;
-    int tiles_n;
-};
-
-/// Tile coordinates for workgroup `pid`: undo the round-robin XCD dealing so
-/// consecutive logical ids share an XCD, then walk 4-row bands of tiles.
-__device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
-    constexpr int kXcds = 8;
-    constexpr int kGroupM = 4;
-    const int total = tiles_m * tiles_n;
-    int logical = pid;
-    if (total % kXcds == 0) {
-        const int per_xcd = total / kXcds;
-        logical = (pid % kXcds) * per_xcd + pid / kXcds;
-    }
-    const int band = kGroupM * tiles_n;
-    const int group = logical / band;
-    const int first_m = group * kGroupM;
-    const int rows_in_group = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
-    const int in_group = logical % band;
-    tm = first_m + in_group % rows_in_group;
-    tn = in_group / rows_in_group;
-}
-
-__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void lora_fused_bf16_kernel(FusedArgs args) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
-
-    const int tid = static_cast<int>(threadIdx.x);
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1;
-    const int wn = wave & 1;
-    int tm;
-    int tn;
-    tile_of(static_cast<int>(blockIdx.x), args.tiles_m, args.tiles_n, tm, tn);
-    const int64_t m0 = static_cast<int64_t>(tm) * kBM;
-    const int64_t n0 = static_cast<int64_t>(tn) * kBN;
-    const int64_t M = args.M;
-    const int64_t N = args.N;
-    const int64_t K = args.K;
-    const int64_t rank = args.rank;
-
-    // Per-thread global load coordinates.
-    //   x tile [256 rows][8 chunks]: chunk id i*256 + tid -> row id>>3, chunk id&7.
-    //   w tile [64 k][256 n] as 8x8 blocks: k-block tid>>5, n-block tid&31.
-    //   a tile [64 k][16 j]: 4 elements per thread, k = tid>>2, j = (tid&3)*4 + e.
-    const int wkb = tid >> 5;
-    const int wnb = tid & 31;
-    const bool w_valid = (n0 + wnb * 8) < N;
-    const int ak = tid >> 2;
-    const int aj = (tid & 3) * 4;
-
-    uint4 xr[8];
-    uint4 wr[8];
-    uint16_t ar[4];
-
-    auto load_global = [&](int64_t k0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int id = i * kFusedThreads + tid;
-            const int64_t row = m0 + (id >> 3);
-            const int chunk = id & 7;
-            xr[i] = row < M ? *reinterpret_cast<const uint4*>(args.x + row * K + k0 + chunk * 8)
-                            : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int64_t k = k0 + wkb * 8 + r;
-            wr[r] = w_valid ? *reinterpret_cast<const uint4*>(args.w + k * N + n0 + wnb * 8)
-                            : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int64_t j = aj + e;
-            ar[e] = j < rank ? args.a[(k0 + ak) * rank + j] : static_cast<uint16_t>(0);
-        }
-    };
-
-    auto store_lds = [&](int stage) {
-        uint8_t* base = lds + stage * kStage;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int id = i * kFusedThreads + tid;
-            *reinterpret_cast<uint4*>(base + lds_offset(id >> 3, id & 7)) = xr[i];
-        }
-        uint4 cols[8];
-        transpose8x8(wr, cols);
-        uint8_t* bt = base + kTileA;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            *reinterpret_cast<uint4*>(bt + lds_offset(wnb * 8 + j, wkb)) = cols[j];
-        }
-        uint8_t* at = base + kTileA + kTileB;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int j = aj + e;
-            *reinterpret_cast<uint16_t*>(at + lds_offset(j, ak >> 3) + (ak & 7) * 2) = ar[e];
-        }
-    };
-
-    f32x16_t acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-        }
-    }
-    f32x4_t xacc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xacc[i][r] = 0.0f;
-    }
-
-    const int64_t k_tiles = K / kBK;
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-
-    for (int64_t kt = 0; kt < k_tiles; ++kt) {
-        const int stage = static_cast<int>(kt & 1);
-        if (kt + 1 < k_tiles) load_global((kt + 1) * kBK);
-
-        const uint8_t* ta = lds + stage * kStage;
-        const uint8_t* tb = ta + kTileA;
-        const uint8_t* tat = tb + kTileB;
-#pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const int chunk = kk * 2 + (lane >> 5);
-            bf16x8_t af[4];
-            bf16x8_t bfr[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                af[i] = *reinterpret_cast<const bf16x8_t*>(
-                    ta + lds_offset(wm * 128 + i * 32 + (lane & 31), chunk));
-                bfr[i] = *reinterpret_cast<const bf16x8_t*>(
-                    tb + lds_offset(wn * 128 + i * 32 + (lane & 31), chunk));
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[i][j] =
-                        __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-        // Adapter down-projection: this wave's 64 rows x 16 columns.
-#pragma unroll
-        for (int kk = 0; kk < kBK / 32; ++kk) {
-            const int chunk = kk * 4 + (lane >> 4);
-            const bf16x8_t bv =
-                *reinterpret_cast<const bf16x8_t*>(tat + lds_offset(lane & 15, chunk));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(
-                    ta + lds_offset(wave * 64 + i * 16 + (lane & 15), chunk));
-                xacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, xacc[i], 0, 0, 0);
-            }
-        }
-
-        if (kt + 1 < k_tiles) store_lds(stage ^ 1);
-        __syncthreads();
-    }
-
-    // ---- epilogue: adapter up-projection and store ----
-    // xa (bf16) exchange tile [256][16] in the (now idle) stage-0 buffer.
-    uint16_t* xa_lds = reinterpret_cast<uint16_t*>(lds);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = wave * 64 + i * 16 + 4 * (lane >> 4) + r;
-            const int col = lane & 15;
-            const float v = xacc[i][r];
-            xa_lds[row * 16 + col] = static_cast<uint16_t>(f32_to_bf16_bits(v));
-            if (args.xa_out != nullptr && tn == 0 && col < rank && m0 + row < M) {
-                args.xa_out[(m0 + row) * rank + col] = v;
-            }
-        }
-    }
-    __syncthreads();
-
-    bf16x8_t xa_frag[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = wm * 128 + i * 32 + (lane & 31);
-        xa_frag[i] = *reinterpret_cast<const bf16x8_t*>(xa_lds + row * 16 + (lane >> 5) * 8);
-    }
-    bf16x8_t b_frag[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int64_t col = n0 + wn * 128 + j * 32 + (lane & 31);
-        uint16_t vals[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int64_t q = (lane >> 5) * 8 + e;
-            vals[e] = (q < rank && col < N) ? args.b[q * N + col] : static_cast<uint16_t>(0);
-        }
-        b_frag[j] = __builtin_bit_cast(bf16x8_t, vals);
-    }
-    const float scale = args.scale;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f32x16_t t;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) t[r] = 0.0f;
-            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa_frag[i], b_frag[j], t, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] += scale * t[r];
-        }
-    }
-
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t col = n0 + wn * 128 + j * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < M && col < N) {
-                    args.y[row * N + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[i][j][r]));
-                }
-            }
-        }
-    }
-}
-
-bool fused_eligible(const void* x, const void* w, const void* a, const void* b, const void* y,
-                    int64_t M, int64_t N, int64_t K, int64_t rank) {
-    (void)a;
-    (void)b;
-    (void)y;
-    return K % kBK == 0 && K > 0 && N % 8 == 0 && rank <= 16 && host_aligned(x, 16) &&
-           host_aligned(w, 16) && ceil_div<int64_t>(M, kBM) * ceil_div<int64_t>(N, kBN) < (1LL << 31);
-}
-
-cf_status launch_fused(const void* x, const void* w, const void* a, const void* b, void* y,
-                       float* xa_out, int64_t M, int64_t N, int64_t K, int64_t rank, float scale,
-                       hipStream_t stream) {
-    FusedArgs args;
-    args.x = static_cast<const uint16_t*>(x);
-    args.w = static_cast<const uint16_t*>(w);
-    args.a = static_cast<const uint16_t*>(a);
-    args.b = static_cast<const uint16_t*>(b);
-    args.y = static_cast<uint16_t*>(y);
-    args.xa_out = xa_out;
-    args.M = M;
-    args.N = N;
-    args.K = K;
-    args.rank = rank;
-    args.scale = scale;
-    args.tiles_m = static_cast<int>(ceil_div<int64_t>(M, kBM));
-    args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
-    const int grid = args.tiles_m * args.tiles_n;
-    lora_fused_bf16_kernel<<<grid, kFusedThreads, 0, stream>>>(args);
-    return check_launch("launching the fused bf16 LoRA kernel", stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -654,8 +310,8 @@ cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void
                cf::dtype_name(dtype));
     auto s = static_cast<hipStream_t>(stream);
     if (dtype == CF_BF16 &&
-        cf::fused_eligible(x, w, a, b, y, batch, out_features, in_features, rank)) {
-        return cf::launch_fused(x, w, a, b, y, xa_out, batch, out_features, in_features, rank,
+        cf::lora_fused_eligible(x, w, batch, out_features, in_features, rank)) {
+        return cf::launch_lora_fused(x, w, a, b, y, xa_out, batch, out_features, in_features, rank,
                                 scale, s);
     }
     CF_REQUIRE(rank == 0 || xa_out != nullptr,
@@ -676,8 +332,8 @@ cf_status cf_matmul(const void* a, const void* b, void* c, cf_dtype dtype, int64
     CF_REQUIRE(dtype == CF_F32 || dtype == CF_BF16, "cf_matmul: dtype %s has no kernel",
                cf::dtype_name(dtype));
     auto s = static_cast<hipStream_t>(stream);
-    if (dtype == CF_BF16 && cf::fused_eligible(a, b, nullptr, nullptr, c, m, n, k, 0)) {
-        return cf::launch_fused(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);
+    if (dtype == CF_BF16 && cf::lora_fused_eligible(a, b, m, n, k, 0)) {
+        return cf::launch_lora_fused(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);
     }
     if (dtype == CF_F32) {
         return cf::launch_generic<float>(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);

@@ -33,7 +33,10 @@ __device__ __forceinline__ float inv_rms(float sum_squares, int64_t cols, float 
     return 1.0f / sqrtf(mean + eps);
 }
 
-template <typename T, int kVecs, bool kResidual>
+/// One wave per kRows consecutive rows, one-shot grid: every load of the
+/// wave's rows is issued before any arithmetic, rows and outputs stream with
+/// nontemporal hints, the weight (reused by every wave) goes through the cache.
+template <typename T, int kVecs, int kRows, bool kResidual>
 __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
     const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ w,
     T* __restrict__ y, T* __restrict__ residual_out, int64_t rows, int64_t cols, float eps) {
@@ -42,8 +45,20 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
     const int64_t vec_cols = cols / kPer;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
                          static_cast<int64_t>(threadIdx.x) / kWaveSize;
-    const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    const int64_t row0 = wave * kRows;
+    if (row0 >= rows) return;  // wave-uniform
 
+    uint4 xv[kRows][kVecs];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const int64_t row = row0 + r;
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
+            xv[r][j] = (row < rows && v < vec_cols) ? load_stream16(x + row * cols + v * kPer)
+                                                    : make_uint4(0, 0, 0, 0);
+        }
+    }
     uint4 wv[kVecs];
 #pragma unroll
     for (int j = 0; j < kVecs; ++j) {
@@ -51,59 +66,55 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
         wv[j] = v < vec_cols ? reinterpret_cast<const uint4*>(w)[v] : make_uint4(0, 0, 0, 0);
     }
 
-    for (int64_t row = wave; row < rows; row += waves) {
-        const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
-        uint4 xv[kVecs];
+    if constexpr (kResidual) {
 #pragma unroll
-        for (int j = 0; j < kVecs; ++j) {
-            const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
-            xv[j] = v < vec_cols ? xr[v] : make_uint4(0, 0, 0, 0);
-        }
-        if constexpr (kResidual) {
-            const uint4* rr = reinterpret_cast<const uint4*>(residual + row * cols);
-            uint4* ro = reinterpret_cast<uint4*>(residual_out + row * cols);
+        for (int r = 0; r < kRows; ++r) {
+            const int64_t row = row0 + r;
 #pragma unroll
             for (int j = 0; j < kVecs; ++j) {
                 const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
-                if (v < vec_cols) {
+                if (row < rows && v < vec_cols) {
                     float a[kPer];
                     float b[kPer];
-                    unpack16<T>(xv[j], a);
-                    unpack16<T>(rr[v], b);
+                    unpack16<T>(xv[r][j], a);
+                    unpack16<T>(load_stream16(residual + row * cols + v * kPer), b);
 #pragma unroll
                     for (int i = 0; i < kPer; ++i) a[i] = a[i] + b[i];
                     // The sum is rounded to the storage type before the norm,
                     // as `x + residual` is in the reference.
-                    xv[j] = pack16<T>(a);
-                    ro[v] = xv[j];
+                    xv[r][j] = pack16<T>(a);
+                    store_stream16(residual_out + row * cols + v * kPer, xv[r][j]);
                 }
             }
         }
+    }
 
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const int64_t row = row0 + r;
         float partial[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             float a[kPer];
-            unpack16<T>(xv[j], a);
+            unpack16<T>(xv[r][j], a);
 #pragma unroll
             for (int i = 0; i < kPer; ++i) partial[i & 3] += a[i] * a[i];
         }
-        const float total = wave_reduce_f32<AddF32>((partial[0] + partial[1]) +
-                                                    (partial[2] + partial[3]));
+        const float total =
+            wave_reduce_f32<AddF32>((partial[0] + partial[1]) + (partial[2] + partial[3]));
         const float scale = inv_rms(total, cols, eps);
-
-        uint4* yr = reinterpret_cast<uint4*>(y + row * cols);
+        if (row >= rows) continue;  // wave-uniform
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
             if (v < vec_cols) {
                 float a[kPer];
                 float g[kPer];
-                unpack16<T>(xv[j], a);
+                unpack16<T>(xv[r][j], a);
                 unpack16<T>(wv[j], g);
 #pragma unroll
                 for (int i = 0; i < kPer; ++i) a[i] = (a[i] * scale) * g[i];
-                yr[v] = pack16<T>(a);
+                store_stream16(y + row * cols + v * kPer, pack16<T>(a));
             }
         }
     }
@@ -137,15 +148,17 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_block_kernel(
     }
 }
 
+/// Rows per wave: enough 16-byte loads in flight per lane (up to 8) without
+/// exceeding 64 VGPRs of row data.
+constexpr int rows_per_wave(int vecs) { return vecs >= 16 ? 1 : (vecs >= 4 ? 2 : 8 / vecs); }
+
 template <typename T, int kVecs, bool kResidual>
 void launch_wave(const void* x, const void* residual, const void* w, void* y, void* residual_out,
                  int64_t rows, int64_t cols, float eps, hipStream_t stream) {
-    // Enough waves to keep every SIMD busy with several rows in flight, but
-    // not more than there are rows.
-    const int64_t max_waves = static_cast<int64_t>(cu_count()) * 16;
-    const int64_t waves = rows < max_waves ? rows : max_waves;
+    constexpr int kRows = rows_per_wave(kVecs);
+    const int64_t waves = ceil_div<int64_t>(rows, kRows);
     const int64_t grid = ceil_div<int64_t>(waves, kWavesPerBlock);
-    rmsnorm_wave_kernel<T, kVecs, kResidual>
+    rmsnorm_wave_kernel<T, kVecs, kRows, kResidual>
         <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
             static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
             static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);

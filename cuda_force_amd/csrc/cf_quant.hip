@@ -68,8 +68,7 @@ __device__ __forceinline__ void load_lane(const T* __restrict__ x, int64_t e, in
                                           float* v) {
     constexpr int kPer = Storage<T>::kPerVec;
     if (kVec && e + kPer <= count) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(x + e);
-        unpack16<T>(raw, v);
+        unpack16<T>(load_stream16(x + e), v);
     } else {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) v[i] = (e + i < count) ? Storage<T>::load(x + e + i) : 0.0f;
@@ -120,7 +119,7 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
         for (int i = 0; i < kPer; ++i) codes[i] = quant_code(v[u][i], b);
 
         if constexpr (kMode == 0) {
-            if (part == 0) scales[block] = b.s;
+            if (part == 0) __builtin_nontemporal_store(b.s, scales + block);
             if (kVec && e + kPer <= count) {
                 uint32_t w[kPer / 4];
 #pragma unroll
@@ -131,9 +130,9 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
                            ((static_cast<uint32_t>(codes[4 * j + 3]) & 0xFFu) << 24);
                 }
                 if constexpr (kPer == 4) {
-                    *reinterpret_cast<uint32_t*>(q + e) = w[0];
+                    store_stream4(q + e, w[0]);
                 } else {
-                    *reinterpret_cast<uint2*>(q + e) = make_uint2(w[0], w[1]);
+                    store_stream8(q + e, make_uint2(w[0], w[1]));
                 }
             } else {
 #pragma unroll
@@ -146,7 +145,7 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
 #pragma unroll
             for (int i = 0; i < kPer; ++i) out[i] = static_cast<float>(codes[i]) * b.s;
             if (kVec && e + kPer <= count) {
-                *reinterpret_cast<uint4*>(y + e) = pack16<T>(out);
+                store_stream16(y + e, pack16<T>(out));
             } else {
 #pragma unroll
                 for (int i = 0; i < kPer; ++i) {
@@ -194,11 +193,11 @@ __global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
         scale[u] = e < count ? scales[e / kQuantBlockSize] : 0.0f;
         if (kVec && e + kPer <= count) {
             if constexpr (kPer == 4) {
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(q + e);
+                const uint32_t w = load_stream4(q + e);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) codes[u][i] = static_cast<int8_t>((w >> (8 * i)) & 0xFFu);
             } else {
-                const uint2 w = *reinterpret_cast<const uint2*>(q + e);
+                const uint2 w = load_stream8(q + e);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     codes[u][i] = static_cast<int8_t>((w.x >> (8 * i)) & 0xFFu);
@@ -219,7 +218,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
 #pragma unroll
         for (int i = 0; i < kPer; ++i) out[i] = static_cast<float>(codes[u][i]) * scale[u];
         if (kVec && e + kPer <= count) {
-            *reinterpret_cast<uint4*>(y + e) = pack16<Tout>(out);
+            store_stream16(y + e, pack16<Tout>(out));
         } else {
 #pragma unroll
             for (int i = 0; i < kPer; ++i) {

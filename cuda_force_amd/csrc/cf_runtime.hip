@@ -76,20 +76,25 @@ int cu_count() {
 
 namespace {
 
-/// Streaming copy: each lane moves 16-byte vectors, four in flight.
+constexpr int kCopyUnroll = 4;
+
+/// Streaming copy: every workgroup moves one contiguous chunk of
+/// 256 x 4 16-byte vectors with nontemporal loads and stores (a one-shot grid
+/// measured faster than a grid-stride loop on MI355X).
 __global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ src,
                                                      uint4* __restrict__ dst, int64_t vectors) {
-    constexpr int kUnroll = 4;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    for (; i + (kUnroll - 1) * stride < vectors; i += kUnroll * stride) {
-        uint4 v[kUnroll];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x * kCopyUnroll + threadIdx.x;
+    uint4 v[kCopyUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) v[u] = src[i + u * stride];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) dst[i + u * stride] = v[u];
+    for (int u = 0; u < kCopyUnroll; ++u) {
+        const int64_t i = base + static_cast<int64_t>(u) * blockDim.x;
+        if (i < vectors) v[u] = load_stream16(src + i);
     }
-    for (; i < vectors; i += stride) dst[i] = src[i];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+        const int64_t i = base + static_cast<int64_t>(u) * blockDim.x;
+        if (i < vectors) store_stream16(dst + i, v[u]);
+    }
 }
 
 __global__ void copy_tail_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
@@ -133,10 +138,11 @@ cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream)
     const bool vec = cf::host_aligned(src, 16) && cf::host_aligned(dst, 16);
     const int64_t vectors = vec ? bytes / 16 : 0;
     if (vectors > 0) {
-        const int64_t wanted = cf::ceil_div<int64_t>(vectors, 256 * 4);
-        const int grid = static_cast<int>(wanted < 65536 ? wanted : 65536);
-        cf::copy16_kernel<<<grid, 256, 0, s>>>(static_cast<const uint4*>(src),
-                                               static_cast<uint4*>(dst), vectors);
+        const int64_t grid = cf::ceil_div<int64_t>(vectors, 256 * cf::kCopyUnroll);
+        CF_REQUIRE(grid < (1LL << 31), "cf_copy_bytes: %lld bytes exceed the launch limit",
+                   static_cast<long long>(bytes));
+        cf::copy16_kernel<<<static_cast<unsigned>(grid), 256, 0, s>>>(
+            static_cast<const uint4*>(src), static_cast<uint4*>(dst), vectors);
     }
     const int64_t done = vectors * 16;
     const int64_t rest = bytes - done;

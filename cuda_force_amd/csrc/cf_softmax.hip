@@ -24,26 +24,28 @@ namespace {
 
 constexpr int kWavesPerBlock = kDefaultBlockSize / kWaveSize;
 
-/// Store `n` (4 or 8) floats as Tout at `p` with 16- or 8-byte stores.
+/// Store `n` (4 or 8) floats as Tout at `p` with 16- or 8-byte streaming stores.
 template <typename Tout, int kN>
 __device__ __forceinline__ void store_vec(Tout* p, const float* v) {
     constexpr int kOutPer = Storage<Tout>::kPerVec;
     if constexpr (kN == kOutPer) {
-        *reinterpret_cast<uint4*>(p) = pack16<Tout>(v);
+        store_stream16(p, pack16<Tout>(v));
     } else if constexpr (kN == 2 * kOutPer) {
-        reinterpret_cast<uint4*>(p)[0] = pack16<Tout>(v);
-        reinterpret_cast<uint4*>(p)[1] = pack16<Tout>(v + kOutPer);
+        store_stream16(p, pack16<Tout>(v));
+        store_stream16(p + kOutPer, pack16<Tout>(v + kOutPer));
     } else {
         // 4 values into a 16-bit type: one 8-byte store.
         static_assert(kN == 4 && kOutPer == 8, "unsupported store width");
         uint2 w;
         w.x = Storage<Tout>::to_bits(v[0]) | (Storage<Tout>::to_bits(v[1]) << 16);
         w.y = Storage<Tout>::to_bits(v[2]) | (Storage<Tout>::to_bits(v[3]) << 16);
-        *reinterpret_cast<uint2*>(p) = w;
+        store_stream8(p, w);
     }
 }
 
-template <typename Tin, typename Tout, int kVecs>
+/// One wave per kRows consecutive rows, one-shot grid; all of the wave's
+/// loads are issued before the first reduction.
+template <typename Tin, typename Tout, int kVecs, int kRows>
 __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const Tin* x, Tout* y,
                                                                          int64_t rows,
                                                                          int64_t cols) {
@@ -52,17 +54,32 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
     const int64_t vec_cols = cols / kPer;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
                          static_cast<int64_t>(threadIdx.x) / kWaveSize;
-    const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    const int64_t row0 = wave * kRows;
+    if (row0 >= rows) return;  // wave-uniform
     const float neg_inf = -__builtin_inff();
 
-    for (int64_t row = wave; row < rows; row += waves) {
-        const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
+    uint4 raw[kRows][kVecs];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t idx = static_cast<int64_t>(j) * kWaveSize + lane;
+            if (row0 + r < rows && idx < vec_cols) {
+                raw[r][j] = load_stream16(x + (row0 + r) * cols + idx * kPer);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const int64_t row = row0 + r;
+        if (row >= rows) continue;  // wave-uniform
         float v[kVecs][kPer];
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             const int64_t idx = static_cast<int64_t>(j) * kWaveSize + lane;
             if (idx < vec_cols) {
-                unpack16<Tin>(xr[idx], v[j]);
+                unpack16<Tin>(raw[r][j], v[j]);
             } else {
 #pragma unroll
                 for (int i = 0; i < kPer; ++i) v[j][i] = neg_inf;
@@ -132,10 +149,20 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_block_kernel(const 
 
 template <typename Tin, typename Tout, int kVecs>
 void launch_wave(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t stream) {
-    const int64_t max_waves = static_cast<int64_t>(cu_count()) * 16;
-    const int64_t waves = rows < max_waves ? rows : max_waves;
+    // Rows per wave: up to 8 16-byte loads in flight per lane, but never so
+    // many rows per wave that fewer waves than SIMDs (4 per CU) would run.
+    constexpr int kRows = kVecs >= 8 ? 1 : 8 / kVecs;
+    const int64_t simds = static_cast<int64_t>(cu_count()) * 4;
+    const int64_t grid_rows = ceil_div<int64_t>(rows, kRows) >= simds ? kRows : 1;
+    const int64_t waves = ceil_div<int64_t>(rows, grid_rows);
     const int64_t grid = ceil_div<int64_t>(waves, kWavesPerBlock);
-    softmax_wave_kernel<Tin, Tout, kVecs>
+    if (grid_rows == 1) {
+        softmax_wave_kernel<Tin, Tout, kVecs, 1>
+            <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+                static_cast<const Tin*>(x), static_cast<Tout*>(y), rows, cols);
+        return;
+    }
+    softmax_wave_kernel<Tin, Tout, kVecs, kRows>
         <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
             static_cast<const Tin*>(x), static_cast<Tout*>(y), rows, cols);
 }
