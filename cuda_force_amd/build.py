@@ -37,6 +37,12 @@ HIP_SOURCES = (
     "cf_lora_fused.hip",
 )
 
+# Per-source additions. The fused LoRA kernel accumulates in VGPRs: the
+# compiler's AGPR accumulator allocation rotates registers every K-step.
+HIPCC_EXTRA_FLAGS = {
+    "cf_lora_fused.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+}
+
 HIP_LIBRARY = PACKAGE_DIR / "libcudaforge_hip.so"
 OFFLOAD_ARCH = "gfx950"
 
@@ -86,7 +92,8 @@ def build_hip_library(jobs: int = 8) -> Path:
 
     def compile_one(name: str) -> Path:
         obj = BUILD_DIR / (Path(name).stem + ".o")
-        _run([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / name), "-o", str(obj)])
+        extra = HIPCC_EXTRA_FLAGS.get(name, ())
+        _run([hipcc, *HIPCC_FLAGS, *extra, "-c", str(CSRC / name), "-o", str(obj)])
         return obj
 
     with ThreadPoolExecutor(max_workers=jobs) as pool:

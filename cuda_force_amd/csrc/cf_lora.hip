@@ -310,7 +310,7 @@ cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void
                cf::dtype_name(dtype));
     auto s = static_cast<hipStream_t>(stream);
     if (dtype == CF_BF16 &&
-        cf::lora_fused_eligible(x, w, batch, out_features, in_features, rank)) {
+        cf::lora_fused_eligible(x, w, a, b, batch, out_features, in_features, rank)) {
         return cf::launch_lora_fused(x, w, a, b, y, xa_out, batch, out_features, in_features, rank,
                                 scale, s);
     }
@@ -332,7 +332,7 @@ cf_status cf_matmul(const void* a, const void* b, void* c, cf_dtype dtype, int64
     CF_REQUIRE(dtype == CF_F32 || dtype == CF_BF16, "cf_matmul: dtype %s has no kernel",
                cf::dtype_name(dtype));
     auto s = static_cast<hipStream_t>(stream);
-    if (dtype == CF_BF16 && cf::lora_fused_eligible(a, b, m, n, k, 0)) {
+    if (dtype == CF_BF16 && cf::lora_fused_eligible(a, b, nullptr, nullptr, m, n, k, 0)) {
         return cf::launch_lora_fused(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);
     }
     if (dtype == CF_F32) {

@@ -3,33 +3,36 @@
 //   y[M, N] = x[M, K] @ w[K, N] + scale * bf16(x @ a)[M, r] @ b[r, N]
 //
 // operator layout of the reference (cuda/include/cudaforge/lora_linear.cuh:26-31),
-// r <= 16, bf16 operands, fp32 accumulation, bf16 output.
+// even r <= 16, bf16 operands, fp32 accumulation, bf16 output.
 //
 // Shape of the kernel:
-//   * 256x256 output tile per workgroup, K-step 64, 8 waves (2 per SIMD) each
-//     owning a 128x64 sub-tile: 4x2 v_mfma_f32_32x32x16_bf16 tiles, 128 fp32
-//     accumulators per lane. Two waves per SIMD let one wave's LDS reads,
-//     transposes and address work issue while the other's MFMAs execute.
-//   * Operands pass through LDS in a K-major layout: each row holds 64 k as
-//     eight 16-byte chunks, XOR-swizzled by the row's low and next three bits
-//     so that fragment reads (8 consecutive rows) and transposed stores (rows
-//     8 apart) both spread over the banks. Two stages: the next K-step's
-//     global loads are in flight in registers while the current stage feeds
-//     the MFMAs; one barrier per K-step.
-//   * Global loads are buffer loads (32-bit lane offsets, uniform K offset,
-//     hardware range check: x rows past M read as zero); nothing in the
-//     K-loop is predicated.
-//   * w is N-major, so each thread loads a 4(k) x 8(n) bf16 block as four
-//     16-byte row segments and transposes it in registers with v_perm_b32
-//     into four-k column pieces before its LDS store.
-//   * The adapter down-projection x @ a rides in the same K-loop on the x tile
-//     already in LDS (v_mfma_f32_16x16x32_bf16, 32 rows x 16 columns per wave,
-//     ~6% extra MFMA work); x is read from HBM once.
-//   * Epilogue: x @ a is rounded to bf16 (the reference materialises it as a
-//     bf16 tensor), exchanged through LDS into the A-operand layout and
-//     multiplied by bf16(scale * b) with one K=16 MFMA per 32x32 tile that
-//     accumulates straight into the base accumulators; then the tile is
-//     rounded to bf16 and stored. No second launch, no [M, r] HBM round trip.
+//   * 256x256 output tile per workgroup, 8 waves (two per SIMD), each owning a
+//     64x128 sub-tile held as 8x4 v_mfma_f32_16x16x32_bf16 accumulators (128
+//     fp32 per lane, accumulated in place in VGPRs; the file is compiled with
+//     -amdgpu-mfma-vgpr-form). The whole product is computed transposed,
+//     C^T = w^T x^T: w supplies the A operand, x the B operand, so each lane
+//     ends up holding 4 consecutive output columns of one row.
+//   * Operands travel HBM -> LDS by buffer loads with the LDS destination
+//     (`buffer_load_dwordx4 ... lds`): no registers are spent on prefetch,
+//     rows past M and columns past N arrive as zeros through the buffer range
+//     check. K-step 32, four LDS stages, prefetch distance three: the loads for
+//     step j + 3 are issued while step j + 1 is read into fragment registers
+//     and step j is multiplied.
+//   * x keeps its K-major layout in LDS (64-byte rows, 16-byte chunks XOR-
+//     swizzled by row bits 1-4 so 16 consecutive rows of one chunk hit
+//     distinct banks). w keeps its N-major layout (512-byte rows, chunks
+//     swizzled by k bits 0, 1 and 3) and is transposed on the way out of LDS
+//     by ds_read_b64_tr_b16, which hands each lane four k values of one
+//     column.
+//   * The adapter down-projection rides in the same loop: x^T fragments
+//     already in registers meet a^T fragments (also transposed out of LDS) in
+//     one extra MFMA per 16 rows; each wave covers 32 of its 64 rows, ~6%
+//     extra MFMA work, and x is read from HBM once.
+//   * Epilogue: x @ a (rounded to bf16, as the reference materialises it) is
+//     exchanged through LDS, bf16(scale * b) is read transposed from an LDS
+//     copy of b loaded at kernel start, and one v_mfma_f32_16x16x16_bf16 per
+//     16x16 block accumulates the adapter term into the base accumulators.
+//     The tile is rounded to bf16 and written with 8-byte stores.
 //   * Workgroup ids are remapped so the tiles dispatched to one XCD (ids are
 //     dealt round-robin over the 8 XCDs) form a band of 4 row-tiles sharing x
 //     row-panels in that XCD's L2.
@@ -37,44 +40,110 @@
 // (cuda/src/lora_linear.cu:138-203).
 #include "cf_lora_fused.hpp"
 
+#include <type_traits>
+
 namespace cf {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
 constexpr int kBM = 256;
 constexpr int kBN = 256;
-constexpr int kBK = 64;
+constexpr int kBK = 32;
+constexpr int kStages = 4;
 constexpr int kThreads = 512;
-constexpr int kLdsRow = kBK * 2;                    // bytes per K-major LDS row
-constexpr int kTileA = kBM * kLdsRow;               // 32 KiB
-constexpr int kTileB = kBN * kLdsRow;               // 32 KiB
-constexpr int kTileAdapter = 16 * kLdsRow;          // 2 KiB: a^T [16][64]
-constexpr int kStage = kTileA + kTileB + kTileAdapter;
-constexpr int kLdsBytes = 2 * kStage;               // 132 KiB
+constexpr int kMaxFusedRank = 16;
+constexpr int kTileX = kBM * kBK * 2;                    // 16 KiB: [256 m][32 k]
+constexpr int kTileW = kBK * kBN * 2;                    // 16 KiB: [32 k][256 n]
+constexpr int kTileA = kBK * kMaxFusedRank * 2;          // 1 KiB:  [32 k][16 j]
+constexpr int kStage = kTileX + kTileW + kTileA;
+constexpr int kTileB = kMaxFusedRank * kBN * 2;          // 8 KiB:  [16 j][256 n]
+constexpr int kXaBytes = (kBM / 16) * 64 * 8;            // 8 KiB: bf16 x @ a fragments
+constexpr int kOffB = kStages * kStage;
+constexpr int kOffXa = kOffB + kTileB;
+constexpr int kLdsBytes = kOffXa + kXaBytes;             // 148 KiB
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 workgroup");
 
-/// Byte offset of 16-byte chunk `chunk` (0..7) of K-major LDS row `row`.
-__device__ __forceinline__ int lds_offset(int row, int chunk) {
-    return row * kLdsRow + ((chunk ^ (row & 7) ^ ((row >> 3) & 7)) << 4);
+// A buffer offset past every range: the load returns zeros.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+/// s_waitcnt immediate that waits until at most n vector-memory operations
+/// of this wave are outstanding (lgkm and exp counters not waited on).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+/// Chunk swizzle of the x tile: row r, logical chunk c (8 k) lives in
+/// physical chunk c ^ x_swizzle(r) of the row's 64 bytes.
+__device__ __forceinline__ int x_swizzle(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+/// Chunk swizzle of the w and b tiles (512-byte rows of 32 chunks).
+__device__ __forceinline__ int w_swizzle(int row) { return 2 * (row & 3) + 8 * ((row >> 3) & 1); }
+
+__device__ __forceinline__ s16x4_t lds_read_tr(const uint8_t* base, int offset) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4_t*)((lds_u8_t*)(const_cast<uint8_t*>(base)) + offset));
 }
 
-/// Transpose a 4(k) x 8(n) block of bf16: in[r] holds k-row r (8 n values);
-/// out[j] receives the 4 k values of column j (low half first).
-__device__ __forceinline__ void transpose4x8(const uint4 (&in)[4], uint2 (&out)[8]) {
-    const uint32_t r0[4] = {in[0].x, in[0].y, in[0].z, in[0].w};
-    const uint32_t r1[4] = {in[1].x, in[1].y, in[1].z, in[1].w};
-    const uint32_t r2[4] = {in[2].x, in[2].y, in[2].z, in[2].w};
-    const uint32_t r3[4] = {in[3].x, in[3].y, in[3].z, in[3].w};
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        // Column 2d takes the low halves, column 2d + 1 the high halves.
-        out[2 * d].x = __builtin_amdgcn_perm(r1[d], r0[d], 0x05040100u);
-        out[2 * d].y = __builtin_amdgcn_perm(r3[d], r2[d], 0x05040100u);
-        out[2 * d + 1].x = __builtin_amdgcn_perm(r1[d], r0[d], 0x07060302u);
-        out[2 * d + 1].y = __builtin_amdgcn_perm(r3[d], r2[d], 0x07060302u);
-    }
+__device__ __forceinline__ bf16x8_t concat(s16x4_t lo, s16x4_t hi) {
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+/// Buffer resource words for a raw (stride 0) buffer of `bytes` bytes.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_t raw_buffer_words(const void* base, uint32_t bytes) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    return i32x4_t{static_cast<int>(addr & 0xffffffffu), static_cast<int>((addr >> 32) & 0xffffu),
+                   static_cast<int>(bytes), kRawBufferFormat};
+}
+
+/// HBM -> LDS copy of 16 (or 4) bytes per lane: lane l's bytes land at LDS
+/// byte lds_dst + 16 l (4 l), read from buffer offset voffset + soffset
+/// (zeros when out of range). Issued from inline assembly on purpose: the
+/// compiler conservatively drains every LDS DMA in flight (vmcnt(0)) before
+/// each transposed LDS read it emits, which would serialise the prefetch
+/// pipeline; DMA it does not know about cannot trigger that. The caller
+/// orders the copies itself (s_waitcnt vmcnt + barrier before the stage is
+/// read); compiler-generated vmcnt waits only become more conservative. M0
+/// (the LDS base register of the copy) is restored afterwards.
+__device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
+                                      uint32_t soffset) {
+    int saved_m0;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved_m0)
+        : "s"(lds_dst), "v"(voffset), "s"(rsrc), "s"(soffset)
+        : "memory");
+}
+
+__device__ __forceinline__ void dma4(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
+                                     uint32_t soffset) {
+    int saved_m0;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved_m0)
+        : "s"(lds_dst), "v"(voffset), "s"(rsrc), "s"(soffset)
+        : "memory");
+}
+
+/// Workgroup barrier that neither waits on memory counters nor lets the
+/// compiler move memory accesses across it; the caller has already waited
+/// for what the other waves must see.
+__device__ __forceinline__ void bare_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 /// Tile coordinates for workgroup `pid`: undo the round-robin XCD dealing so
@@ -113,15 +182,26 @@ struct FusedArgs {
     int tiles_n;
 };
 
+/// Operand fragments of one K-step: x (B operand) row block rb(i), k
+/// 8 (lane/16) .. +7 for lane%16's row; a (A operand of x @ a) column
+/// lane%16, same k.
+struct XFrags {
+    bf16x8_t x[4];
+    bf16x8_t a;
+};
+
+template <bool kAdapter>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lora_fused_bf16_kernel(FusedArgs args) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
 
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 2;  // 0..1: 128-row half of the tile
-    const int wn = wave & 3;   // 0..3: 64-column quarter of the tile
+    // Wave-uniform by construction; readfirstlane tells the compiler so that
+    // everything derived from it (LDS destinations of the DMA) stays scalar.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1;  // 0..3: 64-row quarter of the tile
+    const int wn = wave & 1;   // 0..1: 128-column half of the tile
     int tm;
     int tn;
     tile_of(static_cast<int>(blockIdx.x), args.tiles_m, args.tiles_n, tm, tn);
@@ -132,220 +212,273 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     const int64_t K = args.K;
     const int64_t rank = args.rank;
 
-    // ---- global load roles ----
-    // x tile [256 rows][8 chunks]: chunk id i*512 + tid, row id>>3, chunk id&7.
+    // ---- HBM -> LDS roles (each load instruction fills 1 KiB of LDS, lane l
+    // at byte 16 l; the global side is permuted to realise the swizzles) ----
+    // x: wave covers 16-row slabs q = 2 wave + i; lane -> row 16q + l/4,
+    // physical chunk l%4.
     const int64_t rows_here = M - m0 < kBM ? M - m0 : kBM;
-    const __amdgpu_buffer_rsrc_t xbuf =
-        make_buffer(args.x + m0 * K, static_cast<uint32_t>(rows_here * K * 2));
-    uint32_t xoff[4];
+    const i32x4_t xbuf = raw_buffer_words(args.x + m0 * K, static_cast<uint32_t>(rows_here * K * 2));
+    uint32_t x_dma[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int id = i * kThreads + tid;
-        xoff[i] = static_cast<uint32_t>(((id >> 3) * K + (id & 7) * 8) * 2);
+    for (int i = 0; i < 2; ++i) {
+        const int row = 16 * (wave * 2 + i) + (lane >> 2);
+        const int chunk = (lane & 3) ^ x_swizzle(row);
+        x_dma[i] = static_cast<uint32_t>((row * K + chunk * 8) * 2);
     }
-    // w tile [64 k][256 n] as 4x8 blocks: k-quad tid>>5 (0..15), n-block tid&31.
-    // A clamped column only feeds an output column >= N, which is never stored.
-    const int wkq = tid >> 5;
-    const int wnb = tid & 31;
-    const int64_t wcol = n0 + wnb * 8 < N ? n0 + wnb * 8 : N - 8;
-    const __amdgpu_buffer_rsrc_t wbuf = make_buffer(args.w, static_cast<uint32_t>(K * N * 2));
-    const uint32_t woff = static_cast<uint32_t>((static_cast<int64_t>(wkq) * 4 * N + wcol) * 2);
-    // a tile [64 k][16 j]: two elements per thread, k = tid>>3, j = (tid&7)*2 + e.
-    // The resource spans exactly a (empty for the rank-0 matmul, so every lane
-    // reads zero); columns past the rank are clamped onto the last one, which
-    // is harmless: they only meet rows of b past the rank, read as zero below.
-    const int ak = tid >> 3;
-    const int aj = (tid & 7) * 2;
-    const __amdgpu_buffer_rsrc_t abuf = make_buffer(args.a, static_cast<uint32_t>(K * rank * 2));
-    uint32_t aoff[2];
+    // w: wave covers k-row pairs q = 2 wave + i; lane -> row 2q + l/32,
+    // physical chunk l%32. Columns past N read as zero.
+    const i32x4_t wbuf = raw_buffer_words(args.w, static_cast<uint32_t>(K * N * 2));
+    uint32_t w_dma[2];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int64_t j = aj + e < rank ? aj + e : (rank > 0 ? rank - 1 : 0);
-        aoff[e] = static_cast<uint32_t>((ak * rank + j) * 2);
+    for (int i = 0; i < 2; ++i) {
+        const int row = 2 * (wave * 2 + i) + (lane >> 5);
+        const int64_t col = n0 + 8 * ((lane & 31) ^ w_swizzle(row));
+        w_dma[i] = col < N ? static_cast<uint32_t>((row * N + col) * 2) : kOutOfRange;
+    }
+    // a: 4-byte pieces (two adapter columns; the rank is even); waves 0..3
+    // cover rows 8 wave .. +7, lane -> row 8 wave + l/8, columns 2 (l%8), +1.
+    // Columns past the rank read as zero.
+    const i32x4_t abuf = raw_buffer_words(args.a, static_cast<uint32_t>(kAdapter ? K * rank * 2 : 0));
+    uint32_t a_dma = kOutOfRange;
+    if (kAdapter && wave < 4) {
+        const int row = 8 * wave + (lane >> 3);
+        const int col = 2 * (lane & 7);
+        a_dma = col < rank ? static_cast<uint32_t>((row * rank + col) * 2) : kOutOfRange;
     }
 
-    uint4 xr[4];
-    uint4 wr[4];
-    uint16_t ar[2];
-
-    auto load_global = [&](int64_t k0) {
-        const uint32_t xk = static_cast<uint32_t>(k0 * 2);
+    // LDS byte address of the tile storage (the DMA takes it in M0).
+    const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)lds));
+    auto issue_tile = [&](int64_t kt) {
+        const uint32_t stage = lds_addr + static_cast<uint32_t>(kt % kStages) * kStage;
+        const int64_t k0 = kt * kBK;
+        const uint32_t xs = static_cast<uint32_t>(k0 * 2);
+        const uint32_t ws = static_cast<uint32_t>(k0 * N * 2);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xr[i] = buffer_load16(xbuf, xoff[i], xk);
+        for (int i = 0; i < 2; ++i) dma16(xbuf, stage + (wave * 2 + i) * 1024, x_dma[i], xs);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            wr[r] = buffer_load16(wbuf, woff, static_cast<uint32_t>((k0 + r) * N * 2));
+        for (int i = 0; i < 2; ++i) {
+            dma16(wbuf, stage + kTileX + (wave * 2 + i) * 1024, w_dma[i], ws);
         }
-        const uint32_t ak0 = static_cast<uint32_t>(k0 * rank * 2);
-#pragma unroll
-        for (int e = 0; e < 2; ++e) ar[e] = buffer_load2(abuf, aoff[e], ak0);
+        if (kAdapter && wave < 4) {
+            dma4(abuf, stage + kTileX + kTileW + wave * 256, a_dma,
+                 static_cast<uint32_t>(k0 * rank * 2));
+        }
     };
+    // Loads per K-step of waves 4..7 (waves 0..3 issue one more; waiting for
+    // this count makes them wait for one extra load, which is harmless).
+    constexpr int kLoadsPerTile = 4;
 
-    auto store_lds = [&](int stage) {
-        uint8_t* base = lds + stage * kStage;
+    // ---- LDS -> register fragment roles ----
+    // x (B operand): fragment i holds row block rb(i) = (i + 2 wn) % 4 of the
+    // wave's 64 rows (row wm*64 + 16 rb + lane%16, logical chunk lane/16), so
+    // that the x @ a share of either wave is always fragments 0 and 1. The
+    // swizzle depends on row bits 1-4; bit 4 is rb's parity, which is i's.
+    // Fragments 0, 1 start at x_lo, 2, 3 at x_hi (rb = i + 2 wn or i - 2 wn).
+    int x_lo[2];
+    int x_hi[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int row = wm * 64 + 16 * p + (lane & 15);
+        const int base = row * (kBK * 2) + (((lane >> 4) ^ x_swizzle(row)) << 4);
+        x_lo[p] = base + wn * 2048;
+        x_hi[p] = base - wn * 2048 + 2048;
+    }
+    // w (A operand, transposed read): group g = lane/16 takes k rows 8g .. 8g+3
+    // (then +4); lane j of the group reads row 8g + j/4, columns 4(j%4) .. +3
+    // of the 16-column block; the read returns column j's four k values.
+    const int g = lane >> 4;
+    const int jl = lane & 15;
+    int w_rd[8];
+#pragma unroll
+    for (int jb = 0; jb < 8; ++jb) {
+        const int row = 8 * g + (jl >> 2);
+        const int chunk = 2 * (wn * 8 + jb) + ((jl & 3) >> 1);
+        w_rd[jb] = row * (kBN * 2) + ((chunk ^ w_swizzle(row)) << 4) + (jl & 1) * 8;
+    }
+    const int a_rd = (8 * g + (jl >> 2)) * (kMaxFusedRank * 2) + (jl & 3) * 8;
+
+    auto read_x = [&](XFrags& f, int64_t kt) {
+        const int stage = static_cast<int>(kt % kStages) * kStage;
+        const uint8_t* sx = lds + stage;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int id = i * kThreads + tid;
-            *reinterpret_cast<uint4*>(base + lds_offset(id >> 3, id & 7)) = xr[i];
+            f.x[i] = *reinterpret_cast<const bf16x8_t*>(sx + (i < 2 ? x_lo[i & 1] : x_hi[i & 1]));
         }
-        uint2 cols[8];
-        transpose4x8(wr, cols);
-        uint8_t* bt = base + kTileA;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            *reinterpret_cast<uint2*>(bt + lds_offset(wnb * 8 + j, wkq >> 1) + (wkq & 1) * 8) =
-                cols[j];
-        }
-        uint8_t* at = base + kTileA + kTileB;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            *reinterpret_cast<uint16_t*>(at + lds_offset(aj + e, ak >> 3) + (ak & 7) * 2) = ar[e];
+        if (kAdapter) {
+            const uint8_t* sa = sx + kTileX + kTileW;
+            f.a = concat(lds_read_tr(sa, a_rd), lds_read_tr(sa, a_rd + 4 * kMaxFusedRank * 2));
         }
     };
+    // w fragment jb (A operand): column wn*128 + 16 jb + lane%16, same k.
+    auto read_w = [&](int64_t kt, int jb) {
+        const uint8_t* sw = lds + static_cast<int>(kt % kStages) * kStage + kTileX;
+        return concat(lds_read_tr(sw, w_rd[jb]), lds_read_tr(sw, w_rd[jb] + 4 * kBN * 2));
+    };
 
-    f32x16_t acc[4][2];
+    f32x4_t acc[8][4];  // [w column block jb][x fragment i]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int jb = 0; jb < 8; ++jb) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-        }
+        for (int i = 0; i < 4; ++i) acc[jb][i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    f32x4_t xacc[2];
+    f32x4_t xacc[2];  // (x @ a)^T for row blocks 2 wn + t of this wave's 4
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xacc[t][r] = 0.0f;
-    }
+    for (int t = 0; t < 2; ++t) xacc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // One K-step of MFMAs from LDS stage `stage`.
-    auto compute = [&](int stage) {
-        const uint8_t* ta = lds + stage * kStage;
-        const uint8_t* tb = ta + kTileA;
-        const uint8_t* tat = tb + kTileB;
-#pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const int chunk = kk * 2 + (lane >> 5);
-            bf16x8_t af[4];
-            bf16x8_t bfr[2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                af[i] = *reinterpret_cast<const bf16x8_t*>(
-                    ta + lds_offset(wm * 128 + i * 32 + (lane & 31), chunk));
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                bfr[j] = *reinterpret_cast<const bf16x8_t*>(
-                    tb + lds_offset(wn * 64 + j * 32 + (lane & 31), chunk));
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    acc[i][j] =
-                        __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-        // Adapter down-projection: rows wave*32 .. wave*32+31, 16 columns.
-#pragma unroll
-        for (int kk = 0; kk < kBK / 32; ++kk) {
-            const int chunk = kk * 4 + (lane >> 4);
-            const bf16x8_t bv =
-                *reinterpret_cast<const bf16x8_t*>(tat + lds_offset(lane & 15, chunk));
+    // The w fragments live in one register set: fragment jb of the next
+    // K-step is read into it as soon as the 4 MFMAs of this step that use it
+    // have issued. x is double-buffered (its fragments are used until the
+    // end of the step).
+    bf16x8_t wf[8];
+    auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next) {
+        if (kAdapter) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(
-                    ta + lds_offset(wave * 32 + t * 16 + (lane & 15), chunk));
-                xacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, xacc[t], 0, 0, 0);
+                xacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a, f.x[t], xacc[t], 0, 0, 0);
             }
+        }
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[jb][i] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[jb], f.x[i], acc[jb][i], 0, 0, 0);
+            }
+            if constexpr (decltype(read_next)::value) wf[jb] = read_w(next_kt, jb);
         }
     };
 
-    const int64_t k_tiles = K / kBK;
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-    // Steady state: prefetch K-step kt + 1 into registers, compute step kt,
-    // park the prefetched step in the other stage. The last step is peeled so
-    // the loop body has a single path.
-    for (int64_t kt = 0; kt + 1 < k_tiles; ++kt) {
-        const int stage = static_cast<int>(kt & 1);
-        load_global((kt + 1) * kBK);
-        compute(stage);
-        store_lds(stage ^ 1);
-        __syncthreads();
+    // ---- prologue: b for the epilogue, then K-steps 0..2 in flight ----
+    if (kAdapter) {
+        const i32x4_t bbuf = raw_buffer_words(args.b, static_cast<uint32_t>(rank * N * 2));
+        const int row = 2 * wave + (lane >> 5);
+        const int64_t col = n0 + 8 * ((lane & 31) ^ w_swizzle(row));
+        const uint32_t off =
+            row < rank && col < N ? static_cast<uint32_t>((row * N + col) * 2) : kOutOfRange;
+        dma16(bbuf, lds_addr + kOffB + wave * 1024, off, 0);
     }
-    compute(static_cast<int>((k_tiles - 1) & 1));
-    __syncthreads();
+    const int64_t k_tiles = K / kBK;  // even, >= 2
+    issue_tile(0);
+    issue_tile(1);
+    if (k_tiles > 2) {
+        issue_tile(2);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kLoadsPerTile));
+    } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoadsPerTile));
+    }
+    bare_barrier();
+
+    XFrags f0;
+    XFrags f1;
+    read_x(f0, 0);
+#pragma unroll
+    for (int jb = 0; jb < 8; ++jb) wf[jb] = read_w(0, jb);
+
+    // Step kt: K-step kt + 1 must be in LDS (wait for this wave's loads,
+    // then the barrier for everyone's), the loads for kt + 3 reuse the stage
+    // of kt - 1 (read during step kt - 2, consumed in step kt - 1, so every
+    // wave is past it once it is at this barrier), step kt + 1 is read into
+    // registers while step kt is multiplied. The last four steps are peeled
+    // so the loop body has no branches.
+    using yes = std::true_type;
+    using no = std::false_type;
+    auto step = [&](int64_t kt, XFrags& cur, XFrags& nxt, auto issue, auto wait_all, auto read) {
+        if constexpr (decltype(read)::value) {
+            if constexpr (decltype(wait_all)::value) {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoadsPerTile));
+            }
+            bare_barrier();
+            if constexpr (decltype(issue)::value) issue_tile(kt + 3);
+            read_x(nxt, kt + 1);
+        }
+        multiply(cur, kt + 1, read);
+    };
+    int64_t kt = 0;
+    for (; kt + 4 < k_tiles; kt += 2) {
+        step(kt, f0, f1, yes{}, no{}, yes{});
+        step(kt + 1, f1, f0, yes{}, no{}, yes{});
+    }
+    if (k_tiles >= 4) {
+        step(kt, f0, f1, yes{}, no{}, yes{});
+        step(kt + 1, f1, f0, no{}, no{}, yes{});
+        kt += 2;
+    }
+    step(kt, f0, f1, no{}, yes{}, yes{});
+    step(kt + 1, f1, f0, no{}, no{}, no{});
 
     // ---- epilogue ----
-    // xa (bf16) exchange tile [256][16] in the idle stage-0 buffer.
-    uint16_t* xa_lds = reinterpret_cast<uint16_t*>(lds);
+    if (kAdapter) {
+        // x @ a: lane holds (x @ a)[row wm*64 + 16 (2 wn + t) + lane%16][4 g .. 4 g + 3].
+        uint2* xa_lds = reinterpret_cast<uint2*>(lds + kOffXa);
+        const bool write_xa = args.xa_out != nullptr && tn == 0;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < 2; ++t) {
+            const int rb = wm * 4 + wn * 2 + t;
+            uint2 packed;
+            packed.x = f32_to_bf16_bits(xacc[t][0]) | (f32_to_bf16_bits(xacc[t][1]) << 16);
+            packed.y = f32_to_bf16_bits(xacc[t][2]) | (f32_to_bf16_bits(xacc[t][3]) << 16);
+            xa_lds[rb * 64 + lane] = packed;
+            const int64_t row = m0 + rb * 16 + jl;
+            if (write_xa && row < M) {
+                float* dst = args.xa_out + row * rank;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = wave * 32 + t * 16 + 4 * (lane >> 4) + r;
-            const int col = lane & 15;
-            const float v = xacc[t][r];
-            xa_lds[row * 16 + col] = static_cast<uint16_t>(f32_to_bf16_bits(v));
-            if (args.xa_out != nullptr && tn == 0 && col < rank && m0 + row < M) {
-                args.xa_out[(m0 + row) * rank + col] = v;
+                for (int e = 0; e < 4; ++e) {
+                    if (4 * g + e < rank) dst[4 * g + e] = xacc[t][e];
+                }
+            }
+        }
+        __syncthreads();
+
+        // acc += bf16(scale * b)^T-block @ bf16(x @ a)^T-block, K = 16.
+        // b is read transposed: lane j of group g reads b row 4g + j/4,
+        // columns 4(j%4) .. +3 of the block and receives column j's four
+        // adapter rows 4g .. 4g + 3.
+        const float scale = args.scale;
+        s16x4_t xa_frag[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xa_frag[i] =
+                __builtin_bit_cast(s16x4_t, xa_lds[(wm * 4 + ((i + 2 * wn) & 3)) * 64 + lane]);
+        }
+        const uint8_t* tb = lds + kOffB;
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+            const int row = 4 * g + (jl >> 2);
+            const int chunk = 2 * (wn * 8 + jb) + ((jl & 3) >> 1);
+            const s16x4_t raw =
+                lds_read_tr(tb, row * (kBN * 2) + ((chunk ^ w_swizzle(row)) << 4) + (jl & 1) * 8);
+            s16x4_t bfrag;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float v = scale * bf16_bits_to_f32(static_cast<uint16_t>(raw[e]));
+                bfrag[e] = static_cast<short>(f32_to_bf16_bits(v));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[jb][i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bfrag, xa_frag[i], acc[jb][i],
+                                                                       0, 0, 0);
             }
         }
     }
-    __syncthreads();
 
-    // Up-projection: acc += xa_bf16 @ bf16(scale * b), one K=16 MFMA per 32x32
-    // tile straight into the base accumulators. Rounding scale * b to bf16 is
-    // exact for power-of-two scales (alpha / r = 2 in the usual configurations)
-    // and otherwise adds one bf16 rounding to the adapter term, which the
-    // reference already rounds to bf16 three times.
-    const float scale = args.scale;
-    bf16x8_t xa_frag[4];
+    // Store: acc[jb][i] lane holds y[row wm*64 + 16 rb(i) + lane%16]
+    // [columns wn*128 + 16 jb + 4 g .. +3]; N is a multiple of 8, so a
+    // four-column group is entirely inside or outside the matrix.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int row = wm * 128 + i * 32 + (lane & 31);
-        xa_frag[i] = *reinterpret_cast<const bf16x8_t*>(xa_lds + row * 16 + (lane >> 5) * 8);
-    }
-    // b through a resource spanning exactly [rank, N]: rows q >= rank read as
-    // zero (they meet the clamped adapter columns); a column past N reads
-    // some other element of b but only feeds an output column that is never
-    // stored.
-    const __amdgpu_buffer_rsrc_t bbuf = make_buffer(args.b, static_cast<uint32_t>(rank * N * 2));
+        const int64_t row = m0 + wm * 64 + 16 * ((i + 2 * wn) & 3) + jl;
+        if (row >= M) continue;
+        uint16_t* yrow = args.y + row * N;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
-        uint16_t vals[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int64_t q = (lane >> 5) * 8 + e;
-            const float bv =
-                bf16_bits_to_f32(buffer_load2(bbuf, static_cast<uint32_t>((q * N + col) * 2), 0));
-            vals[e] = static_cast<uint16_t>(f32_to_bf16_bits(scale * bv));
-        }
-        const bf16x8_t b_frag = __builtin_bit_cast(bf16x8_t, vals);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa_frag[i], b_frag, acc[i][j], 0, 0, 0);
-        }
-    }
-
-    // Store: accumulator (row 8*(r/4) + 4*(lane/32) + r%4, column lane%32)
-    // rounded to bf16.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < M && col < N) {
-                    args.y[row * N + col] = static_cast<uint16_t>(f32_to_bf16_bits(acc[i][j][r]));
-                }
+        for (int jb = 0; jb < 8; ++jb) {
+            const int64_t col = n0 + wn * 128 + 16 * jb + 4 * g;
+            if (col < N) {
+                uint2 packed;
+                packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
+                packed.y = f32_to_bf16_bits(acc[jb][i][2]) | (f32_to_bf16_bits(acc[jb][i][3]) << 16);
+                *reinterpret_cast<uint2*>(yrow + col) = packed;
             }
         }
     }
@@ -353,13 +486,15 @@ void lora_fused_bf16_kernel(FusedArgs args) {
 
 }  // namespace
 
-bool lora_fused_eligible(const void* x, const void* w, int64_t M, int64_t N, int64_t K,
-                         int64_t rank) {
-    // Buffer offsets are 32-bit: w must span < 4 GiB and a 256-row x tile too.
-    const bool offsets_fit = K * N * 2 < (1LL << 32) &&
-                             static_cast<int64_t>(kBM) * K * 2 < (1LL << 32) &&
-                             K * rank * 2 < (1LL << 32) && rank * N * 2 + N * 2 < (1LL << 32);
-    return K % kBK == 0 && K > 0 && N % 8 == 0 && rank <= 16 && host_aligned(x, 16) &&
+bool lora_fused_eligible(const void* x, const void* w, const void* a, const void* b, int64_t M,
+                         int64_t N, int64_t K, int64_t rank) {
+    // Buffer offsets are 32-bit: w must span < 4 GiB, a 256-row x tile too.
+    const bool offsets_fit = K * N * 2 < (1LL << 31) && static_cast<int64_t>(kBM) * K * 2 < (1LL << 31) &&
+                             K * rank * 2 < (1LL << 31) && rank * N * 2 < (1LL << 31);
+    const bool adapter_ok =
+        rank == 0 || (rank <= kMaxFusedRank && rank % 2 == 0 && host_aligned(a, 4) &&
+                      host_aligned(b, 16));
+    return K % (2 * kBK) == 0 && K > 0 && N % 8 == 0 && adapter_ok && host_aligned(x, 16) &&
            host_aligned(w, 16) && offsets_fit &&
            ceil_div<int64_t>(M, kBM) * ceil_div<int64_t>(N, kBN) < (1LL << 31);
 }
@@ -382,7 +517,11 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
     args.tiles_m = static_cast<int>(ceil_div<int64_t>(M, kBM));
     args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
     const int grid = args.tiles_m * args.tiles_n;
-    lora_fused_bf16_kernel<<<grid, kThreads, 0, stream>>>(args);
+    if (rank > 0) {
+        lora_fused_bf16_kernel<true><<<grid, kThreads, 0, stream>>>(args);
+    } else {
+        lora_fused_bf16_kernel<false><<<grid, kThreads, 0, stream>>>(args);
+    }
     return check_launch("launching the fused bf16 LoRA kernel", stream);
 }
 

@@ -7,10 +7,10 @@
 namespace cf {
 
 /// True when the fused kernel takes this bf16 problem: K a multiple of 64,
-/// N a multiple of 8, rank <= 16, 16-byte aligned x and w, 32-bit buffer
-/// offsets sufficient.
-bool lora_fused_eligible(const void* x, const void* w, int64_t M, int64_t N, int64_t K,
-                         int64_t rank);
+/// N a multiple of 8, rank 0 or even and <= 16, 16-byte aligned x, w and b,
+/// 4-byte aligned a, 31-bit buffer offsets sufficient.
+bool lora_fused_eligible(const void* x, const void* w, const void* a, const void* b, int64_t M,
+                         int64_t N, int64_t K, int64_t rank);
 
 /// y = x @ w + scale * bf16(x @ a) @ b in one launch (rank 0: y = x @ w);
 /// writes the fp32 x @ a to xa_out when it is non-null.
