@@ -18,12 +18,12 @@
 //     check. K-step 32, four LDS stages, prefetch distance three: the loads for
 //     step j + 3 are issued while step j + 1 is read into fragment registers
 //     and step j is multiplied.
-//   * x keeps its K-major layout in LDS (64-byte rows, 16-byte chunks XOR-
-//     swizzled by row bits 1-4 so 16 consecutive rows of one chunk hit
-//     distinct banks). w keeps its N-major layout (512-byte rows, chunks
-//     swizzled by k bits 0, 1 and 3) and is transposed on the way out of LDS
-//     by ds_read_b64_tr_b16, which hands each lane four k values of one
-//     column.
+//   * x keeps its K-major layout in LDS (64-byte rows, 16-byte chunks
+//     swizzled by row bit 2). w keeps its N-major layout
+//     (512-byte rows, chunks swizzled by k bits 0, 1 and 3) and is
+//     transposed on the way out of LDS by ds_read_b64_tr_b16, which hands
+//     each lane four k values of one column. All operand reads are free of
+//     bank conflicts.
 //   * The adapter down-projection rides in the same loop: x^T fragments
 //     already in registers meet a^T fragments (also transposed out of LDS) in
 //     one extra MFMA per 16 rows; each wave covers 32 of its 64 rows, ~6%
@@ -76,12 +76,32 @@ constexpr uint32_t kOutOfRange = 0x80000000u;
 /// of this wave are outstanding (lgkm and exp counters not waited on).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-/// Chunk swizzle of the x tile: row r, logical chunk c (8 k) lives in
-/// physical chunk c ^ x_swizzle(r) of the row's 64 bytes.
-__device__ __forceinline__ int x_swizzle(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
 
-/// Chunk swizzle of the w and b tiles (512-byte rows of 32 chunks).
+// LDS bank behaviour these layouts are built for (measured on gfx950 with
+// SQ_LDS_BANK_CONFLICT): a ds_read_b64_tr_b16 serves lanes 0-31 and 32-63
+// in separate cycles of 256 bytes, so the 16-lane groups 0 and 1 (2 and 3)
+// must hit different 128-byte halves of the banks. A ds_read_b128 serves
+// two 8-lane octets per cycle, octet o together with o ^ 3 or with 7 - o
+// (the measurements allow both); the x swizzle is conflict-free either way.
+
+/// Chunk swizzle of the x tile (64-byte rows of 4 chunks): row r keeps
+/// logical chunk c in physical chunk c ^ x_swizzle(r).
+__device__ __forceinline__ int x_swizzle(int row) { return ((row >> 2) & 1) << 1; }
+
+/// Chunk swizzle of the w tile (512-byte rows of 32 chunks): k rows 0-3 of
+/// a transposed read land in four different 32-byte bank groups, and rows
+/// 8 apart (the other 16-lane group of the same cycle) in the other half.
 __device__ __forceinline__ int w_swizzle(int row) { return 2 * (row & 3) + 8 * ((row >> 3) & 1); }
+
+/// Same for the b tile, whose transposed reads take rows 4 apart per group.
+__device__ __forceinline__ int b_swizzle(int row) { return 2 * (row & 3) + 8 * ((row >> 2) & 1); }
+
+/// Byte offset in the a tile ([32 k][16 j], 32-byte rows) of row `row`,
+/// byte `byte`: rows 8-15 and 24-31 swap 128-byte halves so the two
+/// 16-lane groups of a transposed read use different banks.
+__device__ __forceinline__ int a_offset(int row, int byte) {
+    return (row * 32 + byte) ^ (((row >> 3) & 1) << 7);
+}
 
 __device__ __forceinline__ s16x4_t lds_read_tr(const uint8_t* base, int offset) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -215,7 +235,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     // ---- HBM -> LDS roles (each load instruction fills 1 KiB of LDS, lane l
     // at byte 16 l; the global side is permuted to realise the swizzles) ----
     // x: wave covers 16-row slabs q = 2 wave + i; lane -> row 16q + l/4,
-    // physical chunk l%4.
+    // physical chunk l%4 (64 contiguous bytes of a row per 4 lanes).
     const int64_t rows_here = M - m0 < kBM ? M - m0 : kBM;
     const i32x4_t xbuf = raw_buffer_words(args.x + m0 * K, static_cast<uint32_t>(rows_here * K * 2));
     uint32_t x_dma[2];
@@ -235,54 +255,52 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         const int64_t col = n0 + 8 * ((lane & 31) ^ w_swizzle(row));
         w_dma[i] = col < N ? static_cast<uint32_t>((row * N + col) * 2) : kOutOfRange;
     }
-    // a: 4-byte pieces (two adapter columns; the rank is even); waves 0..3
-    // cover rows 8 wave .. +7, lane -> row 8 wave + l/8, columns 2 (l%8), +1.
-    // Columns past the rank read as zero.
+    // a: 4-byte pieces (two adapter columns; the rank is even); wave fills
+    // bytes 256 (wave % 4) + 4 l, i.e. rows 8 (wave % 4) .. +7 in the
+    // a_offset layout (an involution within the 256 bytes). Waves 4..7
+    // repeat waves 0..3 (the same bytes to the same place), which keeps the
+    // loop free of branches. Columns past the rank read as zero.
     const i32x4_t abuf = raw_buffer_words(args.a, static_cast<uint32_t>(kAdapter ? K * rank * 2 : 0));
     uint32_t a_dma = kOutOfRange;
-    if (kAdapter && wave < 4) {
-        const int row = 8 * wave + (lane >> 3);
-        const int col = 2 * (lane & 7);
+    if (kAdapter) {
+        const int phys = 256 * (wave & 3) + 4 * lane;
+        const int logical = phys ^ (((phys >> 8) & 1) << 7);  // rows 8-15, 24-31: bit 3 of row
+        const int row = logical >> 5;
+        const int col = (logical & 31) >> 1;
         a_dma = col < rank ? static_cast<uint32_t>((row * rank + col) * 2) : kOutOfRange;
     }
 
     // LDS byte address of the tile storage (the DMA takes it in M0).
     const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)lds));
-    auto issue_tile = [&](int64_t kt) {
+    // One DMA instruction of K-step kt: pieces 0, 1 are x, 2, 3 are w, 4 is
+    // a (adapter only). The K-loop spreads them over a step's MFMAs rather
+    // than issuing them in one burst after the barrier.
+    auto issue_piece = [&](int64_t kt, int piece) {
         const uint32_t stage = lds_addr + static_cast<uint32_t>(kt % kStages) * kStage;
         const int64_t k0 = kt * kBK;
-        const uint32_t xs = static_cast<uint32_t>(k0 * 2);
-        const uint32_t ws = static_cast<uint32_t>(k0 * N * 2);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) dma16(xbuf, stage + (wave * 2 + i) * 1024, x_dma[i], xs);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            dma16(wbuf, stage + kTileX + (wave * 2 + i) * 1024, w_dma[i], ws);
-        }
-        if (kAdapter && wave < 4) {
-            dma4(abuf, stage + kTileX + kTileW + wave * 256, a_dma,
+        if (piece < 2) {
+            dma16(xbuf, stage + (wave * 2 + piece) * 1024, x_dma[piece],
+                  static_cast<uint32_t>(k0 * 2));
+        } else if (piece < 4) {
+            dma16(wbuf, stage + kTileX + (wave * 2 + piece - 2) * 1024, w_dma[piece - 2],
+                  static_cast<uint32_t>(k0 * N * 2));
+        } else if (kAdapter) {
+            dma4(abuf, stage + kTileX + kTileW + (wave & 3) * 256, a_dma,
                  static_cast<uint32_t>(k0 * rank * 2));
         }
     };
-    // Loads per K-step of waves 4..7 (waves 0..3 issue one more; waiting for
-    // this count makes them wait for one extra load, which is harmless).
-    constexpr int kLoadsPerTile = 4;
+    auto issue_tile = [&](int64_t kt) {
+#pragma unroll
+        for (int piece = 0; piece < 5; ++piece) issue_piece(kt, piece);
+    };
+    constexpr int kLoadsPerTile = kAdapter ? 5 : 4;  // DMA instructions per K-step per wave
 
     // ---- LDS -> register fragment roles ----
     // x (B operand): fragment i holds row block rb(i) = (i + 2 wn) % 4 of the
-    // wave's 64 rows (row wm*64 + 16 rb + lane%16, logical chunk lane/16), so
-    // that the x @ a share of either wave is always fragments 0 and 1. The
-    // swizzle depends on row bits 1-4; bit 4 is rb's parity, which is i's.
-    // Fragments 0, 1 start at x_lo, 2, 3 at x_hi (rb = i + 2 wn or i - 2 wn).
-    int x_lo[2];
-    int x_hi[2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int row = wm * 64 + 16 * p + (lane & 15);
-        const int base = row * (kBK * 2) + (((lane >> 4) ^ x_swizzle(row)) << 4);
-        x_lo[p] = base + wn * 2048;
-        x_hi[p] = base - wn * 2048 + 2048;
-    }
+    // wave's 64 rows (row wm*64 + 16 rb + lane%16, chunk lane/16), so that
+    // the x @ a share of either wave is always fragments 0 and 1. The
+    // swizzle only depends on row bit 2, which is lane bit 2.
+    const int x_rd = (wm * 64 + (lane & 15)) * (kBK * 2) + (((lane >> 4) ^ x_swizzle(lane)) << 4);
     // w (A operand, transposed read): group g = lane/16 takes k rows 8g .. 8g+3
     // (then +4); lane j of the group reads row 8g + j/4, columns 4(j%4) .. +3
     // of the 16-column block; the read returns column j's four k values.
@@ -295,18 +313,20 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         const int chunk = 2 * (wn * 8 + jb) + ((jl & 3) >> 1);
         w_rd[jb] = row * (kBN * 2) + ((chunk ^ w_swizzle(row)) << 4) + (jl & 1) * 8;
     }
-    const int a_rd = (8 * g + (jl >> 2)) * (kMaxFusedRank * 2) + (jl & 3) * 8;
+    const int a_rd0 = a_offset(8 * g + (jl >> 2), (jl & 3) * 8);
+    const int a_rd1 = a_offset(8 * g + 4 + (jl >> 2), (jl & 3) * 8);
 
     auto read_x = [&](XFrags& f, int64_t kt) {
         const int stage = static_cast<int>(kt % kStages) * kStage;
         const uint8_t* sx = lds + stage;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            f.x[i] = *reinterpret_cast<const bf16x8_t*>(sx + (i < 2 ? x_lo[i & 1] : x_hi[i & 1]));
+            const int rb = (i + 2 * wn) & 3;
+            f.x[i] = *reinterpret_cast<const bf16x8_t*>(sx + x_rd + rb * 1024);
         }
         if (kAdapter) {
             const uint8_t* sa = sx + kTileX + kTileW;
-            f.a = concat(lds_read_tr(sa, a_rd), lds_read_tr(sa, a_rd + 4 * kMaxFusedRank * 2));
+            f.a = concat(lds_read_tr(sa, a_rd0), lds_read_tr(sa, a_rd1));
         }
     };
     // w fragment jb (A operand): column wn*128 + 16 jb + lane%16, same k.
@@ -330,7 +350,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     // have issued. x is double-buffered (its fragments are used until the
     // end of the step).
     bf16x8_t wf[8];
-    auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next) {
+    auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next, auto issue) {
         if (kAdapter) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
@@ -345,6 +365,9 @@ void lora_fused_bf16_kernel(FusedArgs args) {
                     __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[jb], f.x[i], acc[jb][i], 0, 0, 0);
             }
             if constexpr (decltype(read_next)::value) wf[jb] = read_w(next_kt, jb);
+            if constexpr (decltype(issue)::value) {
+                if (jb < 5) issue_piece(next_kt + 2, jb);
+            }
         }
     };
 
@@ -352,7 +375,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     if (kAdapter) {
         const i32x4_t bbuf = raw_buffer_words(args.b, static_cast<uint32_t>(rank * N * 2));
         const int row = 2 * wave + (lane >> 5);
-        const int64_t col = n0 + 8 * ((lane & 31) ^ w_swizzle(row));
+        const int64_t col = n0 + 8 * ((lane & 31) ^ b_swizzle(row));
         const uint32_t off =
             row < rank && col < N ? static_cast<uint32_t>((row * N + col) * 2) : kOutOfRange;
         dma16(bbuf, lds_addr + kOffB + wave * 1024, off, 0);
@@ -366,7 +389,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     } else {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoadsPerTile));
     }
-    bare_barrier();
+    bare_barrier();  // step 0 in LDS
 
     XFrags f0;
     XFrags f1;
@@ -390,10 +413,9 @@ void lora_fused_bf16_kernel(FusedArgs args) {
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoadsPerTile));
             }
             bare_barrier();
-            if constexpr (decltype(issue)::value) issue_tile(kt + 3);
             read_x(nxt, kt + 1);
         }
-        multiply(cur, kt + 1, read);
+        multiply(cur, kt + 1, read, issue);
     };
     int64_t kt = 0;
     for (; kt + 4 < k_tiles; kt += 2) {
@@ -448,7 +470,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
             const int row = 4 * g + (jl >> 2);
             const int chunk = 2 * (wn * 8 + jb) + ((jl & 3) >> 1);
             const s16x4_t raw =
-                lds_read_tr(tb, row * (kBN * 2) + ((chunk ^ w_swizzle(row)) << 4) + (jl & 1) * 8);
+                lds_read_tr(tb, row * (kBN * 2) + ((chunk ^ b_swizzle(row)) << 4) + (jl & 1) * 8);
             s16x4_t bfrag;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
