@@ -35,6 +35,7 @@ HIP_SOURCES = (
     "cf_activations.hip",
     "cf_lora.hip",
     "cf_lora_fused.hip",
+    "cf_lora_bwd.hip",
 )
 
 # Per-source additions. The fused LoRA kernel accumulates in VGPRs: the

@@ -13,12 +13,15 @@
 // whose epilogue adds scale * (xa @ b).
 //
 // Backward (adapter only, op layout):
-//   G      = dy @ b^T            [M, r]   one wave per row of dy
+//   G      = dy @ b^T            [M, r]
 //   grad_b = scale * xa^T @ dy   [r, N]   column reduction over M
 //   grad_a = scale * x^T @ G     [K, r]   column reduction over M
-// The column reductions run in row chunks into an fp32 workspace and a second
-// kernel sums the chunks in a fixed order (deterministic).
+// bf16 with rank <= 16 runs the MFMA kernels of cf_lora_bwd.hip. The generic
+// path here (fp32, other shapes): G one wave per row of dy, the column
+// reductions in row chunks into an fp32 workspace and a second kernel summing
+// the chunks in a fixed order (deterministic).
 #include "cf_common.hpp"
+#include "cf_lora_bwd.hpp"
 #include "cf_lora_fused.hpp"
 
 namespace cf {
@@ -348,7 +351,10 @@ size_t cf_lora_backward_workspace_bytes(int64_t batch, int64_t in_features, int6
     const int64_t widest = in_features > out_features ? in_features : out_features;
     const size_t g = static_cast<size_t>(batch * rank) * sizeof(float);
     const size_t part = static_cast<size_t>(chunks * rank * widest) * sizeof(float);
-    return ((g + 255) / 256) * 256 + part;
+    const size_t generic = ((g + 255) / 256) * 256 + part;
+    // Enough for either path: which one runs depends on dtype and alignment.
+    const size_t fast = cf::lora_backward_fast_workspace_bytes(batch, in_features, out_features);
+    return generic > fast ? generic : fast;
 }
 
 cf_status cf_lora_backward(const void* x, const void* dy, const void* b, const float* xa,
@@ -380,6 +386,11 @@ cf_status cf_lora_backward(const void* x, const void* dy, const void* b, const f
                needed);
     CF_REQUIRE(cf::host_aligned(workspace, 16), "cf_lora_backward: workspace must be 16-byte aligned");
     auto s = static_cast<hipStream_t>(stream);
+    if (dtype == CF_BF16 && cf::lora_backward_fast_eligible(x, dy, b, batch, in_features,
+                                                            out_features, rank)) {
+        return cf::launch_lora_backward_fast(x, dy, b, xa, grad_a, grad_b, batch, in_features,
+                                             out_features, rank, scale, workspace, s);
+    }
     float* g = static_cast<float*>(workspace);
     const size_t g_bytes = ((static_cast<size_t>(batch * rank) * sizeof(float) + 255) / 256) * 256;
     float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + g_bytes);

@@ -141,9 +141,14 @@ def test_config3_full_size():
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("shape", [(64, 96, 80, 4), (300, 256, 520, 16), (8192, 512, 384, 16), (1000, 130, 70, 24)])
+@pytest.mark.parametrize(
+    "shape",
+    [(64, 96, 80, 4), (130, 64, 96, 5), (300, 256, 520, 16), (8192, 512, 384, 16), (1000, 130, 70, 24),
+     (8192, 4096, 4096, 16)],
+)
 def test_adapter_backward(dtype, shape):
     m, k, n, r = shape
+    g.announce(f"adapter backward {dtype} {shape}")
     gen = rng(sum(shape) + 1)
     x = g.storage_bits(gen.standard_normal((m, k)).astype(np.float32), dtype)
     dy = g.storage_bits(gen.standard_normal((m, n)).astype(np.float32), dtype)
