@@ -12,8 +12,9 @@
 // 16-byte loads into registers (a 4096-wide bf16 row is 8 loads per lane),
 // the sum of squares reduces with DPP inside the wave (no LDS, no barrier),
 // and the row is scaled and stored from the same registers, so HBM sees one
-// read and one write per element. The weight vector is loaded once per wave
-// and reused for every row that wave processes. The reference instead uses a
+// read and one write per element. The weight vector is staged once per
+// workgroup in LDS (or, for ragged rows, read through the cache by each
+// wave). The reference instead uses a
 // block per row with a 32-lane shuffle tree and an LDS exchange, and re-reads
 // the row for the normalising pass (cuda/src/rmsnorm.cu:46-83).
 //
@@ -36,7 +37,13 @@ __device__ __forceinline__ float inv_rms(float sum_squares, int64_t cols, float 
 /// One wave per kRows consecutive rows, one-shot grid: every load of the
 /// wave's rows is issued before any arithmetic, rows and outputs stream with
 /// nontemporal hints, the weight (reused by every wave) goes through the cache.
-template <typename T, int kVecs, int kRows, bool kResidual>
+/// Loads are never conditional on data: a row past the end is loaded from
+/// the last row (and not stored), and with kFullCols (the row is exactly
+/// kVecs vectors per lane) no column is tested either; otherwise the
+/// missing columns are zero-filled after the load. With kFullCols the weight
+/// is staged once per workgroup in LDS instead of being re-read from L2 by
+/// every wave.
+template <typename T, int kVecs, int kRows, bool kResidual, bool kFullCols>
 __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
     const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ w,
     T* __restrict__ y, T* __restrict__ residual_out, int64_t rows, int64_t cols, float eps) {
@@ -46,24 +53,45 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
                          static_cast<int64_t>(threadIdx.x) / kWaveSize;
     const int64_t row0 = wave * kRows;
+    __shared__ uint4 w_lds[kFullCols ? kVecs * kWaveSize : 1];
+    if constexpr (kFullCols) {
+        for (int i = static_cast<int>(threadIdx.x); i < kVecs * kWaveSize; i += kDefaultBlockSize) {
+            w_lds[i] = reinterpret_cast<const uint4*>(w)[i];
+        }
+        __syncthreads();
+    }
     if (row0 >= rows) return;  // wave-uniform
 
     uint4 xv[kRows][kVecs];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-        const int64_t row = row0 + r;
+        const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
-            xv[r][j] = (row < rows && v < vec_cols) ? load_stream16(x + row * cols + v * kPer)
-                                                    : make_uint4(0, 0, 0, 0);
+            const int64_t vc = kFullCols || v < vec_cols ? v : vec_cols - 1;
+            xv[r][j] = load_stream16(x + row * cols + vc * kPer);
         }
     }
     uint4 wv[kVecs];
 #pragma unroll
     for (int j = 0; j < kVecs; ++j) {
         const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
-        wv[j] = v < vec_cols ? reinterpret_cast<const uint4*>(w)[v] : make_uint4(0, 0, 0, 0);
+        if constexpr (kFullCols) {
+            wv[j] = w_lds[v];
+        } else {
+            wv[j] = reinterpret_cast<const uint4*>(w)[v < vec_cols ? v : vec_cols - 1];
+        }
+    }
+    if constexpr (!kFullCols) {
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
+            if (v >= vec_cols) {
+#pragma unroll
+                for (int r = 0; r < kRows; ++r) xv[r][j] = make_uint4(0, 0, 0, 0);
+            }
+        }
     }
 
     if constexpr (kResidual) {
@@ -73,7 +101,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
 #pragma unroll
             for (int j = 0; j < kVecs; ++j) {
                 const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
-                if (row < rows && v < vec_cols) {
+                if (row < rows && (kFullCols || v < vec_cols)) {
                     float a[kPer];
                     float b[kPer];
                     unpack16<T>(xv[r][j], a);
@@ -107,7 +135,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             const int64_t v = static_cast<int64_t>(j) * kWaveSize + lane;
-            if (v < vec_cols) {
+            if (kFullCols || v < vec_cols) {
                 float a[kPer];
                 float g[kPer];
                 unpack16<T>(xv[r][j], a);
@@ -148,9 +176,11 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_block_kernel(
     }
 }
 
-/// Rows per wave: enough 16-byte loads in flight per lane (up to 8) without
-/// exceeding 64 VGPRs of row data.
-constexpr int rows_per_wave(int vecs) { return vecs >= 16 ? 1 : (vecs >= 4 ? 2 : 8 / vecs); }
+/// Rows per wave: at least 8 16-byte loads in flight per lane for short
+/// rows; one row per wave from 8 vectors per lane up, which keeps the VGPR
+/// count (and so the number of resident waves) highest - measured faster
+/// than two rows per wave on [16384, 4096] bf16.
+constexpr int rows_per_wave(int vecs) { return vecs >= 8 ? 1 : (vecs >= 4 ? 2 : 8 / vecs); }
 
 template <typename T, int kVecs, bool kResidual>
 void launch_wave(const void* x, const void* residual, const void* w, void* y, void* residual_out,
@@ -158,10 +188,18 @@ void launch_wave(const void* x, const void* residual, const void* w, void* y, vo
     constexpr int kRows = rows_per_wave(kVecs);
     const int64_t waves = ceil_div<int64_t>(rows, kRows);
     const int64_t grid = ceil_div<int64_t>(waves, kWavesPerBlock);
-    rmsnorm_wave_kernel<T, kVecs, kRows, kResidual>
-        <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
-            static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
+    const bool full_cols = cols / Storage<T>::kPerVec == static_cast<int64_t>(kVecs) * kWaveSize;
+    if (full_cols) {
+        rmsnorm_wave_kernel<T, kVecs, kRows, kResidual, true>
+            <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+                static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
+                static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
+    } else {
+        rmsnorm_wave_kernel<T, kVecs, kRows, kResidual, false>
+            <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
+                static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
+                static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
+    }
 }
 
 template <typename T, bool kResidual>

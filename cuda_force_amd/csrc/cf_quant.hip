@@ -62,12 +62,17 @@ __device__ __forceinline__ int quant_code(float x, const BlockScale& b) {
 
 __device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
 
-/// Load the kPer elements of this lane (zero beyond `count`).
-template <typename T, bool kVec>
+/// Load the kPer elements of this lane (zero beyond `count`). kFull: the
+/// caller guarantees the whole vector is in range and aligned, so the load
+/// is unconditional (no branch, no select on the loaded data, which would
+/// make the compiler wait for each load before issuing the next).
+template <typename T, bool kVec, bool kFull>
 __device__ __forceinline__ void load_lane(const T* __restrict__ x, int64_t e, int64_t count,
                                           float* v) {
     constexpr int kPer = Storage<T>::kPerVec;
-    if (kVec && e + kPer <= count) {
+    if (kFull) {
+        unpack16<T>(load_stream16(x + e), v);
+    } else if (kVec && e + kPer <= count) {
         unpack16<T>(load_stream16(x + e), v);
     } else {
 #pragma unroll
@@ -76,8 +81,10 @@ __device__ __forceinline__ void load_lane(const T* __restrict__ x, int64_t e, in
 }
 
 /// Shared body of quantise and fake-quantise. kMode 0 writes codes + scales,
-/// kMode 1 writes q * s in T.
-template <typename T, bool kVec, int kMode>
+/// kMode 1 writes q * s in T. kFull: every element of this wave's blocks is
+/// inside `count` and the pointers are vector-aligned (all waves but the
+/// last), so loads and stores need no bounds tests.
+template <typename T, bool kVec, int kMode, bool kFull>
 __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __restrict__ q,
                                            float* __restrict__ scales, T* __restrict__ y,
                                            int64_t count) {
@@ -96,7 +103,7 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
         const int64_t block = base_block + u * kBlocksPerStep + sub;
-        load_lane<T, kVec>(x, block * kQuantBlockSize + part * kPer, count, v[u]);
+        load_lane<T, kVec, kFull>(x, block * kQuantBlockSize + part * kPer, count, v[u]);
     }
 
 #pragma unroll
@@ -112,7 +119,7 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
 
         const int64_t block = base_block + u * kBlocksPerStep + sub;
         const int64_t e = block * kQuantBlockSize + part * kPer;
-        if (e >= count) continue;
+        if (!kFull && e >= count) continue;
 
         int codes[kPer];
 #pragma unroll
@@ -120,7 +127,7 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
 
         if constexpr (kMode == 0) {
             if (part == 0) __builtin_nontemporal_store(b.s, scales + block);
-            if (kVec && e + kPer <= count) {
+            if (kFull || (kVec && e + kPer <= count)) {
                 uint32_t w[kPer / 4];
 #pragma unroll
                 for (int j = 0; j < kPer / 4; ++j) {
@@ -144,7 +151,7 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
             float out[kPer];
 #pragma unroll
             for (int i = 0; i < kPer; ++i) out[i] = static_cast<float>(codes[i]) * b.s;
-            if (kVec && e + kPer <= count) {
+            if (kFull || (kVec && e + kPer <= count)) {
                 store_stream16(y + e, pack16<T>(out));
             } else {
 #pragma unroll
@@ -156,28 +163,48 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
     }
 }
 
+/// True when every element of this wave's quantisation blocks is below
+/// `count` (wave-uniform).
+template <typename T>
+__device__ __forceinline__ bool wave_is_full(int64_t count) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    constexpr int64_t kBlocksPerWave = (kWaveSize / (kQuantBlockSize / kPer)) * kUnroll;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveSize) +
+                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
+    return (wave + 1) * kBlocksPerWave * kQuantBlockSize <= count;
+}
+
 template <typename T, bool kVec>
 __global__ __launch_bounds__(kDefaultBlockSize) void quantize_kernel(const T* __restrict__ x,
                                                                      int8_t* __restrict__ q,
                                                                      float* __restrict__ scales,
                                                                      int64_t count) {
-    quant_body<T, kVec, 0>(x, q, scales, nullptr, count);
+    if (kVec && wave_is_full<T>(count)) {
+        quant_body<T, kVec, 0, true>(x, q, scales, nullptr, count);
+    } else {
+        quant_body<T, kVec, 0, false>(x, q, scales, nullptr, count);
+    }
 }
 
 template <typename T, bool kVec>
 __global__ __launch_bounds__(kDefaultBlockSize) void fake_quant_kernel(const T* __restrict__ x,
                                                                        T* __restrict__ y,
                                                                        int64_t count) {
-    quant_body<T, kVec, 1>(x, nullptr, nullptr, y, count);
+    if (kVec && wave_is_full<T>(count)) {
+        quant_body<T, kVec, 1, true>(x, nullptr, nullptr, y, count);
+    } else {
+        quant_body<T, kVec, 1, false>(x, nullptr, nullptr, y, count);
+    }
 }
 
 /// y = float(q) * s, one multiply, rounded to Tout. Each lane owns kPer
 /// consecutive elements (always inside one block); a wave stores 1 KiB per
-/// step with 16-byte stores.
-template <typename Tout, bool kVec>
-__global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
-    const int8_t* __restrict__ q, const float* __restrict__ scales, Tout* __restrict__ y,
-    int64_t count) {
+/// step with 16-byte stores. kFull: the wave's whole range is below `count`
+/// and aligned, so nothing is bounds-tested.
+template <typename Tout, bool kVec, bool kFull>
+__device__ __forceinline__ void dequantize_body(const int8_t* __restrict__ q,
+                                                const float* __restrict__ scales,
+                                                Tout* __restrict__ y, int64_t count) {
     constexpr int kPer = Storage<Tout>::kPerVec;
     constexpr int64_t kStep = static_cast<int64_t>(kWaveSize) * kPer;
     const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
@@ -190,8 +217,8 @@ __global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
         const int64_t e = base + u * kStep;
-        scale[u] = e < count ? scales[e / kQuantBlockSize] : 0.0f;
-        if (kVec && e + kPer <= count) {
+        scale[u] = (kFull || e < count) ? scales[e / kQuantBlockSize] : 0.0f;
+        if (kFull || (kVec && e + kPer <= count)) {
             if constexpr (kPer == 4) {
                 const uint32_t w = load_stream4(q + e);
 #pragma unroll
@@ -213,11 +240,11 @@ __global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
         const int64_t e = base + u * kStep;
-        if (e >= count) continue;
+        if (!kFull && e >= count) continue;
         float out[kPer];
 #pragma unroll
         for (int i = 0; i < kPer; ++i) out[i] = static_cast<float>(codes[u][i]) * scale[u];
-        if (kVec && e + kPer <= count) {
+        if (kFull || (kVec && e + kPer <= count)) {
             store_stream16(y + e, pack16<Tout>(out));
         } else {
 #pragma unroll
@@ -225,6 +252,21 @@ __global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
                 if (e + i < count) Storage<Tout>::store(y + e + i, out[i]);
             }
         }
+    }
+}
+
+template <typename Tout, bool kVec>
+__global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
+    const int8_t* __restrict__ q, const float* __restrict__ scales, Tout* __restrict__ y,
+    int64_t count) {
+    constexpr int64_t kPerWave =
+        static_cast<int64_t>(kWaveSize) * Storage<Tout>::kPerVec * kUnroll;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveSize) +
+                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
+    if (kVec && (wave + 1) * kPerWave <= count) {
+        dequantize_body<Tout, kVec, true>(q, scales, y, count);
+    } else {
+        dequantize_body<Tout, kVec, false>(q, scales, y, count);
     }
 }
 

@@ -4,7 +4,10 @@
 // arithmetic for every storage type, y = exp(x - max) * (1 / sum), which is
 // the order ATen's vectorised CPU softmax uses. A row whose entries are all
 // -inf yields NaN, as torch does; the causal-masked configuration always has a
-// finite entry in column 0.
+// finite entry in column 0. exp is the hardware base-2 exponential of
+// (x - max) * log2(e) (__expf, as the reference's kernel uses): for the
+// non-positive arguments here its relative error is below 1e-7 * |x - max|,
+// inside the 1e-5 fp32 tolerance.
 //
 // Design (fast path): one wavefront per row with the row held in registers:
 // one 16-byte-vector read, a DPP max reduction, exp and a DPP sum reduction
@@ -44,8 +47,12 @@ __device__ __forceinline__ void store_vec(Tout* p, const float* v) {
 }
 
 /// One wave per kRows consecutive rows, one-shot grid; all of the wave's
-/// loads are issued before the first reduction.
-template <typename Tin, typename Tout, int kVecs, int kRows>
+/// loads are issued before the first reduction. No load depends on a
+/// condition (which would make the compiler wait for each one before the
+/// next): rows past the end are loaded from the last row and not stored,
+/// and with kFullCols every lane's vectors are inside the row; otherwise
+/// the missing columns are replaced by -inf after the load.
+template <typename Tin, typename Tout, int kVecs, int kRows, bool kFullCols>
 __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const Tin* x, Tout* y,
                                                                          int64_t rows,
                                                                          int64_t cols) {
@@ -61,12 +68,12 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
     uint4 raw[kRows][kVecs];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
+        const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             const int64_t idx = static_cast<int64_t>(j) * kWaveSize + lane;
-            if (row0 + r < rows && idx < vec_cols) {
-                raw[r][j] = load_stream16(x + (row0 + r) * cols + idx * kPer);
-            }
+            const int64_t ic = kFullCols || idx < vec_cols ? idx : vec_cols - 1;
+            raw[r][j] = load_stream16(x + row * cols + ic * kPer);
         }
     }
 
@@ -78,7 +85,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             const int64_t idx = static_cast<int64_t>(j) * kWaveSize + lane;
-            if (idx < vec_cols) {
+            if (kFullCols || idx < vec_cols) {
                 unpack16<Tin>(raw[r][j], v[j]);
             } else {
 #pragma unroll
@@ -99,7 +106,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
         for (int j = 0; j < kVecs; ++j) {
 #pragma unroll
             for (int i = 0; i < kPer; ++i) {
-                v[j][i] = expf(v[j][i] - row_max);
+                v[j][i] = __expf(v[j][i] - row_max);
                 partial[i & 1] += v[j][i];
             }
         }
@@ -109,7 +116,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             const int64_t idx = static_cast<int64_t>(j) * kWaveSize + lane;
-            if (idx < vec_cols) {
+            if (kFullCols || idx < vec_cols) {
 #pragma unroll
                 for (int i = 0; i < kPer; ++i) v[j][i] = v[j][i] * inv_sum;
                 store_vec<Tout, kPer>(y + row * cols + idx * kPer, v[j]);
@@ -134,14 +141,14 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_block_kernel(const 
         const float row_max = block_reduce_f32<kWavesPerBlock, MaxF32>(local_max, slot);
         float local_sum = 0.0f;
         for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-            local_sum += expf(Storage<Tin>::load(xr + c) - row_max);
+            local_sum += __expf(Storage<Tin>::load(xr + c) - row_max);
         }
         const float inv_sum = 1.0f / block_reduce_f32<kWavesPerBlock, AddF32>(local_sum, slot);
         // When x and y alias, every thread must finish reading before any
         // writes: the reductions above end in a barrier, and this pass reads
         // and writes the same element in the same thread.
         for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-            const float e = expf(Storage<Tin>::load(xr + c) - row_max);
+            const float e = __expf(Storage<Tin>::load(xr + c) - row_max);
             Storage<Tout>::store(y + row * cols + c, e * inv_sum);
         }
     }
@@ -156,15 +163,27 @@ void launch_wave(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t
     const int64_t grid_rows = ceil_div<int64_t>(rows, kRows) >= simds ? kRows : 1;
     const int64_t waves = ceil_div<int64_t>(rows, grid_rows);
     const int64_t grid = ceil_div<int64_t>(waves, kWavesPerBlock);
+    const bool full = cols / Storage<Tin>::kPerVec == static_cast<int64_t>(kVecs) * kWaveSize;
+    const auto* xin = static_cast<const Tin*>(x);
+    auto* out = static_cast<Tout*>(y);
+    const unsigned g = static_cast<unsigned>(grid);
     if (grid_rows == 1) {
-        softmax_wave_kernel<Tin, Tout, kVecs, 1>
-            <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-                static_cast<const Tin*>(x), static_cast<Tout*>(y), rows, cols);
+        if (full) {
+            softmax_wave_kernel<Tin, Tout, kVecs, 1, true><<<g, kDefaultBlockSize, 0, stream>>>(
+                xin, out, rows, cols);
+        } else {
+            softmax_wave_kernel<Tin, Tout, kVecs, 1, false><<<g, kDefaultBlockSize, 0, stream>>>(
+                xin, out, rows, cols);
+        }
         return;
     }
-    softmax_wave_kernel<Tin, Tout, kVecs, kRows>
-        <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            static_cast<const Tin*>(x), static_cast<Tout*>(y), rows, cols);
+    if (full) {
+        softmax_wave_kernel<Tin, Tout, kVecs, kRows, true><<<g, kDefaultBlockSize, 0, stream>>>(
+            xin, out, rows, cols);
+    } else {
+        softmax_wave_kernel<Tin, Tout, kVecs, kRows, false><<<g, kDefaultBlockSize, 0, stream>>>(
+            xin, out, rows, cols);
+    }
 }
 
 template <typename Tin, typename Tout>
