@@ -148,6 +148,20 @@ __device__ __forceinline__ float block_reduce_f32(float v, float* slot) {
     }
 }
 
+/// Workgroup barrier after LDS writes that does not wait for global loads:
+/// s_waitcnt lgkmcnt(0) (this wave's LDS writes are done), then s_barrier.
+/// __syncthreads() would also wait for every outstanding global load
+/// (vmcnt(0)), which defeats loads meant to stay in flight across the
+/// barrier. The empty asm statements keep the compiler from moving memory
+/// accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    // vmcnt field at its maximum (no wait), expcnt 7 (no wait), lgkmcnt 0.
+    __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // Device: 16-bit float storage.
 // ---------------------------------------------------------------------------

@@ -54,13 +54,22 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
                          static_cast<int64_t>(threadIdx.x) / kWaveSize;
     const int64_t row0 = wave * kRows;
     __shared__ uint4 w_lds[kFullCols ? kVecs * kWaveSize : 1];
+    // With kFullCols the weight is staged in LDS: its loads go out first so
+    // that the LDS store below waits for them alone, not for the row loads.
+    // (Unguarded when the weight is a whole number of workgroup-wide
+    // vectors: a guarded index makes the compiler move the staging array
+    // into memory and wait for it.)
+    constexpr int kWeightVecs = kVecs * kWaveSize;
+    constexpr bool kStageGuard = kWeightVecs % kDefaultBlockSize != 0;
+    constexpr int kStage = kFullCols ? ceil_div(kWeightVecs, kDefaultBlockSize) : 1;
+    uint4 wstage[kStage];
     if constexpr (kFullCols) {
-        for (int i = static_cast<int>(threadIdx.x); i < kVecs * kWaveSize; i += kDefaultBlockSize) {
-            w_lds[i] = reinterpret_cast<const uint4*>(w)[i];
+#pragma unroll
+        for (int k = 0; k < kStage; ++k) {
+            const int i = k * kDefaultBlockSize + static_cast<int>(threadIdx.x);
+            if (!kStageGuard || i < kWeightVecs) wstage[k] = reinterpret_cast<const uint4*>(w)[i];
         }
-        __syncthreads();
     }
-    if (row0 >= rows) return;  // wave-uniform
 
     uint4 xv[kRows][kVecs];
 #pragma unroll
@@ -73,6 +82,17 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
             xv[r][j] = load_stream16(x + row * cols + vc * kPer);
         }
     }
+    // Stage the weight while the row loads are in flight (a wave past the
+    // last row still takes part in the barrier, then leaves).
+    if constexpr (kFullCols) {
+#pragma unroll
+        for (int k = 0; k < kStage; ++k) {
+            const int i = k * kDefaultBlockSize + static_cast<int>(threadIdx.x);
+            if (!kStageGuard || i < kWeightVecs) w_lds[i] = wstage[k];
+        }
+        lds_barrier();
+    }
+    if (row0 >= rows) return;  // wave-uniform
     uint4 wv[kVecs];
 #pragma unroll
     for (int j = 0; j < kVecs; ++j) {

@@ -19,11 +19,17 @@
 // The absmax is reduced over the integer bit patterns of |x|, which orders
 // non-negative floats correctly and propagates NaN the way torch.amax does.
 //
-// The per-element divide is the only expensive arithmetic. x * (1/s) is within
-// 2.3e-5 of fl(x/s) for every |x| <= absmax; rint only depends on which side of
-// a half-integer the quotient lies, so the multiply is used unless it lands
-// within 6e-5 of a .5 boundary, where the exact IEEE divide is redone. Blocks
-// with a subnormal scale (1/s would overflow) always divide.
+// The per-element divide is the only expensive arithmetic. With inv the
+// correctly rounded 1/s (one IEEE divide per block), q0 = fl(x * inv) is
+// within 2.3e-5 of fl(x/s) for every |x| <= absmax, so rint(q0) is the code
+// unless q0 lies within 6e-5 of a half-integer. There one Markstein step,
+// q1 = fma(fma(-q0, s, x), inv, q0), recovers fl(x/s) itself (Markstein's
+// correctly-rounded-quotient theorem for a correctly rounded reciprocal) and
+// rint(q1) rounds half to even exactly as rint(x / s) does - no divide, no
+// branch. (bf16 inputs land near a half-integer for ~0.3% of elements, far
+// too often for a divergent fallback.) The theorem needs the residual to
+// stay clear of the subnormal range, which holds for s >= 2^-100; blocks with
+// a smaller scale use the IEEE divide.
 #include "cf_common.hpp"
 
 namespace cf {
@@ -31,7 +37,7 @@ namespace {
 
 constexpr int kUnroll = 4;
 constexpr float kTieMargin = 6.0e-5f;
-constexpr float kFltMinNormal = 1.17549435e-38f;
+constexpr float kMinFastScale = 7.88860905e-31f;  // 2^-100
 
 struct BlockScale {
     float s;
@@ -46,18 +52,29 @@ __device__ __forceinline__ BlockScale block_scale(uint32_t absmax_bits) {
     BlockScale b;
     b.s = s;
     b.inv = 1.0f / s;
-    b.exact = !(s >= kFltMinNormal);
+    b.exact = !(s >= kMinFastScale);
     return b;
 }
 
-/// rint(x / s) clamped to [-127, 127]; NaN gives 0 (what ATen's float->int8
-/// conversion of a NaN yields after torch.clamp propagates it).
-__device__ __forceinline__ int quant_code(float x, const BlockScale& b) {
-    const float quotient = b.exact ? x / b.s : x * b.inv;
-    float r = rintf(quotient);
-    if (fabsf(quotient - r) > 0.5f - kTieMargin) r = rintf(x / b.s);
+/// A rounded quotient clamped to [-127, 127]; NaN gives 0 (what ATen's
+/// float->int8 conversion of a NaN yields after torch.clamp propagates it).
+__device__ __forceinline__ int clamp_code(float r) {
     if (r != r) return 0;
     return static_cast<int>(fminf(fmaxf(r, -127.0f), 127.0f));
+}
+
+/// rint(x / s), round half to even, via the reciprocal and, next to a
+/// half-integer, one Markstein correction (valid unless b.exact).
+__device__ __forceinline__ int fast_code(float x, const BlockScale& b) {
+    const float q0 = x * b.inv;
+    const float r0 = rintf(q0);
+    const float q1 = fmaf(fmaf(-q0, b.s, x), b.inv, q0);  // fl(x / s)
+    return clamp_code(fabsf(q0 - r0) > 0.5f - kTieMargin ? rintf(q1) : r0);
+}
+
+/// rint(x / s) with the IEEE divide.
+__device__ __forceinline__ int exact_code(float x, const BlockScale& b) {
+    return clamp_code(rintf(x / b.s));
 }
 
 __device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
@@ -105,6 +122,9 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
         const int64_t block = base_block + u * kBlocksPerStep + sub;
         load_lane<T, kVec, kFull>(x, block * kQuantBlockSize + part * kPer, count, v[u]);
     }
+    // Keep every load of the step ahead of the first use: without this the
+    // scheduler starts on block 0 after two of the four loads.
+    __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -121,9 +141,17 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
         const int64_t e = block * kQuantBlockSize + part * kPer;
         if (!kFull && e >= count) continue;
 
+        // Reciprocal path for every element; blocks with a scale below
+        // 2^-100 (rare: only when the whole block is that small) divide.
         int codes[kPer];
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) codes[i] = quant_code(v[u][i], b);
+        for (int i = 0; i < kPer; ++i) codes[i] = fast_code(v[u][i], b);
+        if (__any(b.exact)) {
+            if (b.exact) {
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) codes[i] = exact_code(v[u][i], b);
+            }
+        }
 
         if constexpr (kMode == 0) {
             if (part == 0) __builtin_nontemporal_store(b.s, scales + block);

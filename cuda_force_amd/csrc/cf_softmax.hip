@@ -76,6 +76,8 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
             raw[r][j] = load_stream16(x + row * cols + ic * kPer);
         }
     }
+    // Keep all of the wave's loads ahead of the first reduction.
+    __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
