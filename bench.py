@@ -2,6 +2,7 @@
 """Benchmark of the custom-op hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
+                    [--configs 1,2,3,5]
 
 Prints ONE JSON line (the driver's contract). The workload behind `value` is
 BASELINE.json's configs[1] - the memory-bound pair RMSNorm bf16 [16384, 4096]
@@ -19,11 +20,13 @@ profiles/ (null when absent). `cpu_baseline` times the reference's own CPU
 operators (oracle/_ref, built from the reference source) on a bounded sample
 of the same workload on this host's cores.
 
-`breakdown` reports every other configuration the same way (median of
-event-timed launches, cache-cold rotation): config 1 quantise/dequantise,
-config 2 per kernel, config 3 fused LoRA TFLOP/s (with hipBLASLt's plain GEMM
-through torch for context) and its adapter backward, config 5 bulk 7B
-quantise/dequantise aggregate GB/s, and a plain copy's achieved bandwidth.
+`breakdown` reports every other configuration (`--configs` selects them):
+median over 5 batches of back-to-back launches timed by HIP events, after at
+least 0.3 s of warm-up, with cache-cold rotation: config 1
+quantise/dequantise, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
+hipBLASLt's plain GEMM through torch for context) and its adapter backward,
+config 5 bulk 7B quantise/dequantise aggregate GB/s, and a plain copy's
+achieved bandwidth.
 """
 
 from __future__ import annotations
@@ -86,19 +89,39 @@ def sets_for(bytes_per_set: int, minimum: int = 2) -> int:
     return max(minimum, -(-CACHE_FLUSH_BYTES // max(bytes_per_set, 1)))
 
 
-def time_launches(torch, launches, warmup: int, runs: int) -> list[float]:
-    """Event-timed durations (ms) of `runs` launches cycling over `launches`."""
-    for i in range(warmup):
+WARMUP_SECONDS = 0.3
+
+
+def warm(torch, launches, warmup: int) -> None:
+    """At least `warmup` launches and WARMUP_SECONDS of them, so the clocks
+    have ramped before anything is timed."""
+    started = time.perf_counter()
+    i = 0
+    while i < warmup or time.perf_counter() - started < WARMUP_SECONDS:
         launches[i % len(launches)]()
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(runs)]
-    stops = [torch.cuda.Event(enable_timing=True) for _ in range(runs)]
-    for i in range(runs):
-        starts[i].record()
-        launches[i % len(launches)]()
-        stops[i].record()
-    torch.cuda.synchronize()
-    return [s.elapsed_time(e) for s, e in zip(starts, stops)]
+
+
+def time_launches(torch, launches, warmup: int, runs: int, batches: int = 5) -> list[float]:
+    """Average launch duration (ms) of each of `batches` back-to-back batches
+    of `runs` launches cycling over `launches`, timed by HIP events on the
+    current stream (per-launch events would add their own overhead to short
+    kernels)."""
+    warm(torch, launches, warmup)
+    out = []
+    for _ in range(batches):
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(runs):
+            launches[i % len(launches)]()
+        stop.record()
+        torch.cuda.synchronize()
+        out.append(start.elapsed_time(stop) / runs)
+    return out
 
 
 def summary(samples_ms: list[float]) -> dict:
@@ -420,12 +443,13 @@ def profiled_traffic() -> float | None:
 def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=50)
-    parser.add_argument("--warmup", type=int, default=10)
-    parser.add_argument("--runs", type=int, default=50, help="event-timed launches per breakdown kernel")
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=400)
+    parser.add_argument("--runs", type=int, default=40, help="launches per timed batch (5 batches) per breakdown kernel")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--quick", action="store_true", help="skip the breakdown (main step only)")
+    parser.add_argument("--configs", default="1,2,3,5", help="breakdown configs to run (comma-separated)")
     parser.add_argument("--detail", default="", help="also write the full result JSON here")
     args = parser.parse_args(argv)
 
@@ -455,10 +479,13 @@ def main(argv: list[str] | None = None) -> int:
     del calib
     breakdown = {}
     if not args.quick:
+        wanted = {f"config{c.strip()}" for c in args.configs.split(",") if c.strip()}
         for name, fn in (("config1", lambda: bench_quant(torch, cf, args.warmup, args.runs)),
                          ("config2", lambda: bench_rowops(torch, cf, args.warmup, args.runs)),
                          ("config3", lambda: bench_lora(torch, cf, args.warmup, args.runs)),
                          ("config5", lambda: bench_bulk_quant(torch, cf, 3))):
+            if name not in wanted:
+                continue
             log(f"breakdown {name}")
             breakdown.update(fn())
             torch.cuda.empty_cache()

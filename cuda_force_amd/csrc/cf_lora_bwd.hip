@@ -229,8 +229,17 @@ __global__ __launch_bounds__(kThreads) void sum_g_kernel(const float* __restrict
     if (i >= kRankPad * Mp) return;
     const int64_t m = i / kRankPad;
     const int64_t j = i % kRankPad;
+    // Loads of a group of tiles go out together; the adds keep tile order.
     float total = 0.0f;
-    for (int64_t t = 0; t < tiles; ++t) total += gpart[(t * Mp + m) * kRankPad + j];
+    int64_t t = 0;
+    for (; t + 8 <= tiles; t += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = gpart[((t + k) * Mp + m) * kRankPad + j];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) total += v[k];
+    }
+    for (; t < tiles; ++t) total += gpart[(t * Mp + m) * kRankPad + j];
     gt[j * Mp + m] = static_cast<uint16_t>(f32_to_bf16_bits(total));
 }
 
@@ -244,8 +253,17 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const float* __restric
     if (i >= rank * C) return;
     const int64_t j = i / C;
     const int64_t n = i % C;
+    // Loads of a group of tiles go out together; the adds keep tile order.
     float total = 0.0f;
-    for (int64_t t = 0; t < tiles; ++t) total += colpart[(t * kRankPad + j) * C + n];
+    int64_t t = 0;
+    for (; t + 8 <= tiles; t += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = colpart[((t + k) * kRankPad + j) * C + n];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) total += v[k];
+    }
+    for (; t < tiles; ++t) total += colpart[(t * kRankPad + j) * C + n];
     const int64_t dst = kTransposed ? n * rank + j : j * C + n;
     out[dst] = static_cast<uint16_t>(f32_to_bf16_bits(scale * total));
 }
