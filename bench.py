@@ -2,7 +2,7 @@
 """Benchmark of the custom-op hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--configs 1,2,3,5]
+                    [--configs 1,2,3,4,5]
 
 Prints ONE JSON line (the driver's contract). The workload behind `value` is
 BASELINE.json's configs[1] - the memory-bound pair RMSNorm bf16 [16384, 4096]
@@ -25,7 +25,8 @@ median over 5 batches of back-to-back launches timed by HIP events, after at
 least 0.3 s of warm-up, with cache-cold rotation: config 1
 quantise/dequantise, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
 hipBLASLt's plain GEMM through torch for context) and its adapter backward,
-config 5 bulk 7B quantise/dequantise aggregate GB/s, and a plain copy's
+config 4 the Llama block forward (tokens/s end to end, per-operator event
+times and TFLOP/s), config 5 bulk 7B quantise/dequantise aggregate GB/s, and a plain copy's
 achieved bandwidth.
 """
 
@@ -345,6 +346,38 @@ def bench_lora(torch, cf, warmup: int, runs: int) -> dict:
     return out
 
 
+def bench_block(torch, cf, warmup: int, runs: int) -> dict:
+    """config 4: one Llama block (8 x 512 tokens, hidden 4096, 32 heads, MLP 11008,
+    LoRA r16 alpha 32 on every projection) through the custom operators."""
+    from cuda_force_amd.transformer_block import BlockConfig, LlamaBlock, timed_forward
+
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    config = BlockConfig()
+    batch, seq = 8, 512
+    block = LlamaBlock(config, "cuda", torch.bfloat16, gen)
+    x = torch.randn(batch, seq, config.hidden, generator=gen, device="cuda").to(torch.bfloat16)
+    residual = torch.randn(batch, seq, config.hidden, generator=gen, device="cuda").to(torch.bfloat16)
+    tokens = batch * seq
+    flops = block.gemm_flops(tokens, seq)
+    total = summary(time_launches(torch, [lambda: block.forward(x, residual)], warmup, max(runs // 4, 5)))
+    stages: dict[str, list[float]] = {}
+    for _ in range(20):
+        for name, ms in timed_forward(block, x, residual).items():
+            stages.setdefault(name, []).append(ms)
+    per_op = {}
+    for name, samples in stages.items():
+        ms = statistics.median(samples)
+        entry = {"ms": ms}
+        if name in flops:
+            entry["TFLOP/s"] = flops[name] / (ms * 1e-3) / 1e12
+        per_op[name] = entry
+    gemm = sum(flops.values())
+    return {"block_c4_bf16_8x512_h4096": {
+        **total, "tokens": tokens, "tokens/s": tokens / (total["median_ms"] * 1e-3),
+        "gemm_flops": gemm, "gemm_TFLOP/s_end_to_end": gemm / (total["median_ms"] * 1e-3) / 1e12,
+        "per_op_events": per_op}}
+
+
 def bench_bulk_quant(torch, cf, warmup: int) -> dict:
     """config 5: every weight of a 7B model, bf16 -> int8 + scales -> bf16."""
     gen = torch.Generator(device="cuda").manual_seed(5)
@@ -449,7 +482,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--quick", action="store_true", help="skip the breakdown (main step only)")
-    parser.add_argument("--configs", default="1,2,3,5", help="breakdown configs to run (comma-separated)")
+    parser.add_argument("--configs", default="1,2,3,4,5", help="breakdown configs to run (comma-separated)")
     parser.add_argument("--detail", default="", help="also write the full result JSON here")
     args = parser.parse_args(argv)
 
@@ -483,6 +516,7 @@ def main(argv: list[str] | None = None) -> int:
         for name, fn in (("config1", lambda: bench_quant(torch, cf, args.warmup, args.runs)),
                          ("config2", lambda: bench_rowops(torch, cf, args.warmup, args.runs)),
                          ("config3", lambda: bench_lora(torch, cf, args.warmup, args.runs)),
+                         ("config4", lambda: bench_block(torch, cf, 20, args.runs)),
                          ("config5", lambda: bench_bulk_quant(torch, cf, 3))):
             if name not in wanted:
                 continue

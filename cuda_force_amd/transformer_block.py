@@ -102,12 +102,14 @@ class LlamaBlock:
         def heads(t):
             return t.view(batch, seq, c.heads, c.head_dim).transpose(1, 2).contiguous()
 
-        qh, kh, vh = heads(q), heads(k), heads(v)
-        # Every operand of the batched products is contiguous (the transposed
-        # key included): no transposed views reach the bf16 batched GEMM.
-        scores = torch.matmul(qh, kh.transpose(-2, -1).contiguous()) * (1.0 / math.sqrt(c.head_dim))
+        qh, vh = heads(q), heads(v)
+        # Every operand of the batched products is contiguous: the key is laid
+        # out [batch, heads, head_dim, seq] by one copy, so no transposed view
+        # reaches the bf16 batched GEMM.
+        kt = k.view(batch, seq, c.heads, c.head_dim).permute(0, 2, 3, 1).contiguous()
         causal = torch.triu(torch.full((seq, seq), float("-inf"), device=normed.device), 1)
-        scores = (scores + causal.to(scores.dtype)).contiguous()
+        # causal + scores / sqrt(d) in one pass over the score matrix.
+        scores = torch.add(causal.to(q.dtype), torch.matmul(qh, kt), alpha=1.0 / math.sqrt(c.head_dim))
         mark("scores_matmul")
         weights = ops.softmax(scores.view(-1, seq)).view_as(scores)
         mark("softmax")
