@@ -18,8 +18,9 @@
 //     check. K-step 32, four LDS stages, prefetch distance three: the loads for
 //     step j + 3 are issued while step j + 1 is read into fragment registers
 //     and step j is multiplied.
-//   * x keeps its K-major layout in LDS (64-byte rows, 16-byte chunks
-//     swizzled by row bit 2). w keeps its N-major layout
+//   * x keeps its K-major layout in LDS and travels two K-steps per load
+//     (whole 128-byte lines of each row, 16-byte chunks swizzled by the
+//     row's low three bits) into a ring of two slots. w keeps its N-major layout
 //     (512-byte rows, chunks swizzled by k bits 0, 1 and 3) and is
 //     transposed on the way out of LDS by ds_read_b64_tr_b16, which hands
 //     each lane four k values of one column. All operand reads are free of
@@ -58,13 +59,15 @@ constexpr int kBK = 32;
 constexpr int kStages = 4;
 constexpr int kThreads = 512;
 constexpr int kMaxFusedRank = 16;
-constexpr int kTileX = kBM * kBK * 2;                    // 16 KiB: [256 m][32 k]
+constexpr int kXPair = kBM * 2 * kBK * 2;               // 32 KiB: [256 m][64 k], two K-steps
+constexpr int kXSlots = 2;
 constexpr int kTileW = kBK * kBN * 2;                    // 16 KiB: [32 k][256 n]
 constexpr int kTileA = kBK * kMaxFusedRank * 2;          // 1 KiB:  [32 k][16 j]
-constexpr int kStage = kTileX + kTileW + kTileA;
+constexpr int kStage = kTileW + kTileA;
 constexpr int kTileB = kMaxFusedRank * kBN * 2;          // 8 KiB:  [16 j][256 n]
 constexpr int kXaBytes = (kBM / 16) * 64 * 8;            // 8 KiB: bf16 x @ a fragments
-constexpr int kOffB = kStages * kStage;
+constexpr int kOffW = kXSlots * kXPair;
+constexpr int kOffB = kOffW + kStages * kStage;
 constexpr int kOffXa = kOffB + kTileB;
 constexpr int kLdsBytes = kOffXa + kXaBytes;             // 148 KiB
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 workgroup");
@@ -84,9 +87,9 @@ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) |
 // two 8-lane octets per cycle, octet o together with o ^ 3 or with 7 - o
 // (the measurements allow both); the x swizzle is conflict-free either way.
 
-/// Chunk swizzle of the x tile (64-byte rows of 4 chunks): row r keeps
-/// logical chunk c in physical chunk c ^ x_swizzle(r).
-__device__ __forceinline__ int x_swizzle(int row) { return ((row >> 2) & 1) << 1; }
+/// Chunk swizzle of the x tile (128-byte rows of 8 chunks, two K-steps):
+/// row r keeps logical chunk c in physical chunk c ^ (r & 7).
+__device__ __forceinline__ int x_swizzle(int row) { return row & 7; }
 
 /// Chunk swizzle of the w tile (512-byte rows of 32 chunks): k rows 0-3 of
 /// a transposed read land in four different 32-byte bank groups, and rows
@@ -234,15 +237,17 @@ void lora_fused_bf16_kernel(FusedArgs args) {
 
     // ---- HBM -> LDS roles (each load instruction fills 1 KiB of LDS, lane l
     // at byte 16 l; the global side is permuted to realise the swizzles) ----
-    // x: wave covers 16-row slabs q = 2 wave + i; lane -> row 16q + l/4,
-    // physical chunk l%4 (64 contiguous bytes of a row per 4 lanes).
+    // x travels two K-steps at a time, as whole 128-byte lines of each row
+    // (a 64-byte piece per K-step would make every line two L1 requests):
+    // wave covers rows 32 wave .. +31, 8 rows per load; lane -> row
+    // 32 wave + 8 i + l/8, physical chunk l%8.
     const int64_t rows_here = M - m0 < kBM ? M - m0 : kBM;
     const i32x4_t xbuf = raw_buffer_words(args.x + m0 * K, static_cast<uint32_t>(rows_here * K * 2));
-    uint32_t x_dma[2];
+    uint32_t x_dma[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int row = 16 * (wave * 2 + i) + (lane >> 2);
-        const int chunk = (lane & 3) ^ x_swizzle(row);
+    for (int i = 0; i < 4; ++i) {
+        const int row = 32 * wave + 8 * i + (lane >> 3);
+        const int chunk = (lane & 7) ^ x_swizzle(row);
         x_dma[i] = static_cast<uint32_t>((row * K + chunk * 8) * 2);
     }
     // w: wave covers k-row pairs q = 2 wave + i; lane -> row 2q + l/32,
@@ -272,35 +277,37 @@ void lora_fused_bf16_kernel(FusedArgs args) {
 
     // LDS byte address of the tile storage (the DMA takes it in M0).
     const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)lds));
-    // One DMA instruction of K-step kt: pieces 0, 1 are x, 2, 3 are w, 4 is
-    // a (adapter only). The K-loop spreads them over a step's MFMAs rather
-    // than issuing them in one burst after the barrier.
-    auto issue_piece = [&](int64_t kt, int piece) {
-        const uint32_t stage = lds_addr + static_cast<uint32_t>(kt % kStages) * kStage;
+    // DMA instructions: piece 0, 1 of K-step kt are w, piece 2 is a (adapter
+    // only), into the stage ring; piece i of x pair p (K-steps 2p, 2p + 1)
+    // goes into x slot p % 2. The K-loop spreads them over a step's MFMAs
+    // rather than issuing them in one burst after the barrier.
+    auto issue_w = [&](int64_t kt, int piece) {
+        const uint32_t stage = lds_addr + kOffW + static_cast<uint32_t>(kt % kStages) * kStage;
         const int64_t k0 = kt * kBK;
         if (piece < 2) {
-            dma16(xbuf, stage + (wave * 2 + piece) * 1024, x_dma[piece],
-                  static_cast<uint32_t>(k0 * 2));
-        } else if (piece < 4) {
-            dma16(wbuf, stage + kTileX + (wave * 2 + piece - 2) * 1024, w_dma[piece - 2],
+            dma16(wbuf, stage + (wave * 2 + piece) * 1024, w_dma[piece],
                   static_cast<uint32_t>(k0 * N * 2));
         } else if (kAdapter) {
-            dma4(abuf, stage + kTileX + kTileW + (wave & 3) * 256, a_dma,
+            dma4(abuf, stage + kTileW + (wave & 3) * 256, a_dma,
                  static_cast<uint32_t>(k0 * rank * 2));
         }
     };
-    auto issue_tile = [&](int64_t kt) {
-#pragma unroll
-        for (int piece = 0; piece < 5; ++piece) issue_piece(kt, piece);
+    auto issue_x = [&](int64_t pair, int piece) {
+        const uint32_t slot = lds_addr + static_cast<uint32_t>(pair % kXSlots) * kXPair;
+        dma16(xbuf, slot + wave * 4096 + piece * 1024, x_dma[piece],
+              static_cast<uint32_t>(pair * 4 * kBK));
     };
-    constexpr int kLoadsPerTile = kAdapter ? 5 : 4;  // DMA instructions per K-step per wave
+    constexpr int kWLoads = kAdapter ? 3 : 2;  // w (+ a) DMA instructions per K-step per wave
+    constexpr int kXLoads = 4;                 // x DMA instructions per pair of K-steps per wave
 
     // ---- LDS -> register fragment roles ----
     // x (B operand): fragment i holds row block rb(i) = (i + 2 wn) % 4 of the
     // wave's 64 rows (row wm*64 + 16 rb + lane%16, chunk lane/16), so that
     // the x @ a share of either wave is always fragments 0 and 1. The
     // swizzle only depends on row bit 2, which is lane bit 2.
-    const int x_rd = (wm * 64 + (lane & 15)) * (kBK * 2) + (((lane >> 4) ^ x_swizzle(lane)) << 4);
+    // Row wm*64 + 16 rb + lane%16 has row & 7 == lane & 7; the odd K-step of
+    // a pair is the upper four chunks (byte offset ^ 64).
+    const int x_rd = (wm * 64 + (lane & 15)) * (4 * kBK) + (((lane >> 4) ^ x_swizzle(lane)) << 4);
     // w (A operand, transposed read): group g = lane/16 takes k rows 8g .. 8g+3
     // (then +4); lane j of the group reads row 8g + j/4, columns 4(j%4) .. +3
     // of the 16-column block; the read returns column j's four k values.
@@ -317,21 +324,21 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     const int a_rd1 = a_offset(8 * g + 4 + (jl >> 2), (jl & 3) * 8);
 
     auto read_x = [&](XFrags& f, int64_t kt) {
-        const int stage = static_cast<int>(kt % kStages) * kStage;
-        const uint8_t* sx = lds + stage;
+        const uint8_t* sx = lds + static_cast<int>((kt >> 1) % kXSlots) * kXPair;
+        const int x_off = x_rd ^ (static_cast<int>(kt & 1) << 6);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int rb = (i + 2 * wn) & 3;
-            f.x[i] = *reinterpret_cast<const bf16x8_t*>(sx + x_rd + rb * 1024);
+            f.x[i] = *reinterpret_cast<const bf16x8_t*>(sx + x_off + rb * 2048);
         }
         if (kAdapter) {
-            const uint8_t* sa = sx + kTileX + kTileW;
+            const uint8_t* sa = lds + kOffW + static_cast<int>(kt % kStages) * kStage + kTileW;
             f.a = concat(lds_read_tr(sa, a_rd0), lds_read_tr(sa, a_rd1));
         }
     };
     // w fragment jb (A operand): column wn*128 + 16 jb + lane%16, same k.
     auto read_w = [&](int64_t kt, int jb) {
-        const uint8_t* sw = lds + static_cast<int>(kt % kStages) * kStage + kTileX;
+        const uint8_t* sw = lds + kOffW + static_cast<int>(kt % kStages) * kStage;
         return concat(lds_read_tr(sw, w_rd[jb]), lds_read_tr(sw, w_rd[jb] + 4 * kBN * 2));
     };
 
@@ -350,7 +357,9 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     // have issued. x is double-buffered (its fragments are used until the
     // end of the step).
     bf16x8_t wf[8];
-    auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next, auto issue) {
+    // On step kt the DMA goes out for K-step kt + 3 (w, a) and, on odd steps,
+    // for x pair (kt + 3) / 2, whose slot the barrier of step kt has freed.
+    auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next, auto issue, auto odd) {
         if (kAdapter) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
@@ -366,7 +375,15 @@ void lora_fused_bf16_kernel(FusedArgs args) {
             }
             if constexpr (decltype(read_next)::value) wf[jb] = read_w(next_kt, jb);
             if constexpr (decltype(issue)::value) {
-                if (jb < 5) issue_piece(next_kt + 2, jb);
+                if constexpr (decltype(odd)::value) {
+                    if (jb < kXLoads) {
+                        issue_x((next_kt + 2) >> 1, jb);
+                    } else if (jb < kXLoads + kWLoads) {
+                        issue_w(next_kt + 2, jb - kXLoads);
+                    }
+                } else {
+                    if (jb < kWLoads) issue_w(next_kt + 2, jb);
+                }
             }
         }
     };
@@ -381,13 +398,24 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         dma16(bbuf, lds_addr + kOffB + wave * 1024, off, 0);
     }
     const int64_t k_tiles = K / kBK;  // even, >= 2
-    issue_tile(0);
-    issue_tile(1);
+    auto issue_w_all = [&](int64_t kt) {
+#pragma unroll
+        for (int piece = 0; piece < kWLoads; ++piece) issue_w(kt, piece);
+    };
+    auto issue_x_all = [&](int64_t pair) {
+#pragma unroll
+        for (int piece = 0; piece < kXLoads; ++piece) issue_x(pair, piece);
+    };
+    // Issue order as if steps -2 and -1 had run: x pair 0, w 0, w 1 | x pair 1, w 2.
+    issue_x_all(0);
+    issue_w_all(0);
+    issue_w_all(1);
     if (k_tiles > 2) {
-        issue_tile(2);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kLoadsPerTile));
+        issue_x_all(1);
+        issue_w_all(2);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kWLoads + kXLoads));
     } else {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoadsPerTile));
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
     }
     bare_barrier();  // step 0 in LDS
 
@@ -401,34 +429,43 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     // then the barrier for everyone's), the loads for kt + 3 reuse the stage
     // of kt - 1 (read during step kt - 2, consumed in step kt - 1, so every
     // wave is past it once it is at this barrier), step kt + 1 is read into
-    // registers while step kt is multiplied. The last four steps are peeled
-    // so the loop body has no branches.
+    // registers while step kt is multiplied. x pair p goes out on step
+    // 2p - 3 into the slot pair p - 2 left (its last K-step, 2p - 3, was read
+    // during step 2p - 4) and is first read on step 2p - 1. DMA completes in
+    // issue order, so the wait lets exactly the previous step's loads stay
+    // in flight: w (+ a) after an even step, w (+ a) and an x pair after an
+    // odd one. The last four steps are peeled so the loop body has no
+    // branches.
     using yes = std::true_type;
     using no = std::false_type;
-    auto step = [&](int64_t kt, XFrags& cur, XFrags& nxt, auto issue, auto wait_all, auto read) {
+    // Steps with f0 as the current fragments are even, with f1 odd.
+    auto step = [&](int64_t kt, XFrags& cur, XFrags& nxt, auto issue, auto wait_all, auto read,
+                    auto odd) {
         if constexpr (decltype(read)::value) {
             if constexpr (decltype(wait_all)::value) {
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            } else if constexpr (decltype(odd)::value) {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
             } else {
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoadsPerTile));
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads + kXLoads));
             }
             bare_barrier();
             read_x(nxt, kt + 1);
         }
-        multiply(cur, kt + 1, read, issue);
+        multiply(cur, kt + 1, read, issue, odd);
     };
     int64_t kt = 0;
     for (; kt + 4 < k_tiles; kt += 2) {
-        step(kt, f0, f1, yes{}, no{}, yes{});
-        step(kt + 1, f1, f0, yes{}, no{}, yes{});
+        step(kt, f0, f1, yes{}, no{}, yes{}, no{});
+        step(kt + 1, f1, f0, yes{}, no{}, yes{}, yes{});
     }
     if (k_tiles >= 4) {
-        step(kt, f0, f1, yes{}, no{}, yes{});
-        step(kt + 1, f1, f0, no{}, no{}, yes{});
+        step(kt, f0, f1, yes{}, no{}, yes{}, no{});
+        step(kt + 1, f1, f0, no{}, no{}, yes{}, yes{});
         kt += 2;
     }
-    step(kt, f0, f1, no{}, yes{}, yes{});
-    step(kt + 1, f1, f0, no{}, no{}, no{});
+    step(kt, f0, f1, no{}, yes{}, yes{}, no{});
+    step(kt + 1, f1, f0, no{}, no{}, no{}, yes{});
 
     // ---- epilogue ----
     if (kAdapter) {
