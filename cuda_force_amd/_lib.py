@@ -24,6 +24,7 @@ CF_OK = 0
 CF_ERR_INVALID_ARGUMENT = 1
 CF_ERR_UNSUPPORTED = 2
 CF_ERR_HIP = 3
+CF_ERR_OUT_OF_MEMORY = 4
 
 CF_F32 = 0
 CF_F16 = 1
@@ -34,6 +35,31 @@ _I64 = ctypes.c_int64
 _I32 = ctypes.c_int
 _F = ctypes.c_float
 _SZ = ctypes.c_size_t
+
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_PI64 = ctypes.POINTER(ctypes.c_int64)
+_PI32 = ctypes.POINTER(ctypes.c_int)
+
+
+class StreamStatsC(ctypes.Structure):
+    """cf_stream_stats."""
+
+    _fields_ = [("batches_dispatched", ctypes.c_uint64), ("bytes_to_device", ctypes.c_uint64),
+                ("bytes_to_host", ctypes.c_uint64)]
+
+
+class PoolStatsC(ctypes.Structure):
+    """cf_pool_stats."""
+
+    _fields_ = [(name, ctypes.c_uint64) for name in (
+        "bytes_reserved", "bytes_in_use", "peak_bytes_in_use", "allocation_count",
+        "backend_allocations", "reuse_count", "free_count", "free_block_count")]
+
+
+CF_POOL_HOST = 0
+CF_POOL_DEVICE = 1
+CF_POOL_DEVICE_ASYNC = 2
+CF_POOL_PINNED = 3
 
 # name -> (restype, argtypes); must cover every function the header declares.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -63,6 +89,29 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_gelu": (_I32, [_P, _P, _I32, _I64, _P]),
     "cf_swiglu": (_I32, [_P, _P, _P, _I32, _I64, _P]),
     "cf_copy_bytes": (_I32, [_P, _P, _I64, _P]),
+    "cf_scheduler_create": (_I32, [_I64, _I32, _PP]),
+    "cf_scheduler_destroy": (_I32, [_P]),
+    "cf_scheduler_acquire": (_I32, [_P, _PI64, _PP]),
+    "cf_scheduler_stream": (_I32, [_P, _I64, _PP]),
+    "cf_scheduler_stream_count": (_I64, [_P]),
+    "cf_scheduler_copy_to_device": (_I32, [_P, _I64, _P, _P, _SZ]),
+    "cf_scheduler_copy_to_host": (_I32, [_P, _I64, _P, _P, _SZ]),
+    "cf_scheduler_record_completion": (_I32, [_P, _I64]),
+    "cf_scheduler_chain": (_I32, [_P, _I64, _I64]),
+    "cf_scheduler_note_dispatch": (_I32, [_P, _I64]),
+    "cf_scheduler_synchronize": (_I32, [_P, _I64]),
+    "cf_scheduler_query": (_I32, [_P, _I64, _PI32]),
+    "cf_scheduler_event_query": (_I32, [_P, _I64, _PI32]),
+    "cf_scheduler_synchronize_all": (_I32, [_P]),
+    "cf_scheduler_stats": (_I32, [_P, ctypes.POINTER(StreamStatsC), _I64, ctypes.POINTER(StreamStatsC)]),
+    "cf_stream_ordered_allocation_supported": (_I32, []),
+    "cf_pool_create": (_I32, [_I32, _P, _SZ, _PP]),
+    "cf_pool_destroy": (_I32, [_P]),
+    "cf_pool_allocate": (_I32, [_P, _SZ, _PP]),
+    "cf_pool_deallocate": (_I32, [_P, _P]),
+    "cf_pool_trim": (_I32, [_P]),
+    "cf_pool_get_stats": (_I32, [_P, ctypes.POINTER(PoolStatsC)]),
+    "cf_pool_backend_name": (ctypes.c_char_p, [_I32]),
 }
 
 

@@ -36,6 +36,7 @@ HIP_SOURCES = (
     "cf_lora.hip",
     "cf_lora_fused.hip",
     "cf_lora_bwd.hip",
+    "cf_scheduler.hip",
 )
 
 # Per-source additions. The fused LoRA kernel accumulates in VGPRs: the

@@ -24,10 +24,11 @@
  * Empty inputs (count <= 0, rows <= 0 or cols <= 0) return CF_OK without
  * launching anything, as every reference launcher does.
  *
- * Nothing in this library allocates device memory. Entry points that need
- * scratch space take a caller-provided `workspace` and publish its size through
- * a *_workspace_bytes() query, like the reference's lora_workspace_bytes
- * (cuda/include/cudaforge/lora_linear.cuh:62).
+ * No operator entry point allocates device memory. Those that need scratch
+ * space take a caller-provided `workspace` and publish its size through a
+ * *_workspace_bytes() query, like the reference's lora_workspace_bytes
+ * (cuda/include/cudaforge/lora_linear.cuh:62). Only the runtime section at the
+ * end (stream scheduler, caching pools) allocates, which is its purpose.
  */
 #ifndef CUDAFORGE_HIP_H
 #define CUDAFORGE_HIP_H
@@ -46,6 +47,7 @@ typedef enum cf_status {
     CF_ERR_INVALID_ARGUMENT = 1, /* shape, pointer, alignment or size error  */
     CF_ERR_UNSUPPORTED = 2,      /* dtype or shape combination with no kernel */
     CF_ERR_HIP = 3,              /* the HIP runtime reported an error         */
+    CF_ERR_OUT_OF_MEMORY = 4,    /* a pool backend could not supply a block   */
 } cf_status;
 
 typedef enum cf_dtype {
@@ -226,6 +228,147 @@ cf_status cf_swiglu(const void* gate, const void* up, void* y, cf_dtype dtype, i
  * the known-size kernel used to calibrate hardware byte counters and to
  * measure the achievable HBM bandwidth next to the ops above. */
 cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream);
+
+/* ---- runtime: stream scheduler and caching pools ------------------------
+ *
+ * The C form of the reference's GpuScheduler / StreamLease
+ * (cuda/include/cudaforge/gpu_scheduler.cuh:16-142, cuda/src/gpu_scheduler.cu)
+ * and MemoryPool with its backends (cpp/include/cudaforge/memory_pool.hpp:76-216,
+ * gpu_scheduler.cuh:150-258). C++ callers can use the same classes directly
+ * from include/cudaforge_runtime.hpp and include/cudaforge_pool.hpp. A lease
+ * is named by its stream index; the hipStream_t comes back as `void*`. Every
+ * stream is non-blocking and at the default priority. Handles are not
+ * reference counted: destroy each exactly once, after its last use. */
+
+typedef struct cf_scheduler cf_scheduler;
+typedef struct cf_pool cf_pool;
+
+typedef struct cf_stream_stats {
+    uint64_t batches_dispatched;
+    uint64_t bytes_to_device;
+    uint64_t bytes_to_host;
+} cf_stream_stats;
+
+typedef struct cf_pool_stats {
+    uint64_t bytes_reserved;
+    uint64_t bytes_in_use;
+    uint64_t peak_bytes_in_use;
+    uint64_t allocation_count;
+    uint64_t backend_allocations;
+    uint64_t reuse_count;
+    uint64_t free_count;
+    uint64_t free_block_count;
+} cf_pool_stats;
+
+typedef enum cf_pool_backend {
+    CF_POOL_HOST = 0,         /* malloc / free ("host")                     */
+    CF_POOL_DEVICE = 1,       /* hipMalloc / hipFree ("device")             */
+    CF_POOL_DEVICE_ASYNC = 2, /* hipMallocAsync / hipFreeAsync on a stream ("device-async") */
+    CF_POOL_PINNED = 3,       /* hipHostMalloc / hipHostFree ("pinned")     */
+} cf_pool_backend;
+
+/* A scheduler owning `stream_count` (>= 1) streams on `device`; 0 streams is
+ * CF_ERR_INVALID_ARGUMENT, as the reference's std::invalid_argument.
+ * Replaces GpuScheduler::GpuScheduler (cuda/src/gpu_scheduler.cu:10-33). */
+cf_status cf_scheduler_create(int64_t stream_count, int device, cf_scheduler** out);
+
+/* Waits for every stream, then releases them.
+ * Replaces GpuScheduler::~GpuScheduler (cuda/src/gpu_scheduler.cu:35-43). */
+cf_status cf_scheduler_destroy(cf_scheduler* scheduler);
+
+/* Next stream in round-robin order: its index and hipStream_t. Never blocks.
+ * Replaces GpuScheduler::acquire (cuda/src/gpu_scheduler.cu:45-49). */
+cf_status cf_scheduler_acquire(cf_scheduler* scheduler, int64_t* index, void** stream);
+
+/* hipStream_t of stream `index`.
+ * Replaces StreamLease::stream (cuda/include/cudaforge/gpu_scheduler.cuh:41). */
+cf_status cf_scheduler_stream(const cf_scheduler* scheduler, int64_t index, void** stream);
+
+/* Number of streams. Replaces GpuScheduler::stream_count
+ * (cuda/include/cudaforge/gpu_scheduler.cuh:127). */
+int64_t cf_scheduler_stream_count(const cf_scheduler* scheduler);
+
+/* Asynchronous host-to-device / device-to-host copy on stream `index`,
+ * counted in that stream's statistics; 0 bytes is a no-op. Replaces
+ * GpuScheduler::copy_to_device / copy_to_host (cuda/src/gpu_scheduler.cu:51-73). */
+cf_status cf_scheduler_copy_to_device(cf_scheduler* scheduler, int64_t index, void* device,
+                                      const void* host, size_t bytes);
+cf_status cf_scheduler_copy_to_host(cf_scheduler* scheduler, int64_t index, void* host,
+                                    const void* device, size_t bytes);
+
+/* Records stream `index`'s completion event on it.
+ * Replaces StreamLease::record_completion (cuda/include/cudaforge/gpu_scheduler.cuh:47). */
+cf_status cf_scheduler_record_completion(cf_scheduler* scheduler, int64_t index);
+
+/* Stream `waiter` waits (on the device) for the last completion recorded on
+ * stream `signaller`. Replaces GpuScheduler::chain (cuda/src/gpu_scheduler.cu:75-77). */
+cf_status cf_scheduler_chain(cf_scheduler* scheduler, int64_t waiter, int64_t signaller);
+
+/* Counts one dispatched batch on stream `index`.
+ * Replaces GpuScheduler::note_dispatch (cuda/src/gpu_scheduler.cu:79-82). */
+cf_status cf_scheduler_note_dispatch(cf_scheduler* scheduler, int64_t index);
+
+/* Blocks until stream `index` is idle. Replaces StreamLease::synchronize
+ * (cuda/include/cudaforge/gpu_scheduler.cuh:51). */
+cf_status cf_scheduler_synchronize(cf_scheduler* scheduler, int64_t index);
+
+/* *complete = 1 once everything issued to stream `index` has finished
+ * (StreamLease::complete, gpu_scheduler.cuh:53), or, for the event query, once
+ * its last recorded completion event has (CudaEvent::query via
+ * StreamLease::completion_event, gpu_scheduler.cuh:42). */
+cf_status cf_scheduler_query(cf_scheduler* scheduler, int64_t index, int* complete);
+cf_status cf_scheduler_event_query(cf_scheduler* scheduler, int64_t index, int* complete);
+
+/* Blocks until every stream is idle (shutdown, not per batch).
+ * Replaces GpuScheduler::synchronize_all (cuda/src/gpu_scheduler.cu:84-91). */
+cf_status cf_scheduler_synchronize_all(cf_scheduler* scheduler);
+
+/* Copies up to `capacity` per-stream records into `per_stream` (may be NULL
+ * when capacity is 0) and their sums into `totals` (batches_dispatched holds
+ * the total dispatch count). Replaces GpuScheduler::stats
+ * (cuda/src/gpu_scheduler.cu:93-105). */
+cf_status cf_scheduler_stats(const cf_scheduler* scheduler, cf_stream_stats* per_stream,
+                             int64_t capacity, cf_stream_stats* totals);
+
+/* 1 when the current device backs hipMallocAsync with a memory pool.
+ * Replaces supports_stream_ordered_allocation
+ * (cuda/include/cudaforge/gpu_scheduler.cuh:175-186). */
+int cf_stream_ordered_allocation_supported(void);
+
+/* A caching pool over `backend`; `stream` is used by CF_POOL_DEVICE_ASYNC only
+ * (its allocations and frees are ordered on it). Sizes round up to a power of
+ * two, never below `min_block_bytes` (0 is CF_ERR_INVALID_ARGUMENT).
+ * Replaces MemoryPool::MemoryPool (cpp/include/cudaforge/memory_pool.hpp:78-84)
+ * with DeviceAllocatorBackend, StreamOrderedAllocatorBackend,
+ * PinnedAllocatorBackend (gpu_scheduler.cuh:150-258) or HostAllocatorBackend
+ * (memory_pool.hpp:209-216). */
+cf_status cf_pool_create(cf_pool_backend backend, void* stream, size_t min_block_bytes,
+                         cf_pool** out);
+
+/* Returns every block, cached or checked out, to the backend.
+ * Replaces MemoryPool::~MemoryPool (cpp/include/cudaforge/memory_pool.hpp:94). */
+cf_status cf_pool_destroy(cf_pool* pool);
+
+/* *out = a block of at least `bytes` bytes (NULL for 0 bytes). CF_ERR_OUT_OF_MEMORY
+ * where the reference threw std::bad_alloc; the pool stays usable (trim and
+ * retry). Replaces MemoryPool::allocate (cpp/include/cudaforge/memory_pool.hpp:96-123). */
+cf_status cf_pool_allocate(cf_pool* pool, size_t bytes, void** out);
+
+/* Returns a block to its free list; NULL is a no-op, a pointer the pool did not
+ * hand out is CF_ERR_INVALID_ARGUMENT. Replaces MemoryPool::deallocate
+ * (cpp/include/cudaforge/memory_pool.hpp:128-145). */
+cf_status cf_pool_deallocate(cf_pool* pool, void* pointer);
+
+/* Hands cached blocks back to the backend.
+ * Replaces MemoryPool::trim (cpp/include/cudaforge/memory_pool.hpp:150-160). */
+cf_status cf_pool_trim(cf_pool* pool);
+
+/* Replaces MemoryPool::stats (cpp/include/cudaforge/memory_pool.hpp:162-165). */
+cf_status cf_pool_get_stats(const cf_pool* pool, cf_pool_stats* out);
+
+/* "host", "device", "device-async" or "pinned" (NULL for an unknown value).
+ * Replaces MemoryPool::backend_name (cpp/include/cudaforge/memory_pool.hpp:167). */
+const char* cf_pool_backend_name(cf_pool_backend backend);
 
 #ifdef __cplusplus
 }
