@@ -2,7 +2,7 @@
 """Benchmark of the custom-op hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--configs 1,2,3,4,5]
+                    [--configs 1,2,3,4,5,paged]
 
 Prints ONE JSON line (the driver's contract). The workload behind `value` is
 BASELINE.json's configs[1] - the memory-bound pair RMSNorm bf16 [16384, 4096]
@@ -26,7 +26,8 @@ least 0.3 s of warm-up, with cache-cold rotation: config 1
 quantise/dequantise, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
 hipBLASLt's plain GEMM through torch for context) and its adapter backward,
 config 4 the Llama block forward (tokens/s end to end, per-operator event
-times and TFLOP/s), config 5 bulk 7B quantise/dequantise aggregate GB/s, and a plain copy's
+times and TFLOP/s), `paged` the paged-attention decode at the reference's
+benchmark shapes, config 5 bulk 7B quantise/dequantise aggregate GB/s, and a plain copy's
 achieved bandwidth.
 """
 
@@ -378,6 +379,47 @@ def bench_block(torch, cf, warmup: int, runs: int) -> dict:
         "per_op_events": per_op}}
 
 
+def bench_paged(torch, cf, warmup: int, runs: int) -> dict:
+    """Paged-attention decode at the reference's benchmark shapes
+    (benchmarks/benchmark_kernels.cu:369-441: block size 16, fp32, identity
+    and reversed block tables), plus bf16 caches. Algorithmic bytes: K and V
+    once per (sequence, KV head) over the context, plus the query and output."""
+    lib = cf._lib.load()
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    block = 16
+    for seqs, heads, kv_heads, dim, ctx in ((16, 32, 32, 128, 512), (64, 32, 8, 128, 1024),
+                                            (128, 32, 8, 128, 256)):
+        per_seq = -(-ctx // block)
+        blocks = seqs * per_seq
+        for dtype, code, size in ((torch.float32, cf._lib.CF_F32, 4), (torch.bfloat16, cf._lib.CF_BF16, 2)):
+            nbytes = 2 * seqs * kv_heads * ctx * dim * size + 2 * seqs * heads * dim * size
+            sets = []
+            for _ in range(sets_for(nbytes)):
+                k = torch.randn(blocks, block, kv_heads, dim, generator=gen, device="cuda").to(dtype)
+                v = torch.randn(blocks, block, kv_heads, dim, generator=gen, device="cuda").to(dtype)
+                q = torch.randn(seqs, heads, dim, generator=gen, device="cuda").to(dtype)
+                sets.append((q, k, v, torch.empty_like(q)))
+            ctx_lens = torch.full((seqs,), ctx, dtype=torch.int32, device="cuda")
+            ws_bytes = lib.cf_paged_attention_workspace_bytes(seqs, heads, kv_heads, dim, block, per_seq)
+            ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
+            identity = torch.arange(blocks, dtype=torch.int32, device="cuda").view(seqs, per_seq)
+            for layout, table in (("contiguous", identity), ("scattered", identity.flip(0).flip(1).contiguous())):
+                launches = [lambda s=s, t=table: cf._lib.check(lib.cf_paged_attention(
+                    s[0].data_ptr(), s[1].data_ptr(), s[2].data_ptr(), t.data_ptr(), ctx_lens.data_ptr(),
+                    s[3].data_ptr(), code, seqs, heads, kv_heads, dim, block, per_seq, dim ** -0.5,
+                    ws.data_ptr() if ws_bytes else None, ws_bytes, stream)) for s in sets]
+                r = summary(time_launches(torch, launches, warmup, runs))
+                name = "f32" if size == 4 else "bf16"
+                out[f"paged_attention_{name}_{seqs}seq_{ctx}ctx_h{heads}kv{kv_heads}_{layout}"] = {
+                    **r, "bytes": nbytes, "GB/s": gbs(nbytes, r["median_ms"]),
+                    "frac_hbm": gbs(nbytes, r["median_ms"]) / PEAK_HBM_GBS}
+            del sets
+            torch.cuda.empty_cache()
+    return out
+
+
 def bench_bulk_quant(torch, cf, warmup: int) -> dict:
     """config 5: every weight of a 7B model, bf16 -> int8 + scales -> bf16."""
     gen = torch.Generator(device="cuda").manual_seed(5)
@@ -482,7 +524,8 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--quick", action="store_true", help="skip the breakdown (main step only)")
-    parser.add_argument("--configs", default="1,2,3,4,5", help="breakdown configs to run (comma-separated)")
+    parser.add_argument("--configs", default="1,2,3,4,5,paged",
+                        help="breakdown configs to run (comma-separated: 1-5, paged)")
     parser.add_argument("--detail", default="", help="also write the full result JSON here")
     args = parser.parse_args(argv)
 
@@ -512,12 +555,14 @@ def main(argv: list[str] | None = None) -> int:
     del calib
     breakdown = {}
     if not args.quick:
-        wanted = {f"config{c.strip()}" for c in args.configs.split(",") if c.strip()}
+        wanted = {c.strip() if not c.strip().isdigit() else f"config{c.strip()}"
+                  for c in args.configs.split(",") if c.strip()}
         for name, fn in (("config1", lambda: bench_quant(torch, cf, args.warmup, args.runs)),
                          ("config2", lambda: bench_rowops(torch, cf, args.warmup, args.runs)),
                          ("config3", lambda: bench_lora(torch, cf, args.warmup, args.runs)),
                          ("config4", lambda: bench_block(torch, cf, 20, args.runs)),
-                         ("config5", lambda: bench_bulk_quant(torch, cf, 3))):
+                         ("config5", lambda: bench_bulk_quant(torch, cf, 3)),
+                         ("paged", lambda: bench_paged(torch, cf, args.warmup, args.runs))):
             if name not in wanted:
                 continue
             log(f"breakdown {name}")

@@ -89,6 +89,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_gelu": (_I32, [_P, _P, _I32, _I64, _P]),
     "cf_swiglu": (_I32, [_P, _P, _P, _I32, _I64, _P]),
     "cf_copy_bytes": (_I32, [_P, _P, _I64, _P]),
+    "cf_paged_attention_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "cf_paged_attention": (
+        _I32,
+        [_P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _SZ, _P],
+    ),
     "cf_scheduler_create": (_I32, [_I64, _I32, _PP]),
     "cf_scheduler_destroy": (_I32, [_P]),
     "cf_scheduler_acquire": (_I32, [_P, _PI64, _PP]),

@@ -37,6 +37,7 @@ HIP_SOURCES = (
     "cf_lora_fused.hip",
     "cf_lora_bwd.hip",
     "cf_scheduler.hip",
+    "cf_paged_attention.hip",
 )
 
 # Per-source additions. The fused LoRA kernel accumulates in VGPRs: the

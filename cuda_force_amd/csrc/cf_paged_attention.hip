@@ -1,0 +1,643 @@
+// Attention over a paged KV cache for one decode step (one query token per
+// sequence), the operator the reference's block tables exist for
+// (cuda/include/cudaforge/paged_attention.cuh:10-61, cuda/src/paged_attention.cu).
+//
+// Layouts (the reference's): query / out [S, H, D]; k_cache / v_cache
+// [num_blocks, block_size, KVH, D]; block_tables [S, max_blocks] (uint32);
+// context_lens [S]. Token t of sequence s lives in physical block
+// block_tables[s][t / block_size] at offset t % block_size. H is a multiple of
+// KVH (grouped-query attention: head h reads KV head h / (H / KVH)). fp32
+// scores, online softmax, zeros for an empty context.
+//
+// Design on gfx950 (HBM-bound: every K and V element of a context is read once
+// per KV head, 2 * context * D * sizeof(T) bytes per (sequence, KV head)):
+//   * One workgroup (4 waves) per (sequence, KV head, group of up to 8 query
+//     heads, context split): all query heads of a GQA group are served from
+//     one pass over K and V, instead of re-reading the KV head per query head.
+//   * A token's K (and V) row is read by D/4 lanes (fp32) or D/8 lanes (bf16),
+//     16 bytes each, several tokens per wave instruction: whole rows,
+//     coalesced. Each lane keeps its 4 (8) query values and output
+//     accumulators per head; a score is a butterfly sum over the token's lanes.
+//   * The block table is held as a 64-entry window in lane registers, so a
+//     token's address costs a lane shuffle, not a dependent memory load, and
+//     the K/V loads of the next chunk of tokens are in flight while the
+//     current chunk is consumed.
+//   * Online softmax per head per token slot, rescaled once per chunk; slots,
+//     then waves, then splits are merged with the (max, sum, accumulator)
+//     rescaling rule.
+//   * Long contexts are split across workgroups so short batches still fill
+//     256 CUs; a second small kernel combines the splits (caller workspace).
+//     Without a workspace every (sequence, KV head) runs unsplit.
+// Head sizes the 16-byte lane pieces do not tile (fp32: 4 * 2^j <= 256,
+// bf16: 8 * 2^j <= 512), or unaligned tensors, take a wave-per-head kernel
+// (one token per step, lanes over the head dimension, up to 1024).
+#include <cfloat>
+#include <type_traits>
+
+#include "cf_common.hpp"
+
+namespace cf {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * kWaveSize;
+constexpr int kMaxGroup = 8;          // query heads per workgroup
+constexpr int kMinSplitTokens = 256;  // tokens per split, at least
+constexpr int kTargetWorkgroups = 1024;
+
+struct PagedArgs {
+    const void* query;
+    const void* k_cache;
+    const void* v_cache;
+    const uint32_t* tables;
+    const int32_t* context;
+    void* out;
+    float* partial;  // [S][H][splits][D + 2] (m, l, acc[D]) when splits > 1
+    int64_t heads;
+    int64_t kv_heads;
+    int64_t head_dim;
+    int64_t block_size;
+    int64_t max_blocks;
+    int64_t split_tokens;
+    int splits;
+    int head_groups;  // workgroups per KV head (ceil(group / GS))
+    float scale;
+};
+
+/// Values of T in one 16-byte load: a lane's share of a K or V row.
+template <typename T>
+constexpr int vals_per_lane() { return 16 / static_cast<int>(sizeof(T)); }
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4_t load16(const void* base, int64_t byte_offset) {
+    return *reinterpret_cast<const u32x4_t*>(static_cast<const uint8_t*>(base) + byte_offset);
+}
+
+/// The kVals values of a raw 16-byte piece, widened to fp32.
+template <typename T>
+__device__ __forceinline__ void widen(const u32x4_t& raw, float (&v)[vals_per_lane<T>()]) {
+    if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(raw[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = __uint_as_float(raw[e] << 16);
+            v[2 * e + 1] = __uint_as_float(raw[e] & 0xffff0000u);
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store_piece(T* base, int64_t index, const float (&v)[vals_per_lane<T>()]) {
+    u32x4_t raw;
+    if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) raw[e] = __float_as_uint(v[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) raw[e] = f32_to_bf16_bits(v[2 * e]) | (f32_to_bf16_bits(v[2 * e + 1]) << 16);
+    }
+    *reinterpret_cast<u32x4_t*>(base + index) = raw;
+}
+
+/// Sum over aligned groups of kLanes lanes (DPP within 16-lane rows, lane
+/// permutes across rows); every lane of a group gets the group's sum. All 64
+/// lanes must be active.
+template <int kLanes>
+__device__ __forceinline__ float lanes_sum(float v) {
+    if constexpr (kLanes == 2) {
+        v += dpp_f32<kDppQuadXor1>(v);
+    } else if constexpr (kLanes == 4 || kLanes == 8 || kLanes == 16) {
+        v = group_reduce_f32<kLanes, AddF32>(v);
+    } else if constexpr (kLanes >= 32) {
+        v = group_reduce_f32<16, AddF32>(v);
+        v += __shfl_xor(v, 16);
+        if constexpr (kLanes == 64) v += __shfl_xor(v, 32);
+    }
+    return v;
+}
+
+/// Online-softmax state of one query head over kVals output dimensions.
+template <int kVals>
+struct HeadState {
+    float m;
+    float l;
+    float acc[kVals];
+};
+
+/// Folds (m2, l2, acc2) into s: both are partial softmax sums over disjoint
+/// token sets; an empty one has m = -inf and l = 0 and contributes nothing.
+template <int kVals>
+__device__ __forceinline__ void merge_into(HeadState<kVals>& s, float m2, float l2, const float (&acc2)[kVals]) {
+    const float m = fmaxf(s.m, m2);
+    const float c1 = s.m == -INFINITY ? 0.0f : __expf(s.m - m);
+    const float c2 = m2 == -INFINITY ? 0.0f : __expf(m2 - m);
+    s.l = s.l * c1 + l2 * c2;
+#pragma unroll
+    for (int e = 0; e < kVals; ++e) s.acc[e] = s.acc[e] * c1 + acc2[e] * c2;
+    s.m = m;
+}
+
+/// kLanes = D / kVals lanes per token (kVals = 16 bytes of T), kGroup query
+/// heads per workgroup.
+template <typename T, int kLanes, int kGroup>
+__global__ __launch_bounds__(kThreads) void paged_decode_kernel(PagedArgs a) {
+    constexpr int kVals = vals_per_lane<T>();
+    constexpr int kTokensPerStep = kWaveSize / kLanes;
+    constexpr int kDim = kVals * kLanes;
+    // Token steps whose loads are issued together: fewer for larger head
+    // groups, whose per-head state already takes the registers.
+    constexpr int kStepsPerLoad = kGroup <= 2 ? 4 : (kGroup == 4 ? 2 : 1);
+    constexpr int kChunk = kStepsPerLoad * kTokensPerStep;  // tokens per load batch
+    __shared__ float lds_m[kWaves][kGroup];
+    __shared__ float lds_l[kWaves][kGroup];
+    __shared__ float lds_acc[kWaves][kGroup][kDim];
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & (kWaveSize - 1);
+    const int wave = tid / kWaveSize;
+    const int slot = lane / kLanes;   // token slot of this lane within a step
+    const int piece = lane % kLanes;  // dimensions kVals piece .. kVals piece + kVals - 1
+
+    // Workgroup -> (sequence, KV head, head group, split).
+    int64_t id = blockIdx.x;
+    const int split = static_cast<int>(id % a.splits);
+    id /= a.splits;
+    const int hgroup = static_cast<int>(id % a.head_groups);
+    id /= a.head_groups;
+    const int64_t kv_head = id % a.kv_heads;
+    const int64_t seq = id / a.kv_heads;
+
+    const int64_t group = a.heads / a.kv_heads;
+    const int64_t head0 = kv_head * group + static_cast<int64_t>(hgroup) * kGroup;
+    const int n_heads = static_cast<int>(group - static_cast<int64_t>(hgroup) * kGroup < kGroup
+                                             ? group - static_cast<int64_t>(hgroup) * kGroup
+                                             : kGroup);
+
+    float q[kGroup][kVals];
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g) {
+        const int64_t head = head0 + (g < n_heads ? g : 0);  // in range even when unused
+        const u32x4_t raw = load16(a.query, ((seq * a.heads + head) * kDim + kVals * piece) * sizeof(T));
+        widen<T>(raw, q[g]);
+#pragma unroll
+        for (int e = 0; e < kVals; ++e) q[g][e] = g < n_heads ? q[g][e] * a.scale : 0.0f;
+    }
+
+    HeadState<kVals> st[kGroup];
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g) {
+        st[g].m = -INFINITY;
+        st[g].l = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kVals; ++e) st[g].acc[e] = 0.0f;
+    }
+
+    // Tokens of this split, then of this wave (a contiguous share in whole steps).
+    const int64_t capacity = a.max_blocks * a.block_size;  // never read past the table
+    const int64_t stored = a.context[seq] > 0 ? a.context[seq] : 0;
+    const int64_t context = stored < capacity ? stored : capacity;
+    const int64_t t_lo = static_cast<int64_t>(split) * a.split_tokens;
+    const int64_t t_hi = context < t_lo + a.split_tokens ? context : t_lo + a.split_tokens;
+    const int64_t count = t_hi > t_lo ? t_hi - t_lo : 0;
+    const int64_t steps_total = (count + kTokensPerStep - 1) / kTokensPerStep;
+    const int64_t steps_per_wave = (steps_total + kWaves - 1) / kWaves;
+    const int64_t w_lo = t_lo + static_cast<int64_t>(wave) * steps_per_wave * kTokensPerStep;
+    const int64_t w_hi_raw = w_lo + steps_per_wave * kTokensPerStep;
+    const int64_t w_hi = w_hi_raw < t_hi ? w_hi_raw : t_hi;
+    const int64_t row_bytes = a.kv_heads * kDim * static_cast<int64_t>(sizeof(T));
+    const int64_t piece_bytes = (kv_head * kDim + kVals * piece) * static_cast<int64_t>(sizeof(T));
+    const uint32_t* table = a.tables + seq * a.max_blocks;
+
+    // A window of 64 block-table entries, one per lane, so the K/V addresses
+    // of a chunk need a lane shuffle rather than a dependent memory load.
+    int64_t window_base = w_lo / a.block_size;
+    auto load_window = [&](int64_t base) {
+        const int64_t entry = base + lane < a.max_blocks ? base + lane : a.max_blocks - 1;
+        return static_cast<int>(table[entry]);
+    };
+    int window = w_lo < w_hi ? load_window(window_base) : 0;
+
+    auto fetch = [&](int64_t t0, u32x4_t (&raw)[kStepsPerLoad][2]) {
+        // Uniform decisions: every lane sees the same chunk. A chunk spanning
+        // more blocks than the window holds (tiny blocks) reads the table
+        // directly.
+        const int64_t first_block = t0 / a.block_size;
+        const int64_t last_block = (t0 + kChunk - 1 < w_hi - 1 ? t0 + kChunk - 1 : w_hi - 1) / a.block_size;
+        const bool windowed = last_block - first_block < kWaveSize;
+        if (windowed && last_block - window_base >= kWaveSize) {
+            window_base = first_block;
+            window = load_window(window_base);
+        }
+#pragma unroll
+        for (int u = 0; u < kStepsPerLoad; ++u) {
+            const int64_t t = t0 + u * kTokensPerStep + slot;
+            const int64_t tc = t < w_hi ? t : w_hi - 1;  // a valid token even past the end
+            const int64_t block =
+                windowed ? static_cast<uint32_t>(__shfl(window, static_cast<int>(tc / a.block_size - window_base)))
+                         : table[tc / a.block_size];
+            const int64_t offset = (block * a.block_size + tc % a.block_size) * row_bytes + piece_bytes;
+            raw[u][0] = load16(a.k_cache, offset);
+            raw[u][1] = load16(a.v_cache, offset);
+        }
+    };
+
+    // Scores of a chunk first, then one rescale per head per chunk.
+    auto consume = [&](int64_t t0, const u32x4_t (&raw)[kStepsPerLoad][2]) {
+        float score[kGroup][kStepsPerLoad];
+#pragma unroll
+        for (int u = 0; u < kStepsPerLoad; ++u) {
+            float k[kVals];
+            widen<T>(raw[u][0], k);
+            const bool valid = t0 + u * kTokensPerStep + slot < w_hi;
+#pragma unroll
+            for (int g = 0; g < kGroup; ++g) {
+                float part = q[g][0] * k[0];
+#pragma unroll
+                for (int e = 1; e < kVals; ++e) part = fmaf(q[g][e], k[e], part);
+                part = lanes_sum<kLanes>(part);
+                score[g][u] = valid ? part : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g) {
+            float m = st[g].m;
+#pragma unroll
+            for (int u = 0; u < kStepsPerLoad; ++u) m = fmaxf(m, score[g][u]);
+            if (m == -INFINITY) continue;  // nothing valid for this slot yet
+            const float c = __expf(st[g].m - m);  // 0 when the state was empty
+            st[g].l *= c;
+#pragma unroll
+            for (int e = 0; e < kVals; ++e) st[g].acc[e] *= c;
+            st[g].m = m;
+        }
+#pragma unroll
+        for (int u = 0; u < kStepsPerLoad; ++u) {
+            float v[kVals];
+            widen<T>(raw[u][1], v);
+#pragma unroll
+            for (int g = 0; g < kGroup; ++g) {
+                const float p = score[g][u] == -INFINITY ? 0.0f : __expf(score[g][u] - st[g].m);
+                st[g].l += p;
+#pragma unroll
+                for (int e = 0; e < kVals; ++e) st[g].acc[e] = fmaf(p, v[e], st[g].acc[e]);
+            }
+        }
+    };
+
+    // Loads of the next chunk are in flight while this one is consumed.
+    u32x4_t buf_a[kStepsPerLoad][2];
+    u32x4_t buf_b[kStepsPerLoad][2];
+    int64_t t0 = w_lo;
+    if (t0 < w_hi) fetch(t0, buf_a);
+    while (t0 < w_hi) {
+        const int64_t t1 = t0 + kChunk;
+        if (t1 < w_hi) fetch(t1, buf_b);
+        consume(t0, buf_a);
+        if (t1 >= w_hi) break;
+        const int64_t t2 = t1 + kChunk;
+        if (t2 < w_hi) fetch(t2, buf_a);
+        consume(t1, buf_b);
+        t0 = t2;
+    }
+
+    // Merge the token slots of the wave (lanes piece, piece + kLanes, ...).
+#pragma unroll
+    for (int mask = kLanes; mask < kWaveSize; mask <<= 1) {
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g) {
+            const float m2 = __shfl_xor(st[g].m, mask);
+            const float l2 = __shfl_xor(st[g].l, mask);
+            float acc2[kVals];
+#pragma unroll
+            for (int e = 0; e < kVals; ++e) acc2[e] = __shfl_xor(st[g].acc[e], mask);
+            merge_into(st[g], m2, l2, acc2);
+        }
+    }
+    if (slot == 0) {
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g) {
+            if (piece == 0) {
+                lds_m[wave][g] = st[g].m;
+                lds_l[wave][g] = st[g].l;
+            }
+#pragma unroll
+            for (int e = 0; e < kVals; ++e) lds_acc[wave][g][kVals * piece + e] = st[g].acc[e];
+        }
+    }
+    __syncthreads();
+    if (wave != 0 || slot != 0) return;
+
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g) {
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+            float acc2[kVals];
+#pragma unroll
+            for (int e = 0; e < kVals; ++e) acc2[e] = lds_acc[w][g][kVals * piece + e];
+            merge_into(st[g], lds_m[w][g], lds_l[w][g], acc2);
+        }
+        if (g >= n_heads) continue;
+        const int64_t head = head0 + g;
+        if (a.splits == 1) {
+            float o[kVals];
+            const float inv = st[g].l > 0.0f ? 1.0f / st[g].l : 0.0f;
+#pragma unroll
+            for (int e = 0; e < kVals; ++e) o[e] = st[g].acc[e] * inv;
+            store_piece<T>(static_cast<T*>(a.out), (seq * a.heads + head) * kDim + kVals * piece, o);
+        } else {
+            float* part = a.partial + ((seq * a.heads + head) * a.splits + split) * (kDim + 2);
+            if (piece == 0) {
+                part[0] = st[g].m;
+                part[1] = st[g].l;
+            }
+#pragma unroll
+            for (int e = 0; e < kVals; ++e) part[2 + kVals * piece + e] = st[g].acc[e];
+        }
+    }
+}
+
+/// Combines the splits of one (sequence, head): one wave, lanes over D.
+template <typename T>
+__global__ __launch_bounds__(kWaveSize) void paged_combine_kernel(PagedArgs a) {
+    const int64_t row = blockIdx.x;  // seq * heads + head
+    const int64_t dim = a.head_dim;
+    const float* part = a.partial + row * a.splits * (dim + 2);
+    float m = -INFINITY;
+    for (int j = 0; j < a.splits; ++j) m = fmaxf(m, part[j * (dim + 2)]);
+    T* out = static_cast<T*>(a.out) + row * dim;
+    for (int64_t d = threadIdx.x; d < dim; d += kWaveSize) {
+        float num = 0.0f;
+        float den = 0.0f;
+        for (int j = 0; j < a.splits; ++j) {
+            const float* pj = part + j * (dim + 2);
+            const float c = pj[0] == -INFINITY ? 0.0f : __expf(pj[0] - m);
+            den = fmaf(pj[1], c, den);
+            num = fmaf(pj[2 + d], c, num);
+        }
+        const float v = den > 0.0f ? num / den : 0.0f;
+        if constexpr (std::is_same<T, float>::value) {
+            out[d] = v;
+        } else {
+            out[d] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+        }
+    }
+}
+
+/// Any head size up to 1024: one wave per (sequence, head), lanes over the
+/// head dimension (kPer values each), one token per step.
+template <typename T, int kPer>
+__global__ __launch_bounds__(kWaveSize) void paged_decode_wide_kernel(PagedArgs a) {
+    const int lane = static_cast<int>(threadIdx.x);
+    const int64_t row = blockIdx.x;  // seq * heads + head
+    const int64_t seq = row / a.heads;
+    const int64_t head = row % a.heads;
+    const int64_t kv_head = head / (a.heads / a.kv_heads);
+    const int64_t dim = a.head_dim;
+    const T* query = static_cast<const T*>(a.query);
+    const T* k_cache = static_cast<const T*>(a.k_cache);
+    const T* v_cache = static_cast<const T*>(a.v_cache);
+
+    auto read = [](const T* p, int64_t i) -> float {
+        if constexpr (std::is_same<T, float>::value) {
+            return p[i];
+        } else {
+            return __uint_as_float(static_cast<uint32_t>(p[i]) << 16);
+        }
+    };
+    float q[kPer];
+    float acc[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int64_t d = lane + kWaveSize * r;
+        q[r] = d < dim ? read(query, row * dim + d) * a.scale : 0.0f;
+        acc[r] = 0.0f;
+    }
+    float m = -INFINITY;
+    float l = 0.0f;
+    const int64_t capacity = a.max_blocks * a.block_size;
+    const int64_t stored = a.context[seq] > 0 ? a.context[seq] : 0;
+    const int64_t context = stored < capacity ? stored : capacity;
+    const uint32_t* table = a.tables + seq * a.max_blocks;
+    for (int64_t t = 0; t < context; ++t) {
+        const int64_t block = table[t / a.block_size];
+        const int64_t base = ((block * a.block_size + t % a.block_size) * a.kv_heads + kv_head) * dim;
+        float part = 0.0f;
+        float v[kPer];
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const int64_t d = lane + kWaveSize * r;
+            const bool in = d < dim;
+            part = fmaf(q[r], in ? read(k_cache, base + d) : 0.0f, part);
+            v[r] = in ? read(v_cache, base + d) : 0.0f;
+        }
+        const float score = wave_reduce_f32<AddF32>(part);
+        const float mn = fmaxf(m, score);
+        const float c = __expf(m - mn);
+        const float p = __expf(score - mn);
+        l = l * c + p;
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) acc[r] = fmaf(p, v[r], acc[r] * c);
+        m = mn;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int64_t d = lane + kWaveSize * r;
+        if (d >= dim) continue;
+        const float o = acc[r] * inv;
+        if constexpr (std::is_same<T, float>::value) {
+            static_cast<float*>(a.out)[row * dim + d] = o;
+        } else {
+            static_cast<uint16_t*>(a.out)[row * dim + d] = static_cast<uint16_t>(f32_to_bf16_bits(o));
+        }
+    }
+}
+
+/// Lanes per token for the streaming kernel (16 bytes per lane), or 0 when D
+/// needs the wide one.
+int lanes_for(int64_t head_dim, int64_t elem_bytes) {
+    const int64_t per_lane = 16 / elem_bytes;
+    if (head_dim % per_lane != 0) return 0;
+    const int64_t lanes = head_dim / per_lane;
+    if (lanes < 1 || lanes > kWaveSize || (lanes & (lanes - 1)) != 0) return 0;
+    return static_cast<int>(lanes);
+}
+
+int group_size_for(int64_t group) {
+    int gs = 1;
+    while (gs < group && gs < kMaxGroup) gs *= 2;
+    return gs;
+}
+
+struct Plan {
+    int lanes;
+    int gs;
+    int head_groups;
+    int splits;
+    int64_t split_tokens;
+};
+
+Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_dim,
+              int64_t block_size, int64_t max_blocks, int64_t elem_bytes, bool may_split) {
+    Plan p{};
+    p.lanes = lanes_for(head_dim, elem_bytes);
+    const int64_t group = heads / kv_heads;
+    p.gs = group_size_for(group);
+    p.head_groups = static_cast<int>((group + p.gs - 1) / p.gs);
+    const int64_t max_context = max_blocks * block_size;
+    p.splits = 1;
+    p.split_tokens = max_context > 0 ? max_context : 1;
+    if (p.lanes == 0 || !may_split) return p;
+    const int64_t base = sequences * kv_heads * p.head_groups;
+    int64_t splits = (kTargetWorkgroups + base - 1) / base;
+    const int64_t by_length = (max_context + kMinSplitTokens - 1) / kMinSplitTokens;
+    if (splits > by_length) splits = by_length;
+    if (splits < 1) splits = 1;
+    if (splits > 64) splits = 64;
+    p.splits = static_cast<int>(splits);
+    p.split_tokens = (max_context + splits - 1) / splits;
+    return p;
+}
+
+size_t partial_bytes(const Plan& p, int64_t sequences, int64_t heads, int64_t head_dim) {
+    if (p.splits <= 1) return 0;
+    return static_cast<size_t>(sequences) * static_cast<size_t>(heads) * static_cast<size_t>(p.splits) *
+           static_cast<size_t>(head_dim + 2) * sizeof(float);
+}
+
+template <typename T, int kLanes>
+void launch_streaming(const PagedArgs& args, int gs, int64_t workgroups, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(workgroups));
+    switch (gs) {
+        case 1: paged_decode_kernel<T, kLanes, 1><<<grid, kThreads, 0, stream>>>(args); break;
+        case 2: paged_decode_kernel<T, kLanes, 2><<<grid, kThreads, 0, stream>>>(args); break;
+        case 4: paged_decode_kernel<T, kLanes, 4><<<grid, kThreads, 0, stream>>>(args); break;
+        default: paged_decode_kernel<T, kLanes, 8><<<grid, kThreads, 0, stream>>>(args); break;
+    }
+}
+
+template <typename T>
+void launch_typed(const PagedArgs& args, const Plan& plan, int64_t sequences, hipStream_t stream) {
+    if (plan.lanes == 0) {
+        const int64_t per = (args.head_dim + kWaveSize - 1) / kWaveSize;
+        const dim3 grid(static_cast<unsigned>(sequences * args.heads));
+        if (per <= 1) {
+            paged_decode_wide_kernel<T, 1><<<grid, kWaveSize, 0, stream>>>(args);
+        } else if (per <= 2) {
+            paged_decode_wide_kernel<T, 2><<<grid, kWaveSize, 0, stream>>>(args);
+        } else if (per <= 4) {
+            paged_decode_wide_kernel<T, 4><<<grid, kWaveSize, 0, stream>>>(args);
+        } else if (per <= 8) {
+            paged_decode_wide_kernel<T, 8><<<grid, kWaveSize, 0, stream>>>(args);
+        } else {
+            paged_decode_wide_kernel<T, 16><<<grid, kWaveSize, 0, stream>>>(args);
+        }
+        return;
+    }
+    const int64_t workgroups = sequences * args.kv_heads * plan.head_groups * plan.splits;
+    switch (plan.lanes) {
+        case 1: launch_streaming<T, 1>(args, plan.gs, workgroups, stream); break;
+        case 2: launch_streaming<T, 2>(args, plan.gs, workgroups, stream); break;
+        case 4: launch_streaming<T, 4>(args, plan.gs, workgroups, stream); break;
+        case 8: launch_streaming<T, 8>(args, plan.gs, workgroups, stream); break;
+        case 16: launch_streaming<T, 16>(args, plan.gs, workgroups, stream); break;
+        case 32: launch_streaming<T, 32>(args, plan.gs, workgroups, stream); break;
+        default: launch_streaming<T, 64>(args, plan.gs, workgroups, stream); break;
+    }
+    if (plan.splits > 1) {
+        paged_combine_kernel<T><<<dim3(static_cast<unsigned>(sequences * args.heads)), kWaveSize, 0,
+                                  stream>>>(args);
+    }
+}
+
+}  // namespace
+}  // namespace cf
+
+extern "C" {
+
+size_t cf_paged_attention_workspace_bytes(int64_t num_sequences, int64_t num_heads, int64_t num_kv_heads,
+                                          int64_t head_dim, int64_t block_size,
+                                          int64_t max_blocks_per_sequence) {
+    if (num_sequences <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+        max_blocks_per_sequence <= 0 || num_heads % num_kv_heads != 0) {
+        return 0;
+    }
+    // The split plan depends on the element size (16-byte lane pieces): size
+    // for whichever of fp32 and bf16 needs more.
+    size_t bytes = 0;
+    for (int64_t elem : {4, 2}) {
+        const cf::Plan plan = cf::plan_for(num_sequences, num_heads, num_kv_heads, head_dim, block_size,
+                                           max_blocks_per_sequence, elem, true);
+        const size_t need = cf::partial_bytes(plan, num_sequences, num_heads, head_dim);
+        bytes = need > bytes ? need : bytes;
+    }
+    return bytes;
+}
+
+cf_status cf_paged_attention(const void* query, const void* k_cache, const void* v_cache,
+                             const uint32_t* block_tables, const int32_t* context_lens, void* out,
+                             cf_dtype dtype, int64_t num_sequences, int64_t num_heads,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                             int64_t max_blocks_per_sequence, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    if (num_sequences <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+        max_blocks_per_sequence <= 0) {
+        return CF_OK;
+    }
+    if (num_heads % num_kv_heads != 0) {
+        return cf::fail(CF_ERR_INVALID_ARGUMENT,
+                        "paged attention: num_heads %lld is not a multiple of num_kv_heads %lld",
+                        static_cast<long long>(num_heads), static_cast<long long>(num_kv_heads));
+    }
+    if (head_dim > 1024) {
+        return cf::fail(CF_ERR_INVALID_ARGUMENT, "paged attention: head_dim %lld exceeds 1024",
+                        static_cast<long long>(head_dim));
+    }
+    if (dtype != CF_F32 && dtype != CF_BF16) {
+        return cf::fail(CF_ERR_UNSUPPORTED, "paged attention: fp32 or bf16 only");
+    }
+    if (query == nullptr || k_cache == nullptr || v_cache == nullptr || block_tables == nullptr ||
+        context_lens == nullptr || out == nullptr) {
+        return cf::fail(CF_ERR_INVALID_ARGUMENT, "paged attention: null pointer");
+    }
+    const int64_t elem = dtype == CF_F32 ? 4 : 2;
+    const bool aligned = cf::host_aligned(query, 16) && cf::host_aligned(k_cache, 16) &&
+                         cf::host_aligned(v_cache, 16) && cf::host_aligned(out, 16);
+    cf::Plan plan = cf::plan_for(num_sequences, num_heads, num_kv_heads, head_dim, block_size,
+                                 max_blocks_per_sequence, elem, workspace != nullptr);
+    if (plan.lanes != 0 && !aligned) plan = cf::Plan{0, 1, 1, 1, max_blocks_per_sequence * block_size};
+    const size_t needed = cf::partial_bytes(plan, num_sequences, num_heads, head_dim);
+    if (needed > 0 && (workspace_bytes < needed || !cf::host_aligned(workspace, 16))) {
+        plan = cf::plan_for(num_sequences, num_heads, num_kv_heads, head_dim, block_size,
+                            max_blocks_per_sequence, elem, false);
+    }
+    cf::PagedArgs args;
+    args.query = query;
+    args.k_cache = k_cache;
+    args.v_cache = v_cache;
+    args.tables = block_tables;
+    args.context = context_lens;
+    args.out = out;
+    args.partial = static_cast<float*>(workspace);
+    args.heads = num_heads;
+    args.kv_heads = num_kv_heads;
+    args.head_dim = head_dim;
+    args.block_size = block_size;
+    args.max_blocks = max_blocks_per_sequence;
+    args.split_tokens = plan.split_tokens;
+    args.splits = plan.splits;
+    args.head_groups = plan.head_groups;
+    args.scale = scale;
+    auto s = static_cast<hipStream_t>(stream);
+    if (dtype == CF_F32) {
+        cf::launch_typed<float>(args, plan, num_sequences, s);
+    } else {
+        cf::launch_typed<uint16_t>(args, plan, num_sequences, s);
+    }
+    return cf::check_launch("launching paged attention", s);
+}
+
+}  // extern "C"

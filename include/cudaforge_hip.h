@@ -221,6 +221,35 @@ cf_status cf_gelu(const void* x, void* y, cf_dtype dtype, int64_t count, void* s
 cf_status cf_swiglu(const void* gate, const void* up, void* y, cf_dtype dtype, int64_t count,
                     void* stream);
 
+/* ---- paged-attention decode ---------------------------------------------- */
+
+/* Workspace bytes cf_paged_attention uses to split long contexts across
+ * workgroups (0 when it would not split). max_context is
+ * max_blocks_per_sequence * block_size. It has no counterpart in the reference,
+ * whose kernel is one workgroup per (sequence, head) with no split. */
+size_t cf_paged_attention_workspace_bytes(int64_t num_sequences, int64_t num_heads,
+                                          int64_t num_kv_heads, int64_t head_dim,
+                                          int64_t block_size, int64_t max_blocks_per_sequence);
+
+/* Attention for one decode step over a paged KV cache: query / out
+ * [num_sequences, num_heads, head_dim], k_cache / v_cache [num_blocks,
+ * block_size, num_kv_heads, head_dim], block_tables [num_sequences,
+ * max_blocks_per_sequence] (uint32), context_lens [num_sequences] (int32);
+ * dtype CF_F32 (the reference's type) or CF_BF16 for all four tensors, fp32
+ * scores and softmax. Query head h reads KV head h / (num_heads / num_kv_heads).
+ * An empty context writes zeros. Contexts longer than the table holds are read
+ * only as far as the table reaches. `workspace` may be NULL (no context split)
+ * or hold cf_paged_attention_workspace_bytes(...) bytes, 16-byte aligned.
+ * num_heads not a multiple of num_kv_heads, or head_dim > 1024, is
+ * CF_ERR_INVALID_ARGUMENT (the reference returned without launching).
+ * Replaces launch_paged_attention (cuda/include/cudaforge/paged_attention.cuh:61-65). */
+cf_status cf_paged_attention(const void* query, const void* k_cache, const void* v_cache,
+                             const uint32_t* block_tables, const int32_t* context_lens, void* out,
+                             cf_dtype dtype, int64_t num_sequences, int64_t num_heads,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                             int64_t max_blocks_per_sequence, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* ---- measurement helper ------------------------------------------------- */
 
 /* Plain device-to-device copy of `bytes` bytes through a streaming kernel

@@ -10,7 +10,8 @@ Contents:
                 restatement (cf_oracle.c, bit-exact by construction) and an
                 independent numpy restatement, cross-checked in the tests.
   floatops.py   float64 restatements of RMSNorm, softmax, the sum, the LoRA
-                linear and its adapter gradients, and the activations.
+                linear and its adapter gradients, the activations, and
+                paged-attention decode.
   ref_runner.py runs the reference's own CPU operators (cpp/src/bindings.cpp,
                 compiled by `make -C oracle ref` into oracle/_ref/) in a child
                 process, for golden vectors and the "reference" CPU baseline.
@@ -25,6 +26,7 @@ from oracle.floatops import (  # noqa: F401
     gelu_tanh,
     lora_backward,
     lora_linear,
+    paged_attention,
     rmsnorm,
     round_bf16,
     silu,

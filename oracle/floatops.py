@@ -115,3 +115,43 @@ def gelu_tanh(x: np.ndarray) -> np.ndarray:
 def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     """silu(gate) * up (python/cudaforge/ops.py:199-205)."""
     return silu(gate) * np.asarray(up, dtype=np.float64)
+
+
+def paged_attention(
+    query: np.ndarray,
+    k_cache: np.ndarray,
+    v_cache: np.ndarray,
+    block_tables: np.ndarray,
+    context_lens: np.ndarray,
+    scale: float,
+) -> np.ndarray:
+    """One decode step of attention through a paged KV cache, float64
+    (cuda/include/cudaforge/paged_attention.cuh:10-61; the host reference of
+    tests/cuda/test_paged_attention.cu:45-103 computes the same).
+
+    query [S, H, D]; k_cache / v_cache [blocks, block_size, KVH, D];
+    block_tables [S, max_blocks]; context_lens [S]. Token t of sequence s is
+    k_cache[block_tables[s, t // block_size], t % block_size]; query head h reads
+    KV head h // (H // KVH). out[s, h] = softmax(scale * q K^T) V over the first
+    context_lens[s] tokens, zeros for an empty context.
+    """
+    q = np.asarray(query, dtype=np.float64)
+    kc = np.asarray(k_cache, dtype=np.float64)
+    vc = np.asarray(v_cache, dtype=np.float64)
+    sequences, heads, dim = q.shape
+    block_size, kv_heads = kc.shape[1], kc.shape[2]
+    group = heads // kv_heads
+    out = np.zeros((sequences, heads, dim), dtype=np.float64)
+    for s in range(sequences):
+        n = int(context_lens[s])
+        if n <= 0:
+            continue
+        tokens = np.arange(n)
+        blocks = np.asarray(block_tables[s], dtype=np.int64)[tokens // block_size]
+        keys = kc[blocks, tokens % block_size]  # [n, KVH, D]
+        values = vc[blocks, tokens % block_size]
+        for h in range(heads):
+            scores = keys[:, h // group, :] @ q[s, h] * scale
+            weights = np.exp(scores - scores.max())
+            out[s, h] = weights @ values[:, h // group, :] / weights.sum()
+    return out

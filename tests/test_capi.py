@@ -105,3 +105,14 @@ def test_the_error_slot_is_per_thread(lib):
     t.join()
     assert seen["msg"] == b"no error"
     assert b"null pointer" in lib.cf_last_error()
+
+
+def test_paged_attention_argument_errors_need_no_device():
+    lib = _lib.load()
+    null = None
+    assert lib.cf_paged_attention(null, null, null, null, null, null, _lib.CF_F32, 0, 4, 2, 32, 4, 1,
+                                  1.0, null, 0, null) == _lib.CF_OK
+    assert lib.cf_paged_attention(null, null, null, null, null, null, _lib.CF_F32, 1, 3, 2, 32, 4, 1,
+                                  1.0, null, 0, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_paged_attention(null, null, null, null, null, null, _lib.CF_F32, 1, 2, 2, 2048, 4, 1,
+                                  1.0, null, 0, null) == _lib.CF_ERR_INVALID_ARGUMENT

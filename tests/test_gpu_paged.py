@@ -1,0 +1,147 @@
+"""GPU parity of the paged-attention decode kernel (cf_paged_attention)
+against the float64 oracle, through the C ABI.
+
+Cases: the reference's five parity shapes with its fp32 margin (2e-5,
+tests/cuda/test_paged_attention.cu:210-213), table following and block-order
+invariance (:216-289), an empty sequence (:291-307), grouped-query attention
+(:309-), plus what this kernel adds: bf16 caches (tolerance 1e-2 relative to
+the output scale), head sizes served by the wide kernel (80, 1024), long
+contexts split across workgroups (with and without the workspace), and a
+benchmark-sized batch.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from cuda_force_amd import _lib
+
+from .gpu_util import announce
+from .paged_util import REFERENCE_CASES, make_case
+
+pytestmark = pytest.mark.gpu
+
+FP32_MARGIN = 2e-5
+
+
+def run_gpu(case, dtype="f32", workspace=True):
+    s, h, kvh, d, bs, mb = case.dims
+    tdtype = torch.float32 if dtype == "f32" else torch.bfloat16
+    dev = torch.device("cuda:0")
+    q = torch.from_numpy(case.query).to(dev, tdtype)
+    k = torch.from_numpy(case.k_cache).to(dev, tdtype)
+    v = torch.from_numpy(case.v_cache).to(dev, tdtype)
+    tables = torch.from_numpy(case.tables.view(np.int32)).to(dev)
+    ctx = torch.from_numpy(case.context).to(dev)
+    out = torch.full_like(q, float("nan"))
+    lib = _lib.load()
+    nbytes = lib.cf_paged_attention_workspace_bytes(s, h, kvh, d, bs, mb) if workspace else 0
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    code = _lib.CF_F32 if dtype == "f32" else _lib.CF_BF16
+    _lib.check(lib.cf_paged_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), tables.data_ptr(),
+                                      ctx.data_ptr(), out.data_ptr(), code, s, h, kvh, d, bs, mb,
+                                      case.scale, ws.data_ptr() if nbytes else None, nbytes,
+                                      torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def expected_for(case, dtype="f32"):
+    if dtype == "bf16":
+        r = oracle.round_bf16
+        return oracle.paged_attention(r(case.query), r(case.k_cache), r(case.v_cache), case.tables,
+                                      case.context, case.scale)
+    return run_oracle(case)
+
+
+def run_oracle(case):
+    return oracle.paged_attention(case.query, case.k_cache, case.v_cache, case.tables, case.context,
+                                  case.scale)
+
+
+@pytest.mark.parametrize("dims", REFERENCE_CASES, ids=str)
+def test_reference_cases_fp32(dims):
+    announce(f"paged attention fp32 {dims}")
+    case = make_case(*dims, seed=dims[3] * 7 + dims[4])
+    np.testing.assert_allclose(run_gpu(case), run_oracle(case), rtol=0, atol=FP32_MARGIN)
+
+
+def test_follows_the_table_and_ignores_block_order():
+    announce("paged attention: table following / block-order invariance")
+    case = make_case(1, 1, 1, 32, 4, [8], seed=3)
+    base = run_gpu(case)
+    swapped = make_case(1, 1, 1, 32, 4, [8], seed=3)
+    swapped.tables[0, [0, 1]] = swapped.tables[0, [1, 0]]
+    np.testing.assert_allclose(run_gpu(swapped), base, rtol=0, atol=1e-6)
+    repointed = make_case(1, 1, 1, 32, 4, [8], seed=3)
+    used = set(repointed.tables[0].tolist())
+    repointed.tables[0, 0] = next(b for b in range(repointed.k_cache.shape[0]) if b not in used)
+    assert np.abs(run_gpu(repointed) - base).max() > 1e-3
+    np.testing.assert_allclose(run_gpu(repointed), run_oracle(repointed), rtol=0, atol=FP32_MARGIN)
+
+
+def test_empty_sequence_and_gqa():
+    announce("paged attention: empty sequence, GQA")
+    case = make_case(2, 2, 2, 32, 4, [0, 6], seed=11)
+    got = run_gpu(case)
+    assert np.all(got[0] == 0.0)
+    np.testing.assert_allclose(got, run_oracle(case), rtol=0, atol=FP32_MARGIN)
+    gqa = make_case(2, 8, 2, 64, 8, [20, 9], seed=5)
+    np.testing.assert_allclose(run_gpu(gqa), run_oracle(gqa), rtol=0, atol=FP32_MARGIN)
+    big_group = make_case(2, 32, 2, 128, 16, [70, 33], seed=6)  # 16 heads per KV head: 2 workgroups
+    np.testing.assert_allclose(run_gpu(big_group), run_oracle(big_group), rtol=0, atol=FP32_MARGIN)
+
+
+@pytest.mark.parametrize("dims", [(2, 4, 2, 80, 16, [40, 3]), (1, 2, 1, 1024, 8, [19]),
+                                  (2, 2, 2, 8, 4, [13, 4]), (1, 4, 4, 256, 16, [50])], ids=str)
+def test_other_head_sizes(dims):
+    announce(f"paged attention head size {dims[3]}")
+    case = make_case(*dims, seed=dims[3])
+    np.testing.assert_allclose(run_gpu(case), run_oracle(case), rtol=0, atol=FP32_MARGIN)
+
+
+@pytest.mark.parametrize("workspace", [True, False], ids=["split", "unsplit"])
+def test_long_contexts(workspace):
+    announce(f"paged attention long context, workspace={workspace}")
+    case = make_case(2, 8, 2, 128, 16, [3000, 1500], seed=21)
+    s, h, kvh, d, bs, mb = case.dims
+    if workspace:
+        assert _lib.load().cf_paged_attention_workspace_bytes(s, h, kvh, d, bs, mb) > 0
+    np.testing.assert_allclose(run_gpu(case, workspace=workspace), run_oracle(case), rtol=0,
+                               atol=FP32_MARGIN)
+
+
+def test_bf16_cache():
+    announce("paged attention bf16")
+    case = make_case(3, 8, 2, 128, 16, [200, 17, 1], seed=8)
+    got = run_gpu(case, "bf16")
+    expected = expected_for(case, "bf16")
+    scale = np.abs(expected).max()
+    assert np.abs(got - expected).max() <= 1e-2 * scale
+
+
+def test_benchmark_sized_batch():
+    announce("paged attention 64 seq x 1024 ctx, 32 heads / 8 kv, d128")
+    case = make_case(64, 32, 8, 128, 16, [1024] * 64, seed=9, spare=0)
+    got = run_gpu(case)
+    sample = [0, 17, 63]
+    sub = make_case(64, 32, 8, 128, 16, [1024] * 64, seed=9, spare=0)
+    expected = oracle.paged_attention(sub.query[sample], sub.k_cache, sub.v_cache, sub.tables[sample],
+                                      sub.context[sample], sub.scale)
+    np.testing.assert_allclose(got[sample], expected, rtol=0, atol=FP32_MARGIN)
+    assert np.isfinite(got).all()
+
+
+@pytest.mark.parametrize("block_size", [1, 2, 64], ids=lambda b: f"block{b}")
+def test_block_sizes_around_the_table_window(block_size):
+    announce(f"paged attention block size {block_size}")
+    # 8-value head (fp32: 2 lanes, 32 tokens per step) with 1-token blocks: a
+    # chunk spans more blocks than the 64-entry window; 300 tokens also cross
+    # window reloads.
+    for dims in ((2, 2, 1, 8, block_size, [300, 77]), (1, 4, 2, 128, block_size, [300])):
+        case = make_case(*dims, seed=block_size)
+        np.testing.assert_allclose(run_gpu(case), run_oracle(case), rtol=0, atol=FP32_MARGIN)
+        np.testing.assert_allclose(run_gpu(case, workspace=False), run_oracle(case), rtol=0, atol=FP32_MARGIN)
