@@ -2,7 +2,7 @@
 """Benchmark of the custom-op hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--configs 1,2,3,4,5,paged]
+                    [--configs 1,2,3,4,5,paged,tensorcore]
 
 Prints ONE JSON line (the driver's contract). The workload behind `value` is
 BASELINE.json's configs[1] - the memory-bound pair RMSNorm bf16 [16384, 4096]
@@ -27,7 +27,7 @@ quantise/dequantise, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
 hipBLASLt's plain GEMM through torch for context) and its adapter backward,
 config 4 the Llama block forward (tokens/s end to end, per-operator event
 times and TFLOP/s), `paged` the paged-attention decode at the reference's
-benchmark shapes, config 5 bulk 7B quantise/dequantise aggregate GB/s, and a plain copy's
+benchmark shapes, `tensorcore` the fp32 matmul on the bf16 MFMA units, config 5 bulk 7B quantise/dequantise aggregate GB/s, and a plain copy's
 achieved bandwidth.
 """
 
@@ -420,6 +420,33 @@ def bench_paged(torch, cf, warmup: int, runs: int) -> dict:
     return out
 
 
+def bench_tensor_core(torch, cf, warmup: int, runs: int) -> dict:
+    """fp32 matmul on the bf16 MFMA units (hi/lo split, three bf16 products in
+    one GEMM) at the reference benchmark's largest square, and 4096^3; FLOP/s
+    counts the fp32 product (2 m n k), with torch's fp32 matmul for context."""
+    lib = cf._lib.load()
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for n in (1024, 4096):
+        a = torch.randn(n, n, generator=gen, device="cuda")
+        b = torch.randn(n, n, generator=gen, device="cuda")
+        c = torch.empty(n, n, device="cuda")
+        nbytes = lib.cf_matmul_tensor_core_workspace_bytes(n, n, n)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+
+        def tc():
+            cf._lib.check(lib.cf_matmul_tensor_core(a.data_ptr(), b.data_ptr(), c.data_ptr(), n, n, n,
+                                                    ws.data_ptr(), nbytes, stream))
+
+        r = summary(time_launches(torch, [tc], warmup, runs))
+        flops = 2 * n ** 3
+        out[f"tensor_core_matmul_f32_{n}"] = {**r, "TFLOP/s": flops / (r["median_ms"] * 1e-3) / 1e12}
+        r = summary(time_launches(torch, [lambda: torch.matmul(a, b, out=c)], warmup, runs))
+        out[f"torch_matmul_f32_{n}_context"] = {**r, "TFLOP/s": flops / (r["median_ms"] * 1e-3) / 1e12}
+    return out
+
+
 def bench_bulk_quant(torch, cf, warmup: int) -> dict:
     """config 5: every weight of a 7B model, bf16 -> int8 + scales -> bf16."""
     gen = torch.Generator(device="cuda").manual_seed(5)
@@ -524,8 +551,8 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--quick", action="store_true", help="skip the breakdown (main step only)")
-    parser.add_argument("--configs", default="1,2,3,4,5,paged",
-                        help="breakdown configs to run (comma-separated: 1-5, paged)")
+    parser.add_argument("--configs", default="1,2,3,4,5,paged,tensorcore",
+                        help="breakdown configs to run (comma-separated: 1-5, paged, tensorcore)")
     parser.add_argument("--detail", default="", help="also write the full result JSON here")
     args = parser.parse_args(argv)
 
@@ -562,7 +589,8 @@ def main(argv: list[str] | None = None) -> int:
                          ("config3", lambda: bench_lora(torch, cf, args.warmup, args.runs)),
                          ("config4", lambda: bench_block(torch, cf, 20, args.runs)),
                          ("config5", lambda: bench_bulk_quant(torch, cf, 3)),
-                         ("paged", lambda: bench_paged(torch, cf, args.warmup, args.runs))):
+                         ("paged", lambda: bench_paged(torch, cf, args.warmup, args.runs)),
+                         ("tensorcore", lambda: bench_tensor_core(torch, cf, 20, args.runs))):
             if name not in wanted:
                 continue
             log(f"breakdown {name}")

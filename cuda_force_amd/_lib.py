@@ -89,6 +89,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_gelu": (_I32, [_P, _P, _I32, _I64, _P]),
     "cf_swiglu": (_I32, [_P, _P, _P, _I32, _I64, _P]),
     "cf_copy_bytes": (_I32, [_P, _P, _I64, _P]),
+    "cf_tensor_cores_available": (_I32, []),
+    "cf_matmul_tensor_core_shape_supported": (_I32, [_I64, _I64, _I64]),
+    "cf_matmul_tensor_core_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "cf_matmul_tensor_core": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "cf_paged_attention_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "cf_paged_attention": (
         _I32,

@@ -38,6 +38,7 @@ HIP_SOURCES = (
     "cf_lora_bwd.hip",
     "cf_scheduler.hip",
     "cf_paged_attention.hip",
+    "cf_tensor_core.hip",
 )
 
 # Per-source additions. The fused LoRA kernel accumulates in VGPRs: the

@@ -33,7 +33,8 @@
 //     exchanged through LDS, bf16(scale * b) is read transposed from an LDS
 //     copy of b loaded at kernel start, and one v_mfma_f32_16x16x16_bf16 per
 //     16x16 block accumulates the adapter term into the base accumulators.
-//     The tile is rounded to bf16 and written with 8-byte stores.
+//     The tile is rounded to bf16 and written with 8-byte stores (or kept
+//     in fp32, 16-byte stores, for the fp32-output matmul).
 //   * Workgroup ids are remapped so the tiles dispatched to one XCD (ids are
 //     dealt round-robin over the 8 XCDs) form a band of 4 row-tiles sharing x
 //     row-panels in that XCD's L2.
@@ -195,6 +196,7 @@ struct FusedArgs {
     const uint16_t* a;
     const uint16_t* b;
     uint16_t* y;
+    float* y32;  // fp32 output (kOutF32) instead of y
     float* xa_out;
     int64_t M;
     int64_t N;
@@ -213,7 +215,7 @@ struct XFrags {
     bf16x8_t a;
 };
 
-template <bool kAdapter>
+template <bool kAdapter, bool kOutF32>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lora_fused_bf16_kernel(FusedArgs args) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
@@ -533,7 +535,9 @@ void lora_fused_bf16_kernel(FusedArgs args) {
 #pragma unroll
         for (int jb = 0; jb < 8; ++jb) {
             const int64_t col = n0 + wn * 128 + 16 * jb + 4 * g;
-            if (col < N) {
+            if (kOutF32 && col < N) {
+                *reinterpret_cast<f32x4_t*>(args.y32 + row * N + col) = acc[jb][i];
+            } else if (col < N) {
                 uint2 packed;
                 packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
                 packed.y = f32_to_bf16_bits(acc[jb][i][2]) | (f32_to_bf16_bits(acc[jb][i][3]) << 16);
@@ -567,6 +571,7 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
     args.a = static_cast<const uint16_t*>(a);
     args.b = static_cast<const uint16_t*>(b);
     args.y = static_cast<uint16_t*>(y);
+    args.y32 = nullptr;
     args.xa_out = xa_out;
     args.M = M;
     args.N = N;
@@ -577,11 +582,27 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
     args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
     const int grid = args.tiles_m * args.tiles_n;
     if (rank > 0) {
-        lora_fused_bf16_kernel<true><<<grid, kThreads, 0, stream>>>(args);
+        lora_fused_bf16_kernel<true, false><<<grid, kThreads, 0, stream>>>(args);
     } else {
-        lora_fused_bf16_kernel<false><<<grid, kThreads, 0, stream>>>(args);
+        lora_fused_bf16_kernel<false, false><<<grid, kThreads, 0, stream>>>(args);
     }
     return check_launch("launching the fused bf16 LoRA kernel", stream);
+}
+
+cf_status launch_matmul_bf16_f32out(const void* x, const void* w, float* y, int64_t M, int64_t N,
+                                    int64_t K, hipStream_t stream) {
+    FusedArgs args{};
+    args.x = static_cast<const uint16_t*>(x);
+    args.w = static_cast<const uint16_t*>(w);
+    args.y32 = y;
+    args.M = M;
+    args.N = N;
+    args.K = K;
+    args.tiles_m = static_cast<int>(ceil_div<int64_t>(M, kBM));
+    args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
+    const int grid = args.tiles_m * args.tiles_n;
+    lora_fused_bf16_kernel<false, true><<<grid, kThreads, 0, stream>>>(args);
+    return check_launch("launching the bf16 MFMA matmul (fp32 output)", stream);
 }
 
 }  // namespace cf

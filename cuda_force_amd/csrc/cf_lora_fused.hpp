@@ -18,4 +18,10 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
                             float* xa_out, int64_t M, int64_t N, int64_t K, int64_t rank,
                             float scale, hipStream_t stream);
 
+/// y (fp32) = x @ w for bf16 x [M, K] and w [K, N] on the same kernel
+/// (rank 0, fp32 stores); same eligibility as lora_fused_eligible with rank 0
+/// and a 16-byte aligned y.
+cf_status launch_matmul_bf16_f32out(const void* x, const void* w, float* y, int64_t M, int64_t N,
+                                    int64_t K, hipStream_t stream);
+
 }  // namespace cf

@@ -221,6 +221,33 @@ cf_status cf_gelu(const void* x, void* y, cf_dtype dtype, int64_t count, void* s
 cf_status cf_swiglu(const void* gate, const void* up, void* y, cf_dtype dtype, int64_t count,
                     void* stream);
 
+/* ---- fp32 matmul on the matrix cores --------------------------------------- */
+
+/* 1: this build's fp32 matmul runs on the bf16 MFMA units (every gfx950 device
+ * has them). Replaces tensor_cores_available
+ * (cuda/include/cudaforge/tensor_core_matmul.cuh:44). */
+int cf_tensor_cores_available(void);
+
+/* 1 when cf_matmul_tensor_core takes this shape: m, k >= 1 and n a positive
+ * multiple of 8 (the reference also required m, n multiples of 16 and k of 8).
+ * Replaces tensor_core_shape_supported
+ * (cuda/include/cudaforge/tensor_core_matmul.cuh:51). */
+int cf_matmul_tensor_core_shape_supported(int64_t m, int64_t n, int64_t k);
+
+/* Workspace for the bf16 operand parts (0 for an unsupported shape). It has
+ * no counterpart in the reference, whose TF32 kernel read fp32 directly. */
+size_t cf_matmul_tensor_core_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+/* c[m, n] = a[m, k] b[k, n], row-major fp32, on the bf16 MFMA units: each
+ * operand is split into bf16 high and low parts and the three significant
+ * cross products run as one bf16 GEMM with fp32 accumulation (about 16
+ * significant bits per product; the reference's TF32 kept 11). b, c and the
+ * workspace 16-byte aligned. An unsupported shape is CF_ERR_UNSUPPORTED
+ * without launching, where the reference returned false.
+ * Replaces launch_matmul_tensor_core (cuda/include/cudaforge/tensor_core_matmul.cuh:40-41). */
+cf_status cf_matmul_tensor_core(const float* a, const float* b, float* c, int64_t m, int64_t n,
+                                int64_t k, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- paged-attention decode ---------------------------------------------- */
 
 /* Workspace bytes cf_paged_attention uses to split long contexts across

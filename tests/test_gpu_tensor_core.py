@@ -1,0 +1,113 @@
+"""GPU tests of the fp32 matmul on the bf16 MFMA units (cf_matmul_tensor_core).
+
+The reference's cases (tests/cuda/test_tensor_core_matmul.cu:80-151): its four
+shapes against a float64 host product with its TF32 tolerance (relative 2e-2
+plus an absolute 3e-3 sqrt(k)), refusal of shapes the kernel cannot tile, and
+agreement with the CUDA-core fp32 path without being bit-identical to it. The
+hi/lo bf16 split is checked to a much tighter bound than TF32 allows (1e-4
+sqrt(k) absolute on N(0, 1) inputs, from about 2^-16 relative error per
+product), on ragged shapes the reference refused, and at 4096^3.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cuda_force_amd import _lib
+
+from .gpu_util import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def tensor_core(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    lib = _lib.load()
+    m, k = a.shape
+    n = b.shape[1]
+    c = torch.full((m, n), float("nan"), device=a.device)
+    nbytes = lib.cf_matmul_tensor_core_workspace_bytes(m, n, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device)
+    _lib.check(lib.cf_matmul_tensor_core(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, ws.data_ptr(),
+                                         nbytes, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return c
+
+
+def reference_product(a: torch.Tensor, b: torch.Tensor) -> np.ndarray:
+    return a.double().cpu().numpy() @ b.double().cpu().numpy()
+
+
+@pytest.mark.parametrize("shape", [(16, 16, 8), (64, 32, 16), (128, 128, 64), (256, 64, 128)], ids=str)
+def test_reference_shapes_within_tf32_tolerance_and_far_tighter(shape):
+    m, n, k = shape
+    announce(f"tensor-core matmul {shape}")
+    gen = torch.Generator(device="cuda").manual_seed(m + k)
+    a = torch.randn(m, k, generator=gen, device="cuda")
+    b = torch.randn(k, n, generator=gen, device="cuda")
+    got = tensor_core(a, b).cpu().numpy()
+    expected = reference_product(a, b)
+    tf32_bound = 2e-2 * np.abs(expected) + 3e-3 * math.sqrt(k)
+    assert np.all(np.abs(got - expected) <= tf32_bound)
+    assert np.abs(got - expected).max() <= 1e-4 * math.sqrt(k)
+
+
+@pytest.mark.parametrize("shape", [(15, 16, 8), (100, 24, 12), (257, 520, 70), (1, 8, 1)], ids=str)
+def test_ragged_shapes(shape):
+    m, n, k = shape
+    announce(f"tensor-core matmul ragged {shape}")
+    gen = torch.Generator(device="cuda").manual_seed(n)
+    a = torch.randn(m, k, generator=gen, device="cuda")
+    b = torch.randn(k, n, generator=gen, device="cuda")
+    got = tensor_core(a, b).cpu().numpy()
+    assert np.abs(got - reference_product(a, b)).max() <= 1e-4 * math.sqrt(k)
+
+
+def test_refuses_shapes_it_cannot_tile():
+    lib = _lib.load()
+    assert lib.cf_tensor_cores_available() == 1
+    assert lib.cf_matmul_tensor_core_shape_supported(16, 17, 8) == 0
+    assert lib.cf_matmul_tensor_core_shape_supported(0, 16, 8) == 0
+    assert lib.cf_matmul_tensor_core_shape_supported(16, 16, 0) == 0
+    assert lib.cf_matmul_tensor_core_shape_supported(16, 16, 8) == 1
+    assert lib.cf_matmul_tensor_core_shape_supported(256, 512, 128) == 1
+    assert lib.cf_matmul_tensor_core_workspace_bytes(16, 17, 8) == 0
+    a = torch.randn(16, 8, device="cuda")
+    b = torch.randn(8, 17, device="cuda")
+    c = torch.zeros(16, 17, device="cuda")
+    status = lib.cf_matmul_tensor_core(a.data_ptr(), b.data_ptr(), c.data_ptr(), 16, 17, 8, None, 0,
+                                       torch.cuda.current_stream().cuda_stream)
+    assert status == _lib.CF_ERR_UNSUPPORTED
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(c) == 0  # nothing launched
+
+
+def test_agrees_with_the_fp32_core_path_without_being_identical():
+    announce("tensor-core matmul vs the fp32 tiled path")
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    a = torch.randn(128, 64, generator=gen, device="cuda")
+    b = torch.randn(64, 128, generator=gen, device="cuda")
+    tc = tensor_core(a, b)
+    tiled = torch.empty(128, 128, device="cuda")
+    lib = _lib.load()
+    _lib.check(lib.cf_matmul(a.data_ptr(), b.data_ptr(), tiled.data_ptr(), _lib.CF_F32, 128, 128, 64,
+                             torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    diff = (tc - tiled).abs()
+    assert diff.max().item() <= 2e-2 * tiled.abs().max().item() + 3e-3 * 8
+    assert diff.max().item() > 1e-7  # a different arithmetic path, not a copy of the fp32 one
+
+
+def test_large_square():
+    announce("tensor-core matmul 4096^3")
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    n = 4096
+    a = torch.randn(n, n, generator=gen, device="cuda")
+    b = torch.randn(n, n, generator=gen, device="cuda")
+    got = tensor_core(a, b)
+    rows = [0, 1777, 4095]
+    expected = a[rows].double() @ b.double()
+    assert (got[rows].double() - expected).abs().max().item() <= 1e-4 * math.sqrt(n)
