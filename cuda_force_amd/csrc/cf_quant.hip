@@ -154,7 +154,10 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
         }
 
         if constexpr (kMode == 0) {
-            if (part == 0) __builtin_nontemporal_store(b.s, scales + block);
+            // A plain store: the 4-byte scales of neighbouring waves merge into
+            // whole lines in L2 (a non-temporal store of each costs ~7% of the
+            // kernel). The codes and inputs stay non-temporal.
+            if (part == 0) scales[block] = b.s;
             if (kFull || (kVec && e + kPer <= count)) {
                 uint32_t w[kPer / 4];
 #pragma unroll
