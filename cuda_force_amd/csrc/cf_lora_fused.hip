@@ -13,7 +13,8 @@
 //     C^T = w^T x^T: w supplies the A operand, x the B operand, so each lane
 //     ends up holding 4 consecutive output columns of one row.
 //   * Operands travel HBM -> LDS by buffer loads with the LDS destination
-//     (`buffer_load_dwordx4 ... lds`): no registers are spent on prefetch,
+//     (`buffer_load_dwordx4 ... lds`), issued by waves 0-3 only (one per
+//     SIMD): no registers are spent on prefetch,
 //     rows past M and columns past N arrive as zeros through the buffer range
 //     check. K-step 32, four LDS stages, prefetch distance three: the loads for
 //     step j + 3 are issued while step j + 1 is read into fragment registers
@@ -239,34 +240,39 @@ void lora_fused_bf16_kernel(FusedArgs args) {
 
     // ---- HBM -> LDS roles (each load instruction fills 1 KiB of LDS, lane l
     // at byte 16 l; the global side is permuted to realise the swizzles) ----
+    // Only waves 0-3 (one per SIMD) issue DMA, each for its own share and for
+    // wave + 4's: a wave that stalls on a full address queue then always has
+    // a SIMD-mate that keeps issuing MFMAs. `vw` below is the wave whose
+    // share a piece fills.
     // x travels two K-steps at a time, as whole 128-byte lines of each row
     // (a 64-byte piece per K-step would make every line two L1 requests):
-    // wave covers rows 32 wave .. +31, 8 rows per load; lane -> row
-    // 32 wave + 8 i + l/8, physical chunk l%8.
+    // share vw covers rows 32 vw .. +31, 8 rows per load; lane -> row
+    // 32 vw + 8 i + l/8, physical chunk l%8.
     const int64_t rows_here = M - m0 < kBM ? M - m0 : kBM;
     const i32x4_t xbuf = raw_buffer_words(args.x + m0 * K, static_cast<uint32_t>(rows_here * K * 2));
-    uint32_t x_dma[4];
+    uint32_t x_dma[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = 32 * wave + 8 * i + (lane >> 3);
+    for (int i = 0; i < 8; ++i) {
+        const int vw = (wave & 3) + 4 * (i >> 2);
+        const int row = 32 * vw + 8 * (i & 3) + (lane >> 3);
         const int chunk = (lane & 7) ^ x_swizzle(row);
         x_dma[i] = static_cast<uint32_t>((row * K + chunk * 8) * 2);
     }
-    // w: wave covers k-row pairs q = 2 wave + i; lane -> row 2q + l/32,
+    // w: share vw covers k-row pairs q = 2 vw + i; lane -> row 2q + l/32,
     // physical chunk l%32. Columns past N read as zero.
     const i32x4_t wbuf = raw_buffer_words(args.w, static_cast<uint32_t>(K * N * 2));
-    uint32_t w_dma[2];
+    uint32_t w_dma[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int row = 2 * (wave * 2 + i) + (lane >> 5);
+    for (int i = 0; i < 4; ++i) {
+        const int vw = (wave & 3) + 4 * (i >> 1);
+        const int row = 2 * (vw * 2 + (i & 1)) + (lane >> 5);
         const int64_t col = n0 + 8 * ((lane & 31) ^ w_swizzle(row));
         w_dma[i] = col < N ? static_cast<uint32_t>((row * N + col) * 2) : kOutOfRange;
     }
-    // a: 4-byte pieces (two adapter columns; the rank is even); wave fills
-    // bytes 256 (wave % 4) + 4 l, i.e. rows 8 (wave % 4) .. +7 in the
-    // a_offset layout (an involution within the 256 bytes). Waves 4..7
-    // repeat waves 0..3 (the same bytes to the same place), which keeps the
-    // loop free of branches. Columns past the rank read as zero.
+    // a: 4-byte pieces (two adapter columns; the rank is even); issuing wave
+    // w fills bytes 256 w + 4 l, i.e. rows 8 w .. +7 in the a_offset layout
+    // (an involution within the 256 bytes). Columns past the rank read as
+    // zero.
     const i32x4_t abuf = raw_buffer_words(args.a, static_cast<uint32_t>(kAdapter ? K * rank * 2 : 0));
     uint32_t a_dma = kOutOfRange;
     if (kAdapter) {
@@ -279,15 +285,17 @@ void lora_fused_bf16_kernel(FusedArgs args) {
 
     // LDS byte address of the tile storage (the DMA takes it in M0).
     const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)lds));
-    // DMA instructions: piece 0, 1 of K-step kt are w, piece 2 is a (adapter
-    // only), into the stage ring; piece i of x pair p (K-steps 2p, 2p + 1)
-    // goes into x slot p % 2. The K-loop spreads them over a step's MFMAs
-    // rather than issuing them in one burst after the barrier.
+    // DMA instructions of an issuing wave: pieces 0-3 of K-step kt are w
+    // (shares wave and wave + 4), piece 4 is a (adapter only), into the stage
+    // ring; pieces 0-7 of x pair p (K-steps 2p, 2p + 1) go into x slot p % 2.
+    // The K-loop spreads them over a step's MFMAs rather than issuing them in
+    // one burst after the barrier.
     auto issue_w = [&](int64_t kt, int piece) {
         const uint32_t stage = lds_addr + kOffW + static_cast<uint32_t>(kt % kStages) * kStage;
         const int64_t k0 = kt * kBK;
-        if (piece < 2) {
-            dma16(wbuf, stage + (wave * 2 + piece) * 1024, w_dma[piece],
+        if (piece < 4) {
+            const int vw = (wave & 3) + 4 * (piece >> 1);
+            dma16(wbuf, stage + (vw * 2 + (piece & 1)) * 1024, w_dma[piece],
                   static_cast<uint32_t>(k0 * N * 2));
         } else if (kAdapter) {
             dma4(abuf, stage + kTileW + (wave & 3) * 256, a_dma,
@@ -296,11 +304,12 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     };
     auto issue_x = [&](int64_t pair, int piece) {
         const uint32_t slot = lds_addr + static_cast<uint32_t>(pair % kXSlots) * kXPair;
-        dma16(xbuf, slot + wave * 4096 + piece * 1024, x_dma[piece],
+        const int vw = (wave & 3) + 4 * (piece >> 2);
+        dma16(xbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
               static_cast<uint32_t>(pair * 4 * kBK));
     };
-    constexpr int kWLoads = kAdapter ? 3 : 2;  // w (+ a) DMA instructions per K-step per wave
-    constexpr int kXLoads = 4;                 // x DMA instructions per pair of K-steps per wave
+    constexpr int kWLoads = kAdapter ? 5 : 4;  // w (+ a) DMA per K-step per issuing wave
+    constexpr int kXLoads = 8;                 // x DMA per pair of K-steps per issuing wave
 
     // ---- LDS -> register fragment roles ----
     // x (B operand): fragment i holds row block rb(i) = (i + 2 wn) % 4 of the
@@ -361,7 +370,8 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     bf16x8_t wf[8];
     // On step kt the DMA goes out for K-step kt + 3 (w, a) and, on odd steps,
     // for x pair (kt + 3) / 2, whose slot the barrier of step kt has freed.
-    auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next, auto issue, auto odd) {
+    auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next, auto issue, auto odd,
+                        auto issuer) {
         if (kAdapter) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
@@ -376,16 +386,9 @@ void lora_fused_bf16_kernel(FusedArgs args) {
                     __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[jb], f.x[i], acc[jb][i], 0, 0, 0);
             }
             if constexpr (decltype(read_next)::value) wf[jb] = read_w(next_kt, jb);
-            if constexpr (decltype(issue)::value) {
-                if constexpr (decltype(odd)::value) {
-                    if (jb < kXLoads) {
-                        issue_x((next_kt + 2) >> 1, jb);
-                    } else if (jb < kXLoads + kWLoads) {
-                        issue_w(next_kt + 2, jb - kXLoads);
-                    }
-                } else {
-                    if (jb < kWLoads) issue_w(next_kt + 2, jb);
-                }
+            if constexpr (decltype(issue)::value && decltype(issuer)::value) {
+                if constexpr (decltype(odd)::value) issue_x((next_kt + 2) >> 1, jb);
+                if (jb < kWLoads) issue_w(next_kt + 2, jb);
             }
         }
     };
@@ -399,6 +402,10 @@ void lora_fused_bf16_kernel(FusedArgs args) {
             row < rank && col < N ? static_cast<uint32_t>((row * N + col) * 2) : kOutOfRange;
         dma16(bbuf, lds_addr + kOffB + wave * 1024, off, 0);
     }
+    // The K-loop, instantiated for issuing (waves 0-3) and non-issuing waves;
+    // the latter wait for nothing but the barriers (their vmcnt waits find
+    // no DMA of their own in flight).
+    auto run = [&](auto issuer) {
     const int64_t k_tiles = K / kBK;  // even, >= 2
     auto issue_w_all = [&](int64_t kt) {
 #pragma unroll
@@ -409,15 +416,17 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         for (int piece = 0; piece < kXLoads; ++piece) issue_x(pair, piece);
     };
     // Issue order as if steps -2 and -1 had run: x pair 0, w 0, w 1 | x pair 1, w 2.
-    issue_x_all(0);
-    issue_w_all(0);
-    issue_w_all(1);
-    if (k_tiles > 2) {
-        issue_x_all(1);
-        issue_w_all(2);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kWLoads + kXLoads));
-    } else {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
+    if constexpr (decltype(issuer)::value) {
+        issue_x_all(0);
+        issue_w_all(0);
+        issue_w_all(1);
+        if (k_tiles > 2) {
+            issue_x_all(1);
+            issue_w_all(2);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kWLoads + kXLoads));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
+        }
     }
     bare_barrier();  // step 0 in LDS
 
@@ -454,7 +463,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
             bare_barrier();
             read_x(nxt, kt + 1);
         }
-        multiply(cur, kt + 1, read, issue, odd);
+        multiply(cur, kt + 1, read, issue, odd, issuer);
     };
     int64_t kt = 0;
     for (; kt + 4 < k_tiles; kt += 2) {
@@ -468,6 +477,12 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     }
     step(kt, f0, f1, no{}, yes{}, yes{}, no{});
     step(kt + 1, f1, f0, no{}, no{}, no{}, yes{});
+    };
+    if (wave < 4) {
+        run(std::true_type{});
+    } else {
+        run(std::false_type{});
+    }
 
     // ---- epilogue ----
     if (kAdapter) {
