@@ -283,6 +283,37 @@ def bench_rowops(torch, cf, warmup: int, runs: int) -> dict:
         out[label] = {**r, "bytes": sb, "GB/s": gbs(sb, r["median_ms"]),
                       "frac_hbm": gbs(sb, r["median_ms"]) / PEAK_HBM_GBS}
         del sets, launches
+    # The row's neighbours in the same family: fused residual add +
+    # RMSNorm at config 2's shape, and the activations over a Llama-7B MLP
+    # activation ([16384, 11008]).
+    res_bytes = 4 * rows * cols * 2
+    sets = [tuple(torch.randn(rows, cols, generator=gen, device="cuda").to(torch.bfloat16) for _ in range(4))
+            for _ in range(sets_for(res_bytes))]
+    launches = [lambda s=s: cf._lib.check(lib.cf_fused_residual_rmsnorm(
+        s[0].data_ptr(), s[1].data_ptr(), w.data_ptr(), s[2].data_ptr(), s[3].data_ptr(), cf._lib.CF_BF16,
+        rows, cols, 1e-6, torch.cuda.current_stream().cuda_stream)) for s in sets]
+    r = summary(time_launches(torch, launches, warmup, runs))
+    out["fused_residual_rmsnorm_bf16_16384x4096"] = {**r, "bytes": res_bytes, "GB/s": gbs(res_bytes, r["median_ms"]),
+                                                     "frac_hbm": gbs(res_bytes, r["median_ms"]) / PEAK_HBM_GBS}
+    del sets, launches
+    n = 16384 * 11008
+    for name, operands in (("silu", 1), ("gelu", 1), ("swiglu", 2)):
+        nbytes = (operands + 1) * n * 2
+        sets = [tuple(torch.randn(n, generator=gen, device="cuda").to(torch.bfloat16) for _ in range(operands + 1))
+                for _ in range(sets_for(nbytes))]
+        if name == "swiglu":
+            launches = [lambda s=s: cf._lib.check(lib.cf_swiglu(
+                s[0].data_ptr(), s[1].data_ptr(), s[2].data_ptr(), cf._lib.CF_BF16, n,
+                torch.cuda.current_stream().cuda_stream)) for s in sets]
+        else:
+            fn = getattr(lib, f"cf_{name}")
+            launches = [lambda s=s, fn=fn: cf._lib.check(fn(
+                s[0].data_ptr(), s[1].data_ptr(), cf._lib.CF_BF16, n,
+                torch.cuda.current_stream().cuda_stream)) for s in sets]
+        r = summary(time_launches(torch, launches, warmup, runs))
+        out[f"{name}_bf16_16384x11008"] = {**r, "bytes": nbytes, "GB/s": gbs(nbytes, r["median_ms"]),
+                                          "frac_hbm": gbs(nbytes, r["median_ms"]) / PEAK_HBM_GBS}
+        del sets, launches
     # A plain copy of the same size as the RMSNorm traffic: the achievable bound.
     nbytes = rows * cols * 2
     sets = [(torch.empty(nbytes, dtype=torch.uint8, device="cuda"),
