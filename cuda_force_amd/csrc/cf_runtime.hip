@@ -80,20 +80,34 @@ constexpr int kCopyUnroll = 4;
 
 /// Streaming copy: every workgroup moves one contiguous chunk of
 /// 256 x 4 16-byte vectors with nontemporal loads and stores (a one-shot grid
-/// measured faster than a grid-stride loop on MI355X).
-__global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ src,
-                                                     uint4* __restrict__ dst, int64_t vectors) {
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x * kCopyUnroll + threadIdx.x;
+/// measured faster than a grid-stride loop on MI355X). Workgroups whose chunk
+/// is entirely in range load unconditionally: a guarded load makes the
+/// compiler wait for each load before issuing the next.
+template <bool kFull>
+__device__ __forceinline__ void copy16_body(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                            int64_t vectors, int64_t base) {
     uint4 v[kCopyUnroll];
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
-        const int64_t i = base + static_cast<int64_t>(u) * blockDim.x;
-        if (i < vectors) v[u] = load_stream16(src + i);
+        const int64_t i = base + static_cast<int64_t>(u) * 256;
+        if (kFull || i < vectors) v[u] = load_stream16(src + i);
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
-        const int64_t i = base + static_cast<int64_t>(u) * blockDim.x;
-        if (i < vectors) store_stream16(dst + i, v[u]);
+        const int64_t i = base + static_cast<int64_t>(u) * 256;
+        if (kFull || i < vectors) store_stream16(dst + i, v[u]);
+    }
+}
+
+__global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ src,
+                                                     uint4* __restrict__ dst, int64_t vectors) {
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 * kCopyUnroll;
+    const int64_t base = first + threadIdx.x;
+    if (first + 256 * kCopyUnroll <= vectors) {  // workgroup-uniform
+        copy16_body<true>(src, dst, vectors, base);
+    } else {
+        copy16_body<false>(src, dst, vectors, base);
     }
 }
 
