@@ -221,11 +221,10 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
     }
 }
 
-/// gt[j, m] = bf16(sum over column tiles of gpart[tile][m][j]), fixed order.
-__global__ __launch_bounds__(kThreads) void sum_g_kernel(const float* __restrict__ gpart,
-                                                         uint16_t* __restrict__ gt, int64_t Mp,
-                                                         int64_t tiles) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+/// gt[j, m] = bf16(sum over column tiles of gpart[tile][m][j]), fixed order;
+/// thread i of the launch handles element i.
+__device__ __forceinline__ void sum_g(const float* __restrict__ gpart, uint16_t* __restrict__ gt,
+                                      int64_t Mp, int64_t tiles, int64_t i) {
     if (i >= kRankPad * Mp) return;
     const int64_t m = i / kRankPad;
     const int64_t j = i % kRankPad;
@@ -244,12 +243,11 @@ __global__ __launch_bounds__(kThreads) void sum_g_kernel(const float* __restrict
 }
 
 /// out = scale * sum over row tiles of colpart[tile][j][n], j < rank, as
-/// [rank, C] or (kTransposed) [C, rank]; fixed order.
+/// [rank, C] or (kTransposed) [C, rank]; fixed order; thread i handles
+/// element i.
 template <bool kTransposed>
-__global__ __launch_bounds__(kThreads) void finish_kernel(const float* __restrict__ colpart,
-                                                          uint16_t* __restrict__ out, int64_t tiles,
-                                                          int64_t rank, int64_t C, float scale) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+__device__ __forceinline__ void finish(const float* __restrict__ colpart, uint16_t* __restrict__ out,
+                                       int64_t tiles, int64_t rank, int64_t C, float scale, int64_t i) {
     if (i >= rank * C) return;
     const int64_t j = i / C;
     const int64_t n = i % C;
@@ -266,6 +264,32 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const float* __restric
     for (; t < tiles; ++t) total += colpart[(t * kRankPad + j) * C + n];
     const int64_t dst = kTransposed ? n * rank + j : j * C + n;
     out[dst] = static_cast<uint16_t>(f32_to_bf16_bits(scale * total));
+}
+
+/// After the dy pass: grad_b's fixed-order sum (first grad_b_blocks
+/// workgroups) and G's (the rest) are independent, so one launch does both.
+__global__ __launch_bounds__(kThreads) void after_dy_kernel(const float* __restrict__ colpart,
+                                                            uint16_t* __restrict__ grad_b,
+                                                            const float* __restrict__ gpart,
+                                                            uint16_t* __restrict__ gt,
+                                                            int64_t grad_b_blocks, int64_t row_tiles,
+                                                            int64_t rank, int64_t N, float scale,
+                                                            int64_t Mp, int64_t col_tiles) {
+    const int64_t block = blockIdx.x;
+    if (block < grad_b_blocks) {
+        finish<false>(colpart, grad_b, row_tiles, rank, N, scale, block * kThreads + threadIdx.x);
+    } else {
+        sum_g(gpart, gt, Mp, col_tiles, (block - grad_b_blocks) * kThreads + threadIdx.x);
+    }
+}
+
+/// grad_a's fixed-order sum after the x pass, stored transposed ([K, rank]).
+__global__ __launch_bounds__(kThreads) void finish_grad_a_kernel(const float* __restrict__ colpart,
+                                                                 uint16_t* __restrict__ grad_a,
+                                                                 int64_t row_tiles, int64_t rank,
+                                                                 int64_t K, float scale) {
+    finish<true>(colpart, grad_a, row_tiles, rank, K, scale,
+                 static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x);
 }
 
 struct Workspace {
@@ -337,10 +361,10 @@ cf_status launch_lora_backward_fast(const void* x, const void* dy, const void* b
     const int64_t n_tiles = ceil_div<int64_t>(N, kTileCols);
     column_mfma_kernel<true><<<dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(row_tiles)),
                                kThreads, 0, stream>>>(dy_pass);
-    finish_kernel<false><<<static_cast<unsigned>(ceil_div<int64_t>(rank * N, kThreads)), kThreads, 0,
-                           stream>>>(ws.colpart, static_cast<uint16_t*>(grad_b), row_tiles, rank, N,
-                                     scale);
-    sum_g_kernel<<<small_grid, kThreads, 0, stream>>>(ws.gpart, ws.gt, Mp, n_tiles);
+    const int64_t grad_b_blocks = ceil_div<int64_t>(rank * N, kThreads);
+    after_dy_kernel<<<static_cast<unsigned>(grad_b_blocks + small_grid), kThreads, 0, stream>>>(
+        ws.colpart, static_cast<uint16_t*>(grad_b), ws.gpart, ws.gt, grad_b_blocks, row_tiles, rank, N,
+        scale, Mp, n_tiles);
 
     ColumnArgs x_pass;
     x_pass.v = static_cast<const uint16_t*>(x);
@@ -355,9 +379,9 @@ cf_status launch_lora_backward_fast(const void* x, const void* dy, const void* b
     const int64_t k_tiles = ceil_div<int64_t>(K, kTileCols);
     column_mfma_kernel<false><<<dim3(static_cast<unsigned>(k_tiles), static_cast<unsigned>(row_tiles)),
                                 kThreads, 0, stream>>>(x_pass);
-    finish_kernel<true><<<static_cast<unsigned>(ceil_div<int64_t>(rank * K, kThreads)), kThreads, 0,
-                          stream>>>(ws.colpart, static_cast<uint16_t*>(grad_a), row_tiles, rank, K,
-                                    scale);
+    finish_grad_a_kernel<<<static_cast<unsigned>(ceil_div<int64_t>(rank * K, kThreads)), kThreads, 0,
+                           stream>>>(ws.colpart, static_cast<uint16_t*>(grad_a), row_tiles, rank, K,
+                                     scale);
     return check_launch("launching the bf16 LoRA backward", stream);
 }
 
