@@ -10,17 +10,18 @@
 //
 // The work is two reductions over M of HBM-sized operands, so the design
 // reads dy once and x once (the HBM floor) and keeps everything else small:
-//   1. xa (fp32 [M, r]) -> xaT (bf16 [16, Mp], zero-padded), Mp = M rounded
-//      up to the 256-row tile.
-//   2. One pass over dy in 256 x 256 tiles: each 64-row chunk goes HBM ->
-//      registers -> LDS; G partial rows = chunk @ b^T (16x16x32 MFMA, row
-//      fragments by ds_read_b128, b fragments held in registers) and
-//      grad_b partials += xaT-chunk @ chunk (16x16x32 MFMA, the m-contiguous
-//      operand by ds_read_b64_tr_b16). Partials go to fp32 workspaces, one
-//      slice per 256-column tile (G) and per 256-row tile (grad_b).
-//   3. G partials summed in a fixed order -> GT (bf16 [16, Mp]).
-//   4. The same column-reduction pass over x with GT: grad_a partials.
-//   5. Fixed-order sums of the partials, times scale, cast, grad_a transposed.
+//   1. One pass over dy in 256 x 256 tiles (Mp = M rounded up to 256): each
+//      64-row chunk goes HBM -> registers -> LDS; G partial rows = chunk @
+//      b^T (16x16x32 MFMA, row fragments by ds_read_b128, b fragments held in
+//      registers) and grad_b partials += bf16(xa)^T-chunk @ chunk (16x16x32
+//      MFMA; the xa fragments are read from the fp32 xa and rounded in
+//      registers, the m-contiguous operand by ds_read_b64_tr_b16). Partials
+//      go to fp32 workspaces, one slice per 256-column tile (G) and per
+//      256-row tile (grad_b).
+//   2. One launch sums both in a fixed order: grad_b (times scale, cast) and
+//      G -> GT (bf16 [16, Mp]).
+//   3. The same column-reduction pass over x with GT: grad_a partials.
+//   4. Their fixed-order sum, times scale, cast, stored transposed.
 // Deterministic: every sum has a fixed order, no atomics.
 #include "cf_lora_bwd.hpp"
 
@@ -66,22 +67,15 @@ __device__ __forceinline__ bf16x8_t concat(s16x4_t lo, s16x4_t hi) {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-/// xaT[j, m] = bf16(xa[m, j]) for j < rank, m < M; zero elsewhere in [16, Mp].
-__global__ __launch_bounds__(kThreads) void transpose_round_kernel(const float* __restrict__ xa,
-                                                                   uint16_t* __restrict__ xat,
-                                                                   int64_t M, int64_t Mp,
-                                                                   int64_t rank) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= kRankPad * Mp) return;
-    const int64_t j = i / Mp;
-    const int64_t m = i % Mp;
-    const float v = (j < rank && m < M) ? xa[m * rank + j] : 0.0f;
-    xat[i] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+__device__ __forceinline__ uint32_t buffer_load4(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset,
+                                                  uint32_t soffset) {
+    return __builtin_amdgcn_raw_buffer_load_b32(rsrc, voffset, soffset, 0);
 }
 
 struct ColumnArgs {
     const uint16_t* v;     // [M, C] bf16, the operand reduced over rows
-    const uint16_t* pt;    // [16, Mp] bf16, the other factor, m-contiguous
+    const uint16_t* pt;    // [16, Mp] bf16, the other factor, m-contiguous (x pass)
+    const float* xa;       // [M, rank] fp32, the other factor of the dy pass
     const uint16_t* b;     // [rank, C] bf16 (row-dot pass only)
     float* colpart;        // [Mp / 256][16][C] fp32
     float* gpart;          // [ceil(C / 256)][Mp][16] fp32 (row-dot pass only)
@@ -158,7 +152,8 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     const __amdgpu_buffer_rsrc_t ptbuf =
-        make_buffer(args.pt, static_cast<uint32_t>(kRankPad * args.Mp * 2));
+        make_buffer(kRowDot ? static_cast<const void*>(args.xa) : static_cast<const void*>(args.pt),
+                    static_cast<uint32_t>(kRowDot ? args.M * args.rank * 4 : kRankPad * args.Mp * 2));
 
     load_chunk(m0);
     for (int chunk = 0; chunk < kTileRows / kChunkRows; ++chunk) {
@@ -169,12 +164,29 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
         if (chunk + 1 < kTileRows / kChunkRows) load_chunk(row0 + kChunkRows);
 
         // pt fragments: pt[j = lane % 16][row0 + 32 ms + 8 (lane / 16) .. +7].
+        // The dy pass reads them straight from xa ([M, rank] fp32, eight
+        // rows apart by `rank`), rounding to bf16 as the transposed copy would;
+        // rows past M and columns past the rank read as zero.
         bf16x8_t ptfrag[2];
 #pragma unroll
         for (int ms = 0; ms < 2; ++ms) {
-            const uint32_t off =
-                static_cast<uint32_t>((jl * args.Mp + row0 + 32 * ms + 8 * g) * 2);
-            ptfrag[ms] = as_bf16x8(buffer_load16(ptbuf, off, 0));
+            if constexpr (kRowDot) {
+                uint32_t bits[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int64_t m = row0 + 32 * ms + 8 * g + e;
+                    const uint32_t off =
+                        jl < args.rank ? static_cast<uint32_t>((m * args.rank + jl) * 4) : kOutOfRange;
+                    bits[e] = f32_to_bf16_bits(__uint_as_float(buffer_load4(ptbuf, off, 0)));
+                }
+                const uint4 packed = make_uint4(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16),
+                                                bits[4] | (bits[5] << 16), bits[6] | (bits[7] << 16));
+                ptfrag[ms] = as_bf16x8(packed);
+            } else {
+                const uint32_t off =
+                    static_cast<uint32_t>((jl * args.Mp + row0 + 32 * ms + 8 * g) * 2);
+                ptfrag[ms] = as_bf16x8(buffer_load16(ptbuf, off, 0));
+            }
         }
 #pragma unroll
         for (int ms = 0; ms < 2; ++ms) {
@@ -293,7 +305,6 @@ __global__ __launch_bounds__(kThreads) void finish_grad_a_kernel(const float* __
 }
 
 struct Workspace {
-    uint16_t* xat;
     uint16_t* gt;
     float* gpart;
     float* colpart;
@@ -305,8 +316,6 @@ Workspace carve(void* base, int64_t M, int64_t K, int64_t N) {
     const int64_t Mp = ceil_div<int64_t>(M, kTileRows) * kTileRows;
     uint8_t* p = static_cast<uint8_t*>(base);
     Workspace ws;
-    ws.xat = reinterpret_cast<uint16_t*>(p);
-    p += align256(static_cast<size_t>(kRankPad * Mp) * 2);
     ws.gt = reinterpret_cast<uint16_t*>(p);
     p += align256(static_cast<size_t>(kRankPad * Mp) * 2);
     ws.gpart = reinterpret_cast<float*>(p);
@@ -322,7 +331,7 @@ size_t lora_backward_fast_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M <= 0) return 0;
     const int64_t Mp = ceil_div<int64_t>(M, kTileRows) * kTileRows;
     const int64_t widest = K > N ? K : N;
-    return 2 * align256(static_cast<size_t>(kRankPad * Mp) * 2) +
+    return align256(static_cast<size_t>(kRankPad * Mp) * 2) +
            align256(static_cast<size_t>(ceil_div<int64_t>(N, kTileCols) * Mp * kRankPad) * 4) +
            static_cast<size_t>(Mp / kTileRows * kRankPad * widest) * 4;
 }
@@ -332,7 +341,8 @@ bool lora_backward_fast_eligible(const void* x, const void* dy, const void* b, i
     // Buffer offsets are 32-bit with an out-of-range marker at 2^31.
     const int64_t Mp = ceil_div<int64_t>(M, kTileRows) * kTileRows;
     const bool fits = Mp * K * 2 < (1LL << 31) && Mp * N * 2 < (1LL << 31) &&
-                      rank * N * 2 < (1LL << 31) && kRankPad * Mp * 2 < (1LL << 31);
+                      rank * N * 2 < (1LL << 31) && kRankPad * Mp * 2 < (1LL << 31) &&
+                      Mp * rank * 4 < (1LL << 31);
     return M > 0 && K > 0 && N > 0 && rank > 0 && rank <= kRankPad && K % 8 == 0 && N % 8 == 0 &&
            fits && host_aligned(x, 16) && host_aligned(dy, 16) && host_aligned(b, 16);
 }
@@ -346,11 +356,10 @@ cf_status launch_lora_backward_fast(const void* x, const void* dy, const void* b
     const Workspace ws = carve(workspace, M, K, N);
     const unsigned small_grid = static_cast<unsigned>(ceil_div<int64_t>(kRankPad * Mp, kThreads));
 
-    transpose_round_kernel<<<small_grid, kThreads, 0, stream>>>(xa, ws.xat, M, Mp, rank);
-
     ColumnArgs dy_pass;
     dy_pass.v = static_cast<const uint16_t*>(dy);
-    dy_pass.pt = ws.xat;
+    dy_pass.pt = nullptr;
+    dy_pass.xa = xa;
     dy_pass.b = static_cast<const uint16_t*>(b);
     dy_pass.colpart = ws.colpart;
     dy_pass.gpart = ws.gpart;
@@ -369,6 +378,7 @@ cf_status launch_lora_backward_fast(const void* x, const void* dy, const void* b
     ColumnArgs x_pass;
     x_pass.v = static_cast<const uint16_t*>(x);
     x_pass.pt = ws.gt;
+    x_pass.xa = nullptr;
     x_pass.b = nullptr;
     x_pass.colpart = ws.colpart;
     x_pass.gpart = nullptr;
