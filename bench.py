@@ -404,9 +404,23 @@ def bench_block(torch, cf, warmup: int, runs: int) -> dict:
             entry["TFLOP/s"] = flops[name] / (ms * 1e-3) / 1e12
         per_op[name] = entry
     gemm = sum(flops.values())
+    # The same forward captured once into a HIP graph and replayed: the ~20
+    # launches of a block go out as one submission.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            block.forward(x, residual)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        block.forward(x, residual)
+    replay = summary(time_launches(torch, [graph.replay], warmup, max(runs // 4, 5)))
     return {"block_c4_bf16_8x512_h4096": {
         **total, "tokens": tokens, "tokens/s": tokens / (total["median_ms"] * 1e-3),
         "gemm_flops": gemm, "gemm_TFLOP/s_end_to_end": gemm / (total["median_ms"] * 1e-3) / 1e12,
+        "graph_replay_ms": replay["median_ms"], "graph_tokens/s": tokens / (replay["median_ms"] * 1e-3),
         "per_op_events": per_op}}
 
 

@@ -258,9 +258,12 @@ torch::Tensor sum_hip(const torch::Tensor& input) {
     check_contiguous(input, "input");
     const at::DeviceGuard guard(input.device());
     const cf_dtype dtype = to_cf(input, "input");
-    torch::Tensor out = torch::zeros({1}, input.options().dtype(torch::kFloat32));
+    // accumulate = 0: the kernel writes the sum, so no fill is needed (and
+    // none is recorded when the op is captured into a graph).
     const int64_t count = input.numel();
-    if (count > 0) {
+    if (count == 0) return torch::zeros({}, input.options());
+    torch::Tensor out = torch::empty({1}, input.options().dtype(torch::kFloat32));
+    {
         const size_t bytes = cf_reduce_sum_workspace_bytes(count);
         torch::Tensor workspace =
             torch::empty({static_cast<int64_t>(bytes)}, input.options().dtype(torch::kUInt8));
