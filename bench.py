@@ -2,7 +2,7 @@
 """Benchmark of the custom-op hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--configs 1,2,3,4,5,paged,tensorcore]
+                    [--configs 1,2,3,4,5,paged,tensorcore,fp8]
 
 Prints ONE JSON line (the driver's contract). The workload behind `value` is
 BASELINE.json's configs[1] - the memory-bound pair RMSNorm bf16 [16384, 4096]
@@ -48,6 +48,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0       # dense fp8 MFMA
 METRIC = "INT8 quant/RMSNorm/softmax GB/s (% HBM peak); fused LoRA-linear TFLOP/s"
 CACHE_FLUSH_BYTES = 1 << 30    # rotate buffer sets until they exceed this
 
@@ -492,6 +493,44 @@ def bench_tensor_core(torch, cf, warmup: int, runs: int) -> dict:
     return out
 
 
+def bench_fp8(torch, cf, warmup: int, runs: int) -> dict:
+    """fp8 (e4m3fn) MFMA matmul, bf16 output, at 8192^3 and 4096^3; FLOP/s
+    counts 2 m n k against the dense fp8 peak, with hipBLASLt's fp8 GEMM
+    (torch._scaled_mm, per-tensor scales) for context where torch offers it."""
+    lib = cf._lib.load()
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for n in (8192, 4096):
+        codes = torch.randint(0, 256, (2, n, n), generator=gen, device="cuda", dtype=torch.uint8)
+        codes = (codes & 0xA7) | 0x18  # finite, moderate magnitudes
+        x, w = codes[0], codes[1]
+        y = torch.empty(n, n, dtype=torch.bfloat16, device="cuda")
+
+        def fp8():
+            cf._lib.check(lib.cf_matmul_fp8(x.data_ptr(), w.data_ptr(), y.data_ptr(), n, n, n, 1.0, stream))
+
+        r = summary(time_launches(torch, [fp8], warmup, runs))
+        flops = 2 * n ** 3
+        tflops = flops / (r["median_ms"] * 1e-3) / 1e12
+        out[f"matmul_fp8_{n}"] = {**r, "TFLOP/s": tflops, "frac_fp8_peak": tflops / PEAK_FP8_TFLOPS}
+        try:
+            xf = x.view(torch.float8_e4m3fn)
+            wf = w.view(torch.float8_e4m3fn).t().contiguous().t()  # column-major right operand
+            one = torch.ones((), device="cuda")
+            torch._scaled_mm(xf, wf, scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+            r = summary(time_launches(
+                torch, [lambda: torch._scaled_mm(xf, wf, scale_a=one, scale_b=one, out_dtype=torch.bfloat16)],
+                warmup, runs))
+            out[f"torch_scaled_mm_fp8_{n}_context"] = {
+                **r, "TFLOP/s": flops / (r["median_ms"] * 1e-3) / 1e12}
+        except (RuntimeError, AttributeError) as exc:
+            out[f"torch_scaled_mm_fp8_{n}_context"] = {"unavailable": str(exc).splitlines()[0][:160]}
+        del codes, y
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_bulk_quant(torch, cf, warmup: int) -> dict:
     """config 5: every weight of a 7B model, bf16 -> int8 + scales -> bf16."""
     gen = torch.Generator(device="cuda").manual_seed(5)
@@ -596,7 +635,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--quick", action="store_true", help="skip the breakdown (main step only)")
-    parser.add_argument("--configs", default="1,2,3,4,5,paged,tensorcore",
+    parser.add_argument("--configs", default="1,2,3,4,5,paged,tensorcore,fp8",
                         help="breakdown configs to run (comma-separated: 1-5, paged, tensorcore)")
     parser.add_argument("--detail", default="", help="also write the full result JSON here")
     args = parser.parse_args(argv)
@@ -635,7 +674,8 @@ def main(argv: list[str] | None = None) -> int:
                          ("config4", lambda: bench_block(torch, cf, 20, args.runs)),
                          ("config5", lambda: bench_bulk_quant(torch, cf, 3)),
                          ("paged", lambda: bench_paged(torch, cf, args.warmup, args.runs)),
-                         ("tensorcore", lambda: bench_tensor_core(torch, cf, 20, args.runs))):
+                         ("tensorcore", lambda: bench_tensor_core(torch, cf, 20, args.runs)),
+                         ("fp8", lambda: bench_fp8(torch, cf, 20, args.runs))):
             if name not in wanted:
                 continue
             log(f"breakdown {name}")

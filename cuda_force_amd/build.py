@@ -39,12 +39,14 @@ HIP_SOURCES = (
     "cf_scheduler.hip",
     "cf_paged_attention.hip",
     "cf_tensor_core.hip",
+    "cf_matmul_fp8.hip",
 )
 
 # Per-source additions. The fused LoRA kernel accumulates in VGPRs: the
 # compiler's AGPR accumulator allocation rotates registers every K-step.
 HIPCC_EXTRA_FLAGS = {
     "cf_lora_fused.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "cf_matmul_fp8.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
 }
 
 HIP_LIBRARY = PACKAGE_DIR / "libcudaforge_hip.so"

@@ -1,0 +1,92 @@
+// LDS-staging helpers shared by the MFMA GEMM kernels (cf_lora_fused.hip,
+// cf_matmul_fp8.hip): HBM -> LDS copies by buffer loads with the LDS
+// destination, memory-counter waits, a bare barrier and the XCD-aware tile
+// order.
+#pragma once
+
+#include "cf_common.hpp"
+
+namespace cf {
+
+// A buffer offset past every range: the load returns zeros.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+/// s_waitcnt immediate that waits until at most n vector-memory operations
+/// of this wave are outstanding (lgkm and exp counters not waited on).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+/// Buffer resource words for a raw (stride 0) buffer of `bytes` bytes.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_t raw_buffer_words(const void* base, uint32_t bytes) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    return i32x4_t{static_cast<int>(addr & 0xffffffffu), static_cast<int>((addr >> 32) & 0xffffu),
+                   static_cast<int>(bytes), kRawBufferFormat};
+}
+
+/// HBM -> LDS copy of 16 (or 4) bytes per lane: lane l's bytes land at LDS
+/// byte lds_dst + 16 l (4 l), read from buffer offset voffset + soffset
+/// (zeros when out of range). Issued from inline assembly on purpose: the
+/// compiler conservatively drains every LDS DMA in flight (vmcnt(0)) before
+/// each transposed LDS read it emits, which would serialise the prefetch
+/// pipeline; DMA it does not know about cannot trigger that. The caller
+/// orders the copies itself (s_waitcnt vmcnt + barrier before the stage is
+/// read); compiler-generated vmcnt waits only become more conservative. M0
+/// (the LDS base register of the copy) is restored afterwards.
+__device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
+                                      uint32_t soffset) {
+    int saved_m0;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved_m0)
+        : "s"(lds_dst), "v"(voffset), "s"(rsrc), "s"(soffset)
+        : "memory");
+}
+
+__device__ __forceinline__ void dma4(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
+                                     uint32_t soffset) {
+    int saved_m0;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved_m0)
+        : "s"(lds_dst), "v"(voffset), "s"(rsrc), "s"(soffset)
+        : "memory");
+}
+
+/// Workgroup barrier that neither waits on memory counters nor lets the
+/// compiler move memory accesses across it; the caller has already waited
+/// for what the other waves must see.
+__device__ __forceinline__ void bare_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+/// Tile coordinates for workgroup `pid`: undo the round-robin XCD dealing so
+/// consecutive logical ids share an XCD, then walk 4-row bands of tiles.
+__device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    constexpr int kXcds = 8;
+    constexpr int kGroupM = 4;
+    const int total = tiles_m * tiles_n;
+    int logical = pid;
+    if (total % kXcds == 0) {
+        const int per_xcd = total / kXcds;
+        logical = (pid % kXcds) * per_xcd + pid / kXcds;
+    }
+    const int band = kGroupM * tiles_n;
+    const int group = logical / band;
+    const int first_m = group * kGroupM;
+    const int rows_in_group = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+    const int in_group = logical % band;
+    tm = first_m + in_group % rows_in_group;
+    tn = in_group / rows_in_group;
+}
+
+}  // namespace cf

@@ -1,0 +1,393 @@
+// fp8 (OCP e4m3fn) matmul on the fp8 MFMA units of gfx950:
+//
+//   y[M, N] = bf16(scale * (x[M, K] @ w[K, N]))
+//
+// x and w row-major fp8 codes (the operator layout of the LoRA linear and of
+// the matmul the reference demonstrates tensor cores with,
+// cuda/include/cudaforge/tensor_core_matmul.cuh:40-41), fp32 accumulation,
+// one per-tensor scale (the product of the two operands' dequantisation
+// scales) applied in the epilogue, bf16 output. The reference has no fp8
+// path; this is the fp8 half of a bf16/fp8 MFMA matmul replacing its TF32
+// demonstration.
+//
+// Shape of the kernel (the pipeline of the bf16 kernel in cf_lora_fused.hip,
+// with operands of one byte):
+//   * 256x256 output tile per workgroup, 8 waves (two per SIMD), each owning a
+//     64x128 sub-tile held as 2x4 v_mfma_scale_f32_32x32x64_f8f6f4
+//     accumulators (128 fp32 per lane). The MFMA's block scales are fixed at
+//     the E8M0 code 127 (2^0), so it is a plain fp8 product. The product is
+//     computed transposed, y^T = w^T x^T: w supplies the A operand, x the B
+//     operand, so each lane holds runs of 4 consecutive output columns of
+//     one row.
+//   * K-step 64 (one MFMA deep). x travels two K-steps per buffer load with
+//     the LDS destination, as whole 128-byte lines of each row, into a ring
+//     of two slots; w ([64 k][256 n], 256-byte rows) into a ring of four
+//     stages, prefetch distance three. Only waves 0-3 issue the DMA.
+//   * B fragments (x): lane l reads 32 consecutive k bytes of row l % 32 as
+//     two ds_read_b128. A fragments (w): 32 consecutive k values of column
+//     l % 32 from an N-major tile, transposed on the way out of LDS by four
+//     ds_read_b64_tr_b8 (each hands a lane 8 k values of one column). Both
+//     tiles are swizzled so every read is free of bank conflicts.
+//   * Epilogue: scale, round to bf16, 8-byte stores.
+//   * Workgroup ids are remapped so that the tiles of one XCD share x
+//     row-panels in its L2 (tile_of).
+//
+// Shapes: any M; K a positive multiple of 128; N a positive multiple of 16;
+// x, w and y 16-byte aligned.
+#include "cf_common.hpp"
+#include "cf_lds_dma.hpp"
+
+#include <type_traits>
+
+namespace cf {
+namespace {
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x4v_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kBK = 64;                       // k values (bytes) per K-step
+constexpr int kStages = 4;
+constexpr int kThreads = 512;
+constexpr int kXPair = kBM * 2 * kBK;         // 32 KiB: [256 m][128 k], two K-steps
+constexpr int kXSlots = 2;
+constexpr int kTileW = kBK * kBN;             // 16 KiB: [64 k][256 n]
+constexpr int kOffW = kXSlots * kXPair;
+constexpr int kLdsBytes = kOffW + kStages * kTileW;  // 128 KiB
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 workgroup");
+
+constexpr int kUnitScale = 127;  // E8M0 code of 2^0
+
+// Bank behaviour (gfx950, 64 banks of 4 bytes): a 64-bit LDS read serves
+// lanes 0-31 and 32-63 in separate 256-byte cycles; a ds_read_b128 serves
+// two 8-lane octets per cycle, octet o together with o ^ 3 or with 7 - o.
+
+/// Chunk swizzle of the x tile (128-byte rows of eight 16-byte chunks, two
+/// K-steps). A B-fragment read has octet o on rows 8 (o % 4) .. +7, so the
+/// octets served together (rows 0-7 with 24-31, 8-15 with 16-23) must hit
+/// different 128-byte halves: bit 3 of the row flips the chunk's low bit.
+__device__ __forceinline__ int x_swizzle(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+/// Chunk swizzle of the w tile (256-byte rows of sixteen chunks). A
+/// transposed read takes eight consecutive k rows of one 32-byte column pair
+/// in each cycle; moving the pair by k mod 8 puts them in eight different
+/// 32-byte bank groups.
+__device__ __forceinline__ int w_swizzle(int row) { return 2 * (row & 7); }
+
+__device__ __forceinline__ i32x2_t lds_read_tr8(const uint8_t* base, int offset) {
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        (lds_i32x2_t*)((lds_u8_t*)(const_cast<uint8_t*>(base)) + offset));
+}
+
+/// The descriptor in scalar registers (the DMA takes it as an SGPR operand;
+/// the value is wave-uniform, but the compiler cannot always prove it).
+__device__ __forceinline__ i32x4_t uniform(i32x4_t v) {
+    return i32x4_t{__builtin_amdgcn_readfirstlane(v[0]), __builtin_amdgcn_readfirstlane(v[1]),
+                   __builtin_amdgcn_readfirstlane(v[2]), __builtin_amdgcn_readfirstlane(v[3])};
+}
+
+struct Fp8Args {
+    const uint8_t* x;
+    const uint8_t* w;
+    uint16_t* y;
+    int64_t M;
+    int64_t N;
+    int64_t K;
+    float scale;
+    int tiles_m;
+    int tiles_n;
+};
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void matmul_fp8_kernel(Fp8Args args) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1;  // 0..3: 64-row quarter of the tile
+    const int wn = wave & 1;   // 0..1: 128-column half of the tile
+    int tm;
+    int tn;
+    tile_of(static_cast<int>(blockIdx.x), args.tiles_m, args.tiles_n, tm, tn);
+    const int64_t m0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+    const int64_t M = args.M;
+    const int64_t N = args.N;
+    const int64_t K = args.K;
+
+    // ---- HBM -> LDS roles (each load fills 1 KiB of LDS, lane l at byte
+    // 16 l; the global side is permuted to realise the swizzles). Waves 0-3
+    // issue their own share and that of wave + 4 (`vw`). ----
+    // x: share vw = rows 32 vw .. +31, 8 rows per load; lane -> row
+    // 32 vw + 8 i + l/8, physical chunk l % 8. Rows past M read as zero.
+    const int64_t rows_here = M - m0 < kBM ? M - m0 : kBM;
+    const i32x4_t xbuf = uniform(raw_buffer_words(args.x + m0 * K, static_cast<uint32_t>(rows_here * K)));
+    uint32_t x_dma[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int vw = (wave & 3) + 4 * (i >> 2);
+        const int row = 32 * vw + 8 * (i & 3) + (lane >> 3);
+        const int chunk = (lane & 7) ^ x_swizzle(row);
+        x_dma[i] = static_cast<uint32_t>(row * K + chunk * 16);
+    }
+    // w: share vw = k-row quads q = 2 vw + i % 2; lane -> row 4 q + l/16,
+    // physical chunk l % 16. Columns past N read as zero.
+    const i32x4_t wbuf = uniform(raw_buffer_words(args.w, static_cast<uint32_t>(K * N)));
+    uint32_t w_dma[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int vw = (wave & 3) + 4 * (i >> 1);
+        const int row = 4 * (vw * 2 + (i & 1)) + (lane >> 4);
+        const int64_t col = n0 + 16 * ((lane & 15) ^ w_swizzle(row));
+        w_dma[i] = col < N ? static_cast<uint32_t>(row * N + col) : kOutOfRange;
+    }
+
+    const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)lds));
+    auto issue_w = [&](int64_t kt, int piece) {
+        const uint32_t stage = lds_addr + kOffW + static_cast<uint32_t>(kt % kStages) * kTileW;
+        const int vw = (wave & 3) + 4 * (piece >> 1);
+        dma16(wbuf, stage + (vw * 2 + (piece & 1)) * 1024, w_dma[piece],
+              static_cast<uint32_t>(kt * kBK * N));
+    };
+    auto issue_x = [&](int64_t pair, int piece) {
+        const uint32_t slot = lds_addr + static_cast<uint32_t>(pair % kXSlots) * kXPair;
+        const int vw = (wave & 3) + 4 * (piece >> 2);
+        dma16(xbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
+              static_cast<uint32_t>(pair * 2 * kBK));
+    };
+    constexpr int kWLoads = 4;  // w DMA per K-step per issuing wave
+    constexpr int kXLoads = 8;  // x DMA per pair of K-steps per issuing wave
+
+    // ---- LDS -> register fragment roles ----
+    // x (B operand), row block i of the wave: row wm*64 + 32 i + l % 32,
+    // logical chunks 2 (l / 32) and 2 (l / 32) + 1 of the K-step (the odd
+    // K-step of a pair is logical chunks 4-7). The swizzle only depends on
+    // row bits 0-3, which are lane bits 0-3.
+    const int h = lane >> 5;
+    const int x_row = wm * 64 + (lane & 31);
+    const int x_rd0 = x_row * (2 * kBK) + (((2 * h) ^ x_swizzle(lane)) << 4);
+    const int x_rd1 = x_row * (2 * kBK) + (((2 * h + 1) ^ x_swizzle(lane)) << 4);
+    // w (A operand, transposed read), column block jb of the wave: lane l
+    // receives column wn*128 + 32 jb + l % 32, k = 32 (l / 32) + 8 r + e
+    // (byte e of read r). In 16-lane group g, lane j supplies the address of
+    // k row 32 (g / 2) + 8 r + j / 2, columns 16 (g % 2) + 8 (j % 2) .. +7 of
+    // the block.
+    const int g = lane >> 4;
+    const int jl = lane & 15;
+    int w_rd[4];  // read r = 0 of each column block; read r adds 8 rows
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+        const int row = 32 * (g >> 1) + (jl >> 1);
+        const int chunk = wn * 8 + 2 * jb + (g & 1);
+        w_rd[jb] = row * kBN + ((chunk ^ w_swizzle(row)) << 4) + (jl & 1) * 8;
+    }
+    // Rows r * 8 further keep row & 7, hence the same swizzle.
+
+    struct XFrags {
+        i32x8_t x[2];
+    };
+    auto read_x = [&](XFrags& f, int64_t kt) {
+        const uint8_t* sx = lds + static_cast<int>((kt >> 1) % kXSlots) * kXPair;
+        const int odd = static_cast<int>(kt & 1) << 6;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const i32x4v_t lo = *reinterpret_cast<const i32x4v_t*>(sx + ((x_rd0 ^ odd) + i * 32 * 2 * kBK));
+            const i32x4v_t hi = *reinterpret_cast<const i32x4v_t*>(sx + ((x_rd1 ^ odd) + i * 32 * 2 * kBK));
+            f.x[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
+    auto read_w = [&](int64_t kt, int jb) {
+        const uint8_t* sw = lds + kOffW + static_cast<int>(kt % kStages) * kTileW;
+        const i32x2_t r0 = lds_read_tr8(sw, w_rd[jb]);
+        const i32x2_t r1 = lds_read_tr8(sw, w_rd[jb] + 8 * kBN);
+        const i32x2_t r2 = lds_read_tr8(sw, w_rd[jb] + 16 * kBN);
+        const i32x2_t r3 = lds_read_tr8(sw, w_rd[jb] + 24 * kBN);
+        const i32x4v_t lo = __builtin_shufflevector(r0, r1, 0, 1, 2, 3);
+        const i32x4v_t hi = __builtin_shufflevector(r2, r3, 0, 1, 2, 3);
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+
+    f32x16_t acc[4][2];  // [w column block jb][x row block i]
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) acc[jb][i][t] = 0.0f;
+        }
+    }
+
+    // w fragments live in one register set: fragment jb of the next K-step
+    // is read into it once the two MFMAs of this step that use it have
+    // issued. x is double-buffered. On step kt the issuing waves send out
+    // the DMA for K-step kt + 3 (w) and, on odd steps, for x pair
+    // (kt + 3) / 2, spread over the step's eight MFMAs.
+    i32x8_t wf[4];
+    auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next, auto issue, auto odd,
+                        auto issuer) {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                acc[jb][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                    wf[jb], f.x[i], acc[jb][i], 0, 0, 0, kUnitScale, 0, kUnitScale);
+                if constexpr (decltype(issue)::value && decltype(issuer)::value) {
+                    const int s = 2 * jb + i;
+                    if constexpr (decltype(odd)::value) issue_x((next_kt + 2) >> 1, s);
+                    if (s & 1) issue_w(next_kt + 2, s >> 1);
+                }
+            }
+            if constexpr (decltype(read_next)::value) wf[jb] = read_w(next_kt, jb);
+        }
+    };
+
+    auto run = [&](auto issuer) {
+        const int64_t k_tiles = K / kBK;  // even, >= 2
+        auto issue_w_all = [&](int64_t kt) {
+#pragma unroll
+            for (int piece = 0; piece < kWLoads; ++piece) issue_w(kt, piece);
+        };
+        auto issue_x_all = [&](int64_t pair) {
+#pragma unroll
+            for (int piece = 0; piece < kXLoads; ++piece) issue_x(pair, piece);
+        };
+        // Issue order as if steps -2 and -1 had run: x pair 0, w 0, w 1 | x pair 1, w 2.
+        if constexpr (decltype(issuer)::value) {
+            issue_x_all(0);
+            issue_w_all(0);
+            issue_w_all(1);
+            if (k_tiles > 2) {
+                issue_x_all(1);
+                issue_w_all(2);
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kWLoads + kXLoads));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
+            }
+        }
+        bare_barrier();  // step 0 in LDS
+
+        XFrags f0;
+        XFrags f1;
+        read_x(f0, 0);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) wf[jb] = read_w(0, jb);
+
+        // Step kt: K-step kt + 1 must be in LDS (this wave's loads, then the
+        // barrier for everyone's). The loads for kt + 3 reuse the stage of
+        // kt - 1, which every wave has finished reading once it is at this
+        // barrier; x pair p goes out on step 2p - 3 into the slot pair p - 2
+        // left. DMA completes in issue order, so the wait leaves exactly the
+        // previous step's loads in flight: w after an even step, w and an x
+        // pair after an odd one.
+        using yes = std::true_type;
+        using no = std::false_type;
+        auto step = [&](int64_t kt, XFrags& cur, XFrags& nxt, auto issue, auto wait_all, auto read,
+                        auto odd) {
+            if constexpr (decltype(read)::value) {
+                if constexpr (decltype(wait_all)::value) {
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                } else if constexpr (decltype(odd)::value) {
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
+                } else {
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads + kXLoads));
+                }
+                bare_barrier();
+                read_x(nxt, kt + 1);
+            }
+            multiply(cur, kt + 1, read, issue, odd, issuer);
+        };
+        int64_t kt = 0;
+        for (; kt + 4 < k_tiles; kt += 2) {
+            step(kt, f0, f1, yes{}, no{}, yes{}, no{});
+            step(kt + 1, f1, f0, yes{}, no{}, yes{}, yes{});
+        }
+        if (k_tiles >= 4) {
+            step(kt, f0, f1, yes{}, no{}, yes{}, no{});
+            step(kt + 1, f1, f0, no{}, no{}, yes{}, yes{});
+            kt += 2;
+        }
+        step(kt, f0, f1, no{}, yes{}, yes{}, no{});
+        step(kt + 1, f1, f0, no{}, no{}, no{}, yes{});
+    };
+    if (wave < 4) {
+        run(std::true_type{});
+    } else {
+        run(std::false_type{});
+    }
+
+    // Store: acc[jb][i] element t of lane l is y[row wm*64 + 32 i + l % 32]
+    // [column wn*128 + 32 jb + 8 (t / 4) + 4 (l / 32) + t % 4]; N is a
+    // multiple of 16, so a four-column run is entirely inside or outside.
+    const float scale = args.scale;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int64_t row = m0 + wm * 64 + 32 * i + (lane & 31);
+        if (row >= M) continue;
+        uint16_t* yrow = args.y + row * N;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t col = n0 + wn * 128 + 32 * jb + 8 * q + 4 * h;
+                if (col < N) {
+                    const f32x16_t& a = acc[jb][i];
+                    uint2 packed;
+                    packed.x = f32_to_bf16_bits(scale * a[4 * q]) |
+                               (f32_to_bf16_bits(scale * a[4 * q + 1]) << 16);
+                    packed.y = f32_to_bf16_bits(scale * a[4 * q + 2]) |
+                               (f32_to_bf16_bits(scale * a[4 * q + 3]) << 16);
+                    *reinterpret_cast<uint2*>(yrow + col) = packed;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+}  // namespace cf
+
+extern "C" {
+
+int cf_matmul_fp8_shape_supported(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0 || n % 16 != 0 || k % (2 * cf::kBK) != 0) return 0;
+    // 32-bit buffer offsets: all of w, and one 256-row panel of x.
+    if (k * n >= (1LL << 31) || static_cast<int64_t>(cf::kBM) * k >= (1LL << 31)) return 0;
+    return cf::ceil_div<int64_t>(m, cf::kBM) * cf::ceil_div<int64_t>(n, cf::kBN) < (1LL << 31) ? 1 : 0;
+}
+
+cf_status cf_matmul_fp8(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k, float scale,
+                        void* stream) {
+    if (!cf_matmul_fp8_shape_supported(m, n, k)) {
+        return cf::fail(CF_ERR_UNSUPPORTED,
+                        "cf_matmul_fp8: shape %lld x %lld x %lld is not tiled (k must be a positive multiple "
+                        "of 128, n of 16)",
+                        static_cast<long long>(m), static_cast<long long>(n), static_cast<long long>(k));
+    }
+    if (x == nullptr || w == nullptr || y == nullptr) {
+        return cf::fail(CF_ERR_INVALID_ARGUMENT, "cf_matmul_fp8: null pointer");
+    }
+    if (!cf::host_aligned(x, 16) || !cf::host_aligned(w, 16) || !cf::host_aligned(y, 16)) {
+        return cf::fail(CF_ERR_UNSUPPORTED, "cf_matmul_fp8: x, w and y must be 16-byte aligned");
+    }
+    cf::Fp8Args args;
+    args.x = static_cast<const uint8_t*>(x);
+    args.w = static_cast<const uint8_t*>(w);
+    args.y = static_cast<uint16_t*>(y);
+    args.M = m;
+    args.N = n;
+    args.K = k;
+    args.scale = scale;
+    args.tiles_m = static_cast<int>(cf::ceil_div<int64_t>(m, cf::kBM));
+    args.tiles_n = static_cast<int>(cf::ceil_div<int64_t>(n, cf::kBN));
+    auto s = static_cast<hipStream_t>(stream);
+    cf::matmul_fp8_kernel<<<args.tiles_m * args.tiles_n, cf::kThreads, 0, s>>>(args);
+    return cf::check_launch("launching the fp8 MFMA matmul", s);
+}
+
+}  // extern "C"

@@ -248,6 +248,23 @@ size_t cf_matmul_tensor_core_workspace_bytes(int64_t m, int64_t n, int64_t k);
 cf_status cf_matmul_tensor_core(const float* a, const float* b, float* c, int64_t m, int64_t n,
                                 int64_t k, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- fp8 matmul on the matrix cores ------------------------------------- */
+
+/* 1 when cf_matmul_fp8 takes this shape: m >= 1, k a positive multiple of
+ * 128, n a positive multiple of 16, k * n < 2^31. It has no counterpart in
+ * the reference (no fp8 path there); it is the fp8 half of the MFMA matmul that
+ * replaces the TF32 demonstration (cuda/include/cudaforge/tensor_core_matmul.cuh:40-41). */
+int cf_matmul_fp8_shape_supported(int64_t m, int64_t n, int64_t k);
+
+/* y[m, n] = bf16(scale * (x[m, k] w[k, n])) for row-major OCP e4m3fn codes x
+ * and w (one byte each), fp32 accumulation on the fp8 MFMA units, bf16 y; scale
+ * is the product of the operands' per-tensor dequantisation scales. x, w and y
+ * 16-byte aligned. An unsupported shape is CF_ERR_UNSUPPORTED without
+ * launching. No workspace, no allocation. It has no counterpart in the
+ * reference, which has no fp8 path. */
+cf_status cf_matmul_fp8(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k,
+                        float scale, void* stream);
+
 /* ---- paged-attention decode ---------------------------------------------- */
 
 /* Workspace bytes cf_paged_attention uses to split long contexts across

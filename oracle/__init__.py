@@ -10,8 +10,8 @@ Contents:
                 restatement (cf_oracle.c, bit-exact by construction) and an
                 independent numpy restatement, cross-checked in the tests.
   floatops.py   float64 restatements of RMSNorm, softmax, the sum, the LoRA
-                linear and its adapter gradients, the activations, and
-                paged-attention decode.
+                linear and its adapter gradients, the activations,
+                paged-attention decode, and the fp8 (e4m3fn) matmul.
   ref_runner.py runs the reference's own CPU operators (cpp/src/bindings.cpp,
                 compiled by `make -C oracle ref` into oracle/_ref/) in a child
                 process, for golden vectors and the "reference" CPU baseline.
@@ -22,10 +22,12 @@ invariants, planted mistakes) is listed in tests/test_oracle.py.
 
 from oracle.floatops import (  # noqa: F401
     bf16_bits_to_f32,
+    e4m3fn_to_f64,
     f32_to_bf16_bits,
     gelu_tanh,
     lora_backward,
     lora_linear,
+    matmul_fp8,
     paged_attention,
     rmsnorm,
     round_bf16,

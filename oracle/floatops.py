@@ -155,3 +155,26 @@ def paged_attention(
             weights = np.exp(scores - scores.max())
             out[s, h] = weights @ values[:, h // group, :] / weights.sum()
     return out
+
+
+def e4m3fn_to_f64(codes: np.ndarray) -> np.ndarray:
+    """Decode OCP fp8 e4m3fn codes (OCP 8-bit floating point specification
+    v1.0, E4M3: sign, 4 exponent bits with bias 7, 3 mantissa bits; exponent
+    0 is subnormal, m * 2^-9; S.1111.111 is NaN; no infinities). The reference
+    has no fp8 type; this is the format the fp8 matmul consumes."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    exponent = (c >> 3) & 0xF
+    mantissa = c & 0x7
+    normal = np.ldexp(1.0 + mantissa / 8.0, exponent - 7)
+    subnormal = np.ldexp(mantissa.astype(np.float64), -9)
+    value = sign * np.where(exponent == 0, subnormal, normal)
+    return np.where((c & 0x7F) == 0x7F, np.nan, value)
+
+
+def matmul_fp8(x_codes: np.ndarray, w_codes: np.ndarray, scale: float) -> np.ndarray:
+    """scale * (x @ w) for e4m3fn codes x [M, K] and w [K, N], float64 (every
+    fp8 product is exact; the sum is float64). The fp8 half of the MFMA matmul
+    that replaces the TF32 demonstration (cuda/include/cudaforge/
+    tensor_core_matmul.cuh:40-41 keeps C = A B row-major with fp32 operands)."""
+    return float(scale) * (e4m3fn_to_f64(x_codes) @ e4m3fn_to_f64(w_codes))
