@@ -14,7 +14,8 @@ wall time, with inputs resident in HBM; buffer sets rotate so the working set
 
 `roofline` is the dominant kernel of the step (RMSNorm): algorithmic bytes per
 launch over its average duration measured with HIP events on its launch
-stream during the timed steps, against 8 TB/s. `traffic` is the HBM bytes
+stream during the timed steps (every 8th launch is bracketed: an event pair on
+every step would lengthen each step by its own queue packets), against 8 TB/s. `traffic` is the HBM bytes
 per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed under
 profiles/ (null when absent). `cpu_baseline` times the reference's own CPU
 operators (oracle/_ref, built from the reference source) on a bounded sample
@@ -27,8 +28,9 @@ quantise/dequantise, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
 hipBLASLt's plain GEMM through torch for context) and its adapter backward,
 config 4 the Llama block forward (tokens/s end to end, per-operator event
 times and TFLOP/s), `paged` the paged-attention decode at the reference's
-benchmark shapes, `tensorcore` the fp32 matmul on the bf16 MFMA units, config 5 bulk 7B quantise/dequantise aggregate GB/s, and a plain copy's
-achieved bandwidth.
+benchmark shapes, `tensorcore` the fp32 matmul on the bf16 MFMA units, `fp8`
+the fp8 MFMA matmul (with hipBLASLt's fp8 GEMM for context), config 5 bulk 7B
+quantise/dequantise aggregate GB/s, and a plain copy's achieved bandwidth.
 """
 
 from __future__ import annotations
@@ -49,6 +51,7 @@ sys.path.insert(0, str(ROOT))
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA
 PEAK_FP8_TFLOPS = 5000.0       # dense fp8 MFMA
+EVENT_STRIDE = 8               # main step: event pair on every 8th RMSNorm launch
 METRIC = "INT8 quant/RMSNorm/softmax GB/s (% HBM peak); fused LoRA-linear TFLOP/s"
 CACHE_FLUSH_BYTES = 1 << 30    # rotate buffer sets until they exceed this
 
@@ -203,14 +206,20 @@ def bench_main_step(torch, cf, steps: int, warmup: int) -> dict:
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    # Every EVENT_STRIDE-th RMSNorm launch of the timed region is bracketed
+    # by an event pair on its stream: an event record is a packet of its own
+    # in the queue, and a pair on every step lengthened the step by ~6 us
+    # (54.2 against 48.0 us on MI355X), so the sampled launches measure the
+    # kernel live without slowing the steps around them.
+    events = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for i in range(0, steps, EVENT_STRIDE)}
     torch.cuda.synchronize()
     started = time.perf_counter()
     for i in range(steps):
-        step(i, events[i])
+        step(i, events.get(i))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - started
-    rms_ms = [a.elapsed_time(b) for a, b in events]
+    rms_ms = [a.elapsed_time(b) for a, b in events.values()]
     ms_per_step = elapsed * 1e3 / steps
     rms_avg = statistics.fmean(rms_ms)
     return {
@@ -708,7 +717,7 @@ def main(argv: list[str] | None = None) -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "rmsnorm_wave_kernel<bf16, 8>",
+            "kernel": "rmsnorm_tile_kernel<bf16, 512>",
             "achieved": achieved,
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

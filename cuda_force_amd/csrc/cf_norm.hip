@@ -8,7 +8,10 @@
 // the storage type, then rmsnorm(r). rsqrt is taken as 1 / sqrt with IEEE
 // sqrt and divide, the way ATen's CPU rsqrt computes it.
 //
-// Design (fast path): one wavefront owns a row. The row is loaded once with
+// Design (fast path for rows of 256, 512 or 1024 16-byte vectors with many
+// rows): rmsnorm_tile_kernel, where a workgroup owns 1-4 whole rows and each
+// of its load instructions reads 4 KiB of contiguous memory; row sums meet in
+// LDS. Otherwise one wavefront owns a row. The row is loaded once with
 // 16-byte loads into registers (a 4096-wide bf16 row is 8 loads per lane),
 // the sum of squares reduces with DPP inside the wave (no LDS, no barrier),
 // and the row is scaled and stored from the same registers, so HBM sees one
@@ -22,6 +25,8 @@
 // row length that is not a whole number of 16-byte vectors use a workgroup per
 // row that reads the row twice (the second pass hits L2).
 #include "cf_common.hpp"
+
+#include <type_traits>
 
 namespace cf {
 namespace {
@@ -168,6 +173,161 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_wave_kernel(
     }
 }
 
+/// Sum of squares of one 16-byte vector. bf16 pairs go through
+/// v_dot2_f32_bf16 (the products of bf16 values are exact in fp32), which
+/// keeps the row in its packed registers.
+template <typename T>
+__device__ __forceinline__ float sum_squares16(const uint4& v) {
+    if constexpr (std::is_same_v<T, bf16_t>) {
+        typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+        const bf16x2_v a = __builtin_bit_cast(bf16x2_v, v.x);
+        const bf16x2_v b = __builtin_bit_cast(bf16x2_v, v.y);
+        const bf16x2_v c = __builtin_bit_cast(bf16x2_v, v.z);
+        const bf16x2_v d = __builtin_bit_cast(bf16x2_v, v.w);
+        const float p = __builtin_amdgcn_fdot2_f32_bf16(c, c, __builtin_amdgcn_fdot2_f32_bf16(a, a, 0.0f, false),
+                                                        false);
+        const float q = __builtin_amdgcn_fdot2_f32_bf16(d, d, __builtin_amdgcn_fdot2_f32_bf16(b, b, 0.0f, false),
+                                                        false);
+        return p + q;
+    } else {
+        constexpr int kPer = Storage<T>::kPerVec;
+        float a[kPer];
+        unpack16<T>(v, a);
+        float p[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) p[i & 1] += a[i] * a[i];
+        return p[0] + p[1];
+    }
+}
+
+/// (x * scale) * g for one 16-byte vector, rounded to T. For bf16 with
+/// `finite` (the row's sum of squares and this weight vector are finite, so
+/// no product is NaN) the rounding is v_cvt_pk_bf16_f32, which then equals
+/// f32_to_bf16_bits bit for bit.
+template <typename T>
+__device__ __forceinline__ uint4 scale16(const uint4& x, const uint4& g, float scale, bool finite) {
+    if constexpr (std::is_same_v<T, bf16_t>) {
+        if (finite) {
+            auto pair = [&](uint32_t xw, uint32_t gw) {
+                const float x0 = __uint_as_float(xw << 16);
+                const float x1 = __uint_as_float(xw & 0xffff0000u);
+                const float g0 = __uint_as_float(gw << 16);
+                const float g1 = __uint_as_float(gw & 0xffff0000u);
+                return f32x2_to_bf16x2_bits((x0 * scale) * g0, (x1 * scale) * g1);
+            };
+            return make_uint4(pair(x.x, g.x), pair(x.y, g.y), pair(x.z, g.z), pair(x.w, g.w));
+        }
+    }
+    constexpr int kPer = Storage<T>::kPerVec;
+    float a[kPer];
+    float w[kPer];
+    unpack16<T>(x, a);
+    unpack16<T>(g, w);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) a[i] = (a[i] * scale) * w[i];
+    return pack16<T>(a);
+}
+
+/// True when all values of a 16-byte vector of T are finite.
+template <typename T>
+__device__ __forceinline__ bool finite16(const uint4& v) {
+    if constexpr (std::is_same_v<T, float>) {
+        const uint32_t m = 0x7f800000u;
+        return (v.x & m) != m && (v.y & m) != m && (v.z & m) != m && (v.w & m) != m;
+    } else {
+        const uint32_t m = std::is_same_v<T, bf16_t> ? 0x7f807f80u : 0x7c007c00u;
+        auto ok = [&](uint32_t w) { return (w & (m & 0xffffu)) != (m & 0xffffu) && (w & (m & 0xffff0000u)) != (m & 0xffff0000u); };
+        return ok(v.x) && ok(v.y) && ok(v.z) && ok(v.w);
+    }
+}
+
+/// Rows of exactly kV 16-byte vectors, kV in {256, 512, 1024}: a 256-thread
+/// workgroup owns 1024 / kV consecutive rows (16 KiB of bf16), and each of
+/// its four load instructions reads 4 KiB of contiguous memory (lane l of
+/// wave v takes vector 256 u + 64 v + l of the workgroup's span). This is the
+/// access pattern at which a plain copy runs fastest on MI355X; one wave per
+/// 8 KiB row with eight loads per lane measured ~5% slower. Row sums are
+/// reduced in each wave (DPP), then across the four waves through LDS in a
+/// fixed order. A workgroup that reaches past the last row loads the last
+/// row again in place of the missing ones and stores nothing for them.
+template <typename T, int kV, bool kResidual>
+__global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_tile_kernel(
+    const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ w,
+    T* __restrict__ y, T* __restrict__ residual_out, int64_t rows, int64_t cols, float eps) {
+    static_assert(kV == 256 || kV == 512 || kV == 1024, "row of 256, 512 or 1024 vectors");
+    static_assert(kDefaultBlockSize == 256, "four waves");
+    constexpr int kPer = Storage<T>::kPerVec;
+    constexpr int kLoads = 4;
+    constexpr int kRows = 256 * kLoads / kV;      // rows per workgroup: 4, 2, 1
+    constexpr int kWeights = kV / 256;            // weight vectors per thread: 1, 2, 4
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid / kWaveSize;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRows;
+    const bool whole = row0 + kRows <= rows;      // workgroup-uniform
+    __shared__ float partials[kWavesPerBlock][kRows];
+
+    uint4 v[kLoads];
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+        const int64_t r = row0 + (u * 256) / kV;
+        const int64_t row = whole || r < rows ? r : rows - 1;
+        v[u] = load_stream16(x + row * cols + static_cast<int64_t>((u * 256) % kV + tid) * kPer);
+    }
+    uint4 g[kWeights];
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < kWeights; ++i) {
+        g[i] = reinterpret_cast<const uint4*>(w)[i * 256 + tid];
+        finite = finite && finite16<T>(g[i]);
+    }
+    if constexpr (kResidual) {
+#pragma unroll
+        for (int u = 0; u < kLoads; ++u) {
+            const int64_t r = row0 + (u * 256) / kV;
+            const int64_t off = (whole || r < rows ? r : rows - 1) * cols +
+                                static_cast<int64_t>((u * 256) % kV + tid) * kPer;
+            float a[kPer];
+            float b[kPer];
+            unpack16<T>(v[u], a);
+            unpack16<T>(load_stream16(residual + off), b);
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) a[i] = a[i] + b[i];
+            // The sum is rounded to the storage type before the norm, as
+            // `x + residual` is in the reference.
+            v[u] = pack16<T>(a);
+            if (whole || r < rows) store_stream16(residual_out + off, v[u]);
+        }
+    }
+
+    float part[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) part[r] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) part[(u * 256) / kV] += sum_squares16<T>(v[u]);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        part[r] = wave_reduce_f32<AddF32>(part[r]);
+        if ((tid & (kWaveSize - 1)) == 0) partials[wave][r] = part[r];
+    }
+    __syncthreads();
+    float scale[kRows];
+    bool row_finite[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const float total = (partials[0][r] + partials[1][r]) + (partials[2][r] + partials[3][r]);
+        scale[r] = inv_rms(total, cols, eps);
+        row_finite[r] = finite && __builtin_isfinite(total);
+    }
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+        const int r = (u * 256) / kV;
+        if (whole || row0 + r < rows) {
+            const int64_t off = (row0 + r) * cols + static_cast<int64_t>((u * 256) % kV + tid) * kPer;
+            store_stream16(y + off, scale16<T>(v[u], g[u % kWeights], scale[r], row_finite[r]));
+        }
+    }
+}
+
 /// Any shape and alignment: one workgroup per row, two passes over the row.
 template <typename T, bool kResidual>
 __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_block_kernel(
@@ -231,7 +391,29 @@ cf_status dispatch(const void* x, const void* residual, const void* w, void* y,
                host_aligned(y, 16);
     if (kResidual) vec = vec && host_aligned(residual, 16) && host_aligned(residual_out, 16);
     const int64_t vectors_per_lane = ceil_div<int64_t>(cols / kPer, kWaveSize);
-    if (vec && vectors_per_lane <= 16) {
+    const int64_t row_vectors = cols / kPer;
+    // The tiled kernel wins once there are several rounds of workgroups
+    // (measured on [16384, 2048 / 4096 / 8192] bf16: 1-3 points of HBM
+    // peak); with a single round ([4096, 4096] bf16, 2048 workgroups) the
+    // wave kernel is faster.
+    const int64_t tile_groups = (row_vectors == 256 || row_vectors == 512 || row_vectors == 1024)
+                                    ? ceil_div<int64_t>(rows, 1024 / row_vectors)
+                                    : 0;
+    if (vec && tile_groups >= 16 * static_cast<int64_t>(cu_count())) {
+        const auto grid = static_cast<unsigned>(tile_groups);
+        auto launch = [&](auto kernel) {
+            kernel<<<grid, kDefaultBlockSize, 0, stream>>>(
+                static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
+                static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
+        };
+        if (row_vectors == 256) {
+            launch(rmsnorm_tile_kernel<T, 256, kResidual>);
+        } else if (row_vectors == 512) {
+            launch(rmsnorm_tile_kernel<T, 512, kResidual>);
+        } else {
+            launch(rmsnorm_tile_kernel<T, 1024, kResidual>);
+        }
+    } else if (vec && vectors_per_lane <= 16) {
         if (vectors_per_lane <= 1) {
             launch_wave<T, 1, kResidual>(x, residual, w, y, residual_out, rows, cols, eps, stream);
         } else if (vectors_per_lane <= 2) {

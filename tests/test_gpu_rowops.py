@@ -92,6 +92,74 @@ def test_rmsnorm_unit_input_returns_the_weight_and_is_scale_invariant():
     np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
 
 
+# The workgroup-tiled RMSNorm (rows of 256, 512 or 1024 16-byte vectors, at
+# least 16 workgroups per CU = 4096 on MI355X) only runs at these sizes; each
+# has a ragged last workgroup.
+TILE_SHAPES = [("bf16", (16385, 2048)), ("bf16", (8193, 4096)), ("bf16", (4097, 8192)),
+               ("f16", (8193, 4096)), ("f32", (16387, 1024)), ("f32", (4097, 4096))]
+
+
+@pytest.mark.parametrize("dtype,shape", TILE_SHAPES, ids=[f"{d}-{s[0]}x{s[1]}" for d, s in TILE_SHAPES])
+def test_rmsnorm_tiled_kernel_matches_the_oracle(dtype, shape):
+    rows, cols = shape
+    g.announce(f"rmsnorm tiled {dtype} {shape}")
+    r = rng(rows + 7 * cols)
+    x = g.storage_bits(r.standard_normal((rows, cols)).astype(np.float32), dtype)
+    w = g.storage_bits((1 + 0.1 * r.standard_normal(cols)).astype(np.float32), dtype)
+    y = run_rmsnorm(x, w, dtype, 1e-6)
+    picked = np.concatenate([np.arange(64), rng(rows).choice(rows, 256, replace=False), np.arange(rows - 64, rows)])
+    exact = oracle.rmsnorm(g.host_values(x[picked], dtype), g.host_values(w, dtype), 1e-6)
+    assert_close(y[picked], exact, dtype, f"tiled rmsnorm {dtype} {shape}")
+
+
+def test_rmsnorm_tiled_kernel_non_finite_bits():
+    """A NaN in a row and an infinite weight: the tiled kernel's fast bf16
+    rounding is skipped for them, so NaN outputs carry the reference's
+    canonical bits (0x7FC0) and the rest round exactly as the oracle does."""
+    rows, cols = 8192, 4096
+    g.announce("rmsnorm tiled bf16 non-finite")
+    r = rng(99)
+    xf = r.standard_normal((rows, cols)).astype(np.float32)
+    xf[5, 100] = np.nan
+    xf[9, 7] = 0.0
+    wf = (1 + 0.1 * r.standard_normal(cols)).astype(np.float32)
+    wf[7] = np.inf
+    x = g.storage_bits(xf, "bf16")
+    w = g.storage_bits(wf, "bf16")
+    y = run_rmsnorm(x, w, "bf16", 1e-6)
+    picked = np.arange(16)
+    with np.errstate(invalid="ignore", over="ignore"):
+        exact = oracle.rmsnorm(g.host_values(x[picked], "bf16"), g.host_values(w, "bf16"), 1e-6)
+    np.testing.assert_array_equal(y[5], np.full(cols, 0x7FC0, np.uint16))
+    assert y[9, 7] == 0x7FC0  # 0 * inf
+    inf_col = oracle.f32_to_bf16_bits(exact[:, 7].astype(np.float32))
+    np.testing.assert_array_equal(y[picked, 7], inf_col)
+    finite_rows = [i for i in picked if i != 5]
+    cols_ok = np.arange(cols) != 7
+    assert_close(y[finite_rows][:, cols_ok], exact[finite_rows][:, cols_ok], "bf16", "non-finite neighbours")
+
+
+@pytest.mark.parametrize("dtype,shape", [("bf16", (8193, 4096)), ("f32", (4097, 4096))], ids=str)
+def test_fused_residual_rmsnorm_tiled_kernel(dtype, shape):
+    g.announce(f"fused residual rmsnorm tiled {dtype} {shape}")
+    r = rng(shape[0] + 3)
+    x = g.storage_bits(r.standard_normal(shape).astype(np.float32), dtype)
+    res = g.storage_bits(r.standard_normal(shape).astype(np.float32), dtype)
+    w = g.storage_bits((1 + 0.1 * r.standard_normal(shape[1])).astype(np.float32), dtype)
+    xg, rg, wg = g.to_gpu(x, dtype), g.to_gpu(res, dtype), g.to_gpu(w, dtype)
+    yg, sg = torch.empty_like(xg), torch.empty_like(xg)
+    g.call("cf_fused_residual_rmsnorm", xg.data_ptr(), rg.data_ptr(), wg.data_ptr(), yg.data_ptr(),
+           sg.data_ptr(), g.cf(dtype), shape[0], shape[1], 1e-6, g.stream())
+    torch.cuda.synchronize()
+    summed = g.storage_bits(g.host_values(x, dtype) + g.host_values(res, dtype), dtype)
+    got_sum = g.to_host(sg)
+    np.testing.assert_array_equal(got_sum.view(np.uint32) if dtype == "f32" else got_sum,
+                                  summed.view(np.uint32) if dtype == "f32" else summed)
+    picked = np.concatenate([np.arange(32), np.arange(shape[0] - 32, shape[0])])
+    exact = oracle.rmsnorm(g.host_values(summed[picked], dtype), g.host_values(w, dtype), 1e-6)
+    assert_close(g.to_host(yg)[picked], exact, dtype, "fused residual rmsnorm tiled")
+
+
 def test_config2_rmsnorm_full_size():
     g.announce("config 2: rmsnorm bf16 [16384, 4096]")
     r = rng(2002)
