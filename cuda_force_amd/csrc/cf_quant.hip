@@ -20,16 +20,20 @@
 // non-negative floats correctly and propagates NaN the way torch.amax does.
 //
 // The per-element divide is the only expensive arithmetic. With inv the
-// correctly rounded 1/s (one IEEE divide per block), q0 = fl(x * inv) is
-// within 2.3e-5 of fl(x/s) for every |x| <= absmax, so rint(q0) is the code
-// unless q0 lies within 6e-5 of a half-integer. There one Markstein step,
-// q1 = fma(fma(-q0, s, x), inv, q0), recovers fl(x/s) itself (Markstein's
-// correctly-rounded-quotient theorem for a correctly rounded reciprocal) and
-// rint(q1) rounds half to even exactly as rint(x / s) does - no divide, no
-// branch. (bf16 inputs land near a half-integer for ~0.3% of elements, far
-// too often for a divergent fallback.) The theorem needs the residual to
-// stay clear of the subnormal range, which holds for s >= 2^-100; blocks with
-// a smaller scale use the IEEE divide.
+// correctly rounded 1/s (one IEEE divide per block) and q0 = fl(x * inv), one
+// Markstein step, q1 = fma(fma(-q0, s, x), inv, q0), recovers fl(x/s) itself
+// (Markstein's correctly-rounded-quotient theorem for a correctly rounded
+// reciprocal), and rint(q1) rounds half to even exactly as rint(x / s) does -
+// no divide, no branch. The theorem needs the residual to stay clear of the
+// subnormal range, which holds for s >= 2^-100; blocks with a smaller scale
+// use the IEEE divide.
+//
+// In a block with a finite absmax and such a scale (every block of ordinary
+// data) |x / s| <= 127 + tiny and no element is NaN, so the code needs no
+// clamp: code + 128 is an exact integer in [1, 255], which v_cvt_pk_u8_f32
+// converts and packs into its byte of the output word in one instruction;
+// XOR 0x80 per byte re-centres the four codes. Other blocks (absmax NaN or
+// infinite, or a scale below 2^-100) take clamp_code per element.
 #include "cf_common.hpp"
 
 namespace cf {
@@ -70,6 +74,19 @@ __device__ __forceinline__ int fast_code(float x, const BlockScale& b) {
     const float r0 = rintf(q0);
     const float q1 = fmaf(fmaf(-q0, b.s, x), b.inv, q0);  // fl(x / s)
     return clamp_code(fabsf(q0 - r0) > 0.5f - kTieMargin ? rintf(q1) : r0);
+}
+
+/// Four codes of an ordinary block (finite absmax, s >= 2^-100) packed into
+/// one word; see the file comment.
+__device__ __forceinline__ uint32_t pack4_ordinary(const float* v, const BlockScale& b) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float q0 = v[i] * b.inv;
+        const float q1 = fmaf(fmaf(-q0, b.s, v[i]), b.inv, q0);  // fl(v / s)
+        w = __builtin_amdgcn_cvt_pk_u8_f32(rintf(q1) + 128.0f, i, w);
+    }
+    return w ^ 0x80808080u;
 }
 
 /// rint(x / s) with the IEEE divide.
@@ -141,8 +158,46 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
         const int64_t e = block * kQuantBlockSize + part * kPer;
         if (!kFull && e >= count) continue;
 
-        // Reciprocal path for every element; blocks with a scale below
-        // 2^-100 (rare: only when the whole block is that small) divide.
+        if constexpr (kMode == 0) {
+            const bool ordinary = m < 0x7F800000u && !b.exact;
+            uint32_t w[kPer / 4];
+            if (ordinary) {
+#pragma unroll
+                for (int j = 0; j < kPer / 4; ++j) w[j] = pack4_ordinary(&v[u][4 * j], b);
+            } else {
+                int c[kPer];
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) c[i] = b.exact ? exact_code(v[u][i], b) : fast_code(v[u][i], b);
+#pragma unroll
+                for (int j = 0; j < kPer / 4; ++j) {
+                    w[j] = (static_cast<uint32_t>(c[4 * j]) & 0xFFu) |
+                           ((static_cast<uint32_t>(c[4 * j + 1]) & 0xFFu) << 8) |
+                           ((static_cast<uint32_t>(c[4 * j + 2]) & 0xFFu) << 16) |
+                           ((static_cast<uint32_t>(c[4 * j + 3]) & 0xFFu) << 24);
+                }
+            }
+            // A plain store: the 4-byte scales of neighbouring waves merge into
+            // whole lines in L2 (a non-temporal store of each costs ~7% of the
+            // kernel). The codes and inputs stay non-temporal.
+            if (part == 0) scales[block] = b.s;
+            if (kFull || (kVec && e + kPer <= count)) {
+                if constexpr (kPer == 4) {
+                    store_stream4(q + e, w[0]);
+                } else {
+                    store_stream8(q + e, make_uint2(w[0], w[1]));
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) {
+                    if (e + i < count) q[e + i] = static_cast<int8_t>((w[i / 4] >> (8 * (i % 4))) & 0xFFu);
+                }
+            }
+            continue;
+        }
+
+        // Fake quantisation: the reciprocal path for every element; blocks with
+        // a scale below 2^-100 (rare: only when the whole block is that small)
+        // divide.
         int codes[kPer];
 #pragma unroll
         for (int i = 0; i < kPer; ++i) codes[i] = fast_code(v[u][i], b);
@@ -153,42 +208,15 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
             }
         }
 
-        if constexpr (kMode == 0) {
-            // A plain store: the 4-byte scales of neighbouring waves merge into
-            // whole lines in L2 (a non-temporal store of each costs ~7% of the
-            // kernel). The codes and inputs stay non-temporal.
-            if (part == 0) scales[block] = b.s;
-            if (kFull || (kVec && e + kPer <= count)) {
-                uint32_t w[kPer / 4];
+        float out[kPer];
 #pragma unroll
-                for (int j = 0; j < kPer / 4; ++j) {
-                    w[j] = (static_cast<uint32_t>(codes[4 * j]) & 0xFFu) |
-                           ((static_cast<uint32_t>(codes[4 * j + 1]) & 0xFFu) << 8) |
-                           ((static_cast<uint32_t>(codes[4 * j + 2]) & 0xFFu) << 16) |
-                           ((static_cast<uint32_t>(codes[4 * j + 3]) & 0xFFu) << 24);
-                }
-                if constexpr (kPer == 4) {
-                    store_stream4(q + e, w[0]);
-                } else {
-                    store_stream8(q + e, make_uint2(w[0], w[1]));
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < kPer; ++i) {
-                    if (e + i < count) q[e + i] = static_cast<int8_t>(codes[i]);
-                }
-            }
+        for (int i = 0; i < kPer; ++i) out[i] = static_cast<float>(codes[i]) * b.s;
+        if (kFull || (kVec && e + kPer <= count)) {
+            store_stream16(y + e, pack16<T>(out));
         } else {
-            float out[kPer];
 #pragma unroll
-            for (int i = 0; i < kPer; ++i) out[i] = static_cast<float>(codes[i]) * b.s;
-            if (kFull || (kVec && e + kPer <= count)) {
-                store_stream16(y + e, pack16<T>(out));
-            } else {
-#pragma unroll
-                for (int i = 0; i < kPer; ++i) {
-                    if (e + i < count) Storage<T>::store(y + e + i, out[i]);
-                }
+            for (int i = 0; i < kPer; ++i) {
+                if (e + i < count) Storage<T>::store(y + e + i, out[i]);
             }
         }
     }

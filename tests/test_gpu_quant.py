@@ -106,6 +106,63 @@ def test_quotients_near_half_integers_take_the_exact_divide():
     assert_bits_equal(q, q_ref.reshape(-1))
 
 
+def test_ties_over_consecutive_block_maxima():
+    """Quotients within a few ulps of k + 0.5 for 8192 consecutive fp32 block
+    maxima at each of five magnitudes: the scales' significands run through
+    every low-bit pattern there (all-ones included), which is where a
+    reciprocal-based quotient could round apart from x / s."""
+    r = rng(123)
+    starts = np.array([127.0, 1.0, 3.0e-30, 7.5e20, 254.0 - 2.0 ** -16], dtype=np.float32)
+    absmax = np.concatenate([(s.view(np.int32) + np.arange(8192, dtype=np.int32)).view(np.float32)
+                             for s in starts])
+    blocks = absmax.size
+    scale = (absmax / np.float32(127)).astype(np.float32)
+    k = r.integers(-126, 126, (blocks, 64)).astype(np.float32)
+    target = ((k + np.float32(0.5)) * scale[:, None]).astype(np.float32)
+    x = (target.view(np.int32) + r.integers(-2, 3, (blocks, 64)).astype(np.int32)).view(np.float32)
+    x[:, 0] = absmax
+    q, sc = gpu_quantize(x)
+    q_ref, s_ref = oracle.quantize_int8(x)
+    assert_bits_equal(sc, s_ref)
+    assert_bits_equal(q, q_ref.reshape(-1))
+
+
+def test_exact_half_integer_quotients_round_to_even_bf16():
+    """bf16 blocks with absmax 127 * 2^j (so s = 2^j exactly) and elements
+    (k + 0.5) * 2^j: every quotient is an exact tie, rounded half to even."""
+    r = rng(124)
+    blocks = 8192
+    j = r.integers(-60, 60, blocks).astype(np.float32)
+    k = r.integers(-127, 127, (blocks, 64)).astype(np.float32)
+    xf = ((k + np.float32(0.5)) * np.exp2(j)[:, None]).astype(np.float32)
+    xf[:, 0] = np.float32(127) * np.exp2(j)
+    x = oracle.f32_to_bf16_bits(xf)
+    assert np.array_equal(oracle.bf16_bits_to_f32(x), xf)  # all exactly representable
+    q, sc = gpu_quantize(x, "bf16")
+    q_ref, s_ref = oracle.quantize_int8(xf)
+    assert_bits_equal(sc, s_ref)
+    assert_bits_equal(q, q_ref.reshape(-1))
+    assert np.all(np.abs(q.reshape(blocks, 64)[:, 1:].astype(np.int32)) % 2 == 0)  # ties went to even
+
+
+def test_blocks_around_the_smallest_fast_scale():
+    """Block maxima from just below to just above 127 * 2^-100 (the boundary
+    between the reciprocal path and the IEEE divide), elements spread over
+    the block's range including near-ties."""
+    r = rng(125)
+    centre = np.float32(127 * 2.0 ** -100)
+    absmax = (centre.view(np.int32) + np.arange(-2048, 2048, dtype=np.int32)).view(np.float32)
+    blocks = absmax.size
+    frac = r.uniform(-1, 1, (blocks, 64)).astype(np.float32)
+    x = (frac * absmax[:, None]).astype(np.float32)
+    x[:, 0] = absmax
+    x[:, 1] = -absmax
+    q, sc = gpu_quantize(x)
+    q_ref, s_ref = oracle.quantize_int8(x)
+    assert_bits_equal(sc, s_ref)
+    assert_bits_equal(q, q_ref.reshape(-1))
+
+
 @pytest.mark.parametrize("out", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("n", [1, 65, 4096, 100_003])
 def test_dequantise_is_bit_exact(out, n):
