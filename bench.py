@@ -13,9 +13,14 @@ wall time, with inputs resident in HBM; buffer sets rotate so the working set
 (>= 1 GiB) exceeds the 256 MB Infinity Cache and every step reads from HBM.
 
 `roofline` is the dominant kernel of the step (RMSNorm): algorithmic bytes per
-launch over its average duration measured with HIP events on its launch
-stream during the timed steps (every 8th launch is bracketed: an event pair on
-every step would lengthen each step by its own queue packets), against 8 TB/s. `traffic` is the HBM bytes
+launch over its average duration during the timed steps (every 8th launch),
+against 8 TB/s. The duration comes from HIP events that the RMSNorm dispatch
+itself records
+(cf_time_next_launch -> hipExtLaunchKernel with start/stop events on the
+launch stream): the kernel's own start and end timestamps, the figure a
+rocprofv3 kernel trace reports, with no event packets queued around the
+launch (an event pair around it also times the dispatch and completion
+packets, ~2.5 us on a 45 us kernel). `traffic` is the HBM bytes
 per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed under
 profiles/ (null when absent). `cpu_baseline` times the reference's own CPU
 operators (oracle/_ref, built from the reference source) on a bounded sample
@@ -23,7 +28,11 @@ of the same workload on this host's cores.
 
 `breakdown` reports every other configuration (`--configs` selects them):
 median over 5 batches of back-to-back launches timed by HIP events, after at
-least 0.3 s of warm-up, with cache-cold rotation: config 1
+least 0.3 s of warm-up, with cache-cold rotation (`median_ms`: launch-to-launch
+time, which for kernels of a few microseconds is the host's launch rate), and
+for entry points that launch one kernel also the median of 25 dispatches
+timed by their own start/end timestamps (`kernel_median_ms`, the kernel-trace
+figure; `kernel_frac_*` is computed from it): config 1
 quantise/dequantise, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
 hipBLASLt's plain GEMM through torch for context) and its adapter backward,
 config 4 the Llama block forward (tokens/s end to end, per-operator event
@@ -51,7 +60,8 @@ sys.path.insert(0, str(ROOT))
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA
 PEAK_FP8_TFLOPS = 5000.0       # dense fp8 MFMA
-EVENT_STRIDE = 8               # main step: event pair on every 8th RMSNorm launch
+KERNEL_SAMPLES = 25            # breakdown: dispatches timed by their own timestamps
+TIMER_STRIDE = 8               # main step: every 8th RMSNorm dispatch is timed
 METRIC = "INT8 quant/RMSNorm/softmax GB/s (% HBM peak); fused LoRA-linear TFLOP/s"
 CACHE_FLUSH_BYTES = 1 << 30    # rotate buffer sets until they exceed this
 
@@ -130,6 +140,37 @@ def time_launches(torch, launches, warmup: int, runs: int, batches: int = 5) -> 
     return out
 
 
+def kernel_times(torch, cf, launches, count: int = KERNEL_SAMPLES) -> list[float]:
+    """Execution time (ms) of `count` back-to-back dispatches, cycling over
+    `launches`, each timed by the start/end timestamps of its own dispatch
+    (cf_time_next_launch). Only for entry points that launch one kernel."""
+    timers = [cf._lib.DispatchTimer() for _ in range(count)]
+    torch.cuda.synchronize()
+    for i, timer in enumerate(timers):
+        timer.arm()
+        launches[i % len(launches)]()
+    torch.cuda.synchronize()
+    samples = [timer.elapsed_ms() for timer in timers]
+    for timer in timers:
+        timer.close()
+    return samples
+
+
+def with_kernel_time(torch, cf, entry: dict, launches, nbytes: int | None = None,
+                     flops: int | None = None, peak: float | None = None) -> dict:
+    """Add the dispatch-timestamp median (and the rate it gives) to `entry`."""
+    ms = statistics.median(kernel_times(torch, cf, launches))
+    entry["kernel_median_ms"] = ms
+    if nbytes is not None:
+        entry["kernel_GB/s"] = gbs(nbytes, ms)
+        entry["kernel_frac_hbm"] = gbs(nbytes, ms) / PEAK_HBM_GBS
+    if flops is not None:
+        tflops = flops / (ms * 1e-3) / 1e12
+        entry["kernel_TFLOP/s"] = tflops
+        entry["kernel_frac_peak"] = tflops / peak
+    return entry
+
+
 def summary(samples_ms: list[float]) -> dict:
     ordered = sorted(samples_ms)
     return {
@@ -193,33 +234,31 @@ def bench_main_step(torch, cf, steps: int, warmup: int) -> dict:
     lib = cf._lib.load()
     CF_BF16 = cf._lib.CF_BF16
 
-    def step(i: int, rms_events=None):
+    def step(i: int, timer=None):
         x, y, lx, ly = sets[i % nsets]
         stream = torch.cuda.current_stream().cuda_stream
-        if rms_events is not None:
-            rms_events[0].record()
+        if timer is not None:
+            timer.arm()
         cf._lib.check(lib.cf_rmsnorm(x.data_ptr(), w.data_ptr(), y.data_ptr(), CF_BF16, rows, cols, 1e-6, stream))
-        if rms_events is not None:
-            rms_events[1].record()
         cf._lib.check(lib.cf_softmax(lx.data_ptr(), CF_BF16, ly.data_ptr(), CF_BF16, s_rows, s_cols, stream))
 
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    # Every EVENT_STRIDE-th RMSNorm launch of the timed region is bracketed
-    # by an event pair on its stream: an event record is a packet of its own
-    # in the queue, and a pair on every step lengthened the step by ~6 us
-    # (54.2 against 48.0 us on MI355X), so the sampled launches measure the
-    # kernel live without slowing the steps around them.
-    events = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for i in range(0, steps, EVENT_STRIDE)}
+    # Every TIMER_STRIDE-th RMSNorm launch of the timed region records its
+    # own start and end timestamps on an event pair (cf_time_next_launch):
+    # no extra packets enter the queue. A timed dispatch still costs its step
+    # ~1.9 us of completion bookkeeping on MI355X, hence the sampling.
+    timers = {i: cf._lib.DispatchTimer() for i in range(0, steps, TIMER_STRIDE)}
     torch.cuda.synchronize()
     started = time.perf_counter()
     for i in range(steps):
-        step(i, events.get(i))
+        step(i, timers.get(i))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - started
-    rms_ms = [a.elapsed_time(b) for a, b in events.values()]
+    rms_ms = [timer.elapsed_ms() for timer in timers.values()]
+    for timer in timers.values():
+        timer.close()
     ms_per_step = elapsed * 1e3 / steps
     rms_avg = statistics.fmean(rms_ms)
     return {
@@ -256,7 +295,9 @@ def bench_quant(torch, cf, warmup: int, runs: int) -> dict:
             torch.cuda.current_stream().cuda_stream))
 
     q = summary(time_launches(torch, [quant(s) for s in sets], warmup, runs))
+    with_kernel_time(torch, cf, q, [quant(s) for s in sets], nbytes=qb)
     d = summary(time_launches(torch, [dequant(s) for s in sets], warmup, runs))
+    with_kernel_time(torch, cf, d, [dequant(s) for s in sets], nbytes=bytes_dequant(n, 4))
     return {
         "quantize_f32_4096x4096": {**q, "GB/s": gbs(qb, q["median_ms"]), "bytes": qb,
                                    "frac_hbm": gbs(qb, q["median_ms"]) / PEAK_HBM_GBS},
@@ -279,6 +320,7 @@ def bench_rowops(torch, cf, warmup: int, runs: int) -> dict:
         s[0].data_ptr(), w.data_ptr(), s[1].data_ptr(), cf._lib.CF_BF16, rows, cols, 1e-6,
         torch.cuda.current_stream().cuda_stream)) for s in sets]
     r = summary(time_launches(torch, launches, warmup, runs))
+    with_kernel_time(torch, cf, r, launches, nbytes=rb)
     out["rmsnorm_bf16_16384x4096"] = {**r, "bytes": rb, "GB/s": gbs(rb, r["median_ms"]),
                                       "frac_hbm": gbs(rb, r["median_ms"]) / PEAK_HBM_GBS}
     del sets, launches
@@ -290,6 +332,7 @@ def bench_rowops(torch, cf, warmup: int, runs: int) -> dict:
             s[0].data_ptr(), cf._lib.CF_BF16, s[1].data_ptr(), cf._lib.CF_BF16, a, b,
             torch.cuda.current_stream().cuda_stream)) for s in sets]
         r = summary(time_launches(torch, launches, warmup, runs))
+        with_kernel_time(torch, cf, r, launches, nbytes=sb)
         out[label] = {**r, "bytes": sb, "GB/s": gbs(sb, r["median_ms"]),
                       "frac_hbm": gbs(sb, r["median_ms"]) / PEAK_HBM_GBS}
         del sets, launches
@@ -303,6 +346,7 @@ def bench_rowops(torch, cf, warmup: int, runs: int) -> dict:
         s[0].data_ptr(), s[1].data_ptr(), w.data_ptr(), s[2].data_ptr(), s[3].data_ptr(), cf._lib.CF_BF16,
         rows, cols, 1e-6, torch.cuda.current_stream().cuda_stream)) for s in sets]
     r = summary(time_launches(torch, launches, warmup, runs))
+    with_kernel_time(torch, cf, r, launches, nbytes=res_bytes)
     out["fused_residual_rmsnorm_bf16_16384x4096"] = {**r, "bytes": res_bytes, "GB/s": gbs(res_bytes, r["median_ms"]),
                                                      "frac_hbm": gbs(res_bytes, r["median_ms"]) / PEAK_HBM_GBS}
     del sets, launches
@@ -321,6 +365,7 @@ def bench_rowops(torch, cf, warmup: int, runs: int) -> dict:
                 s[0].data_ptr(), s[1].data_ptr(), cf._lib.CF_BF16, n,
                 torch.cuda.current_stream().cuda_stream)) for s in sets]
         r = summary(time_launches(torch, launches, warmup, runs))
+        with_kernel_time(torch, cf, r, launches, nbytes=nbytes)
         out[f"{name}_bf16_16384x11008"] = {**r, "bytes": nbytes, "GB/s": gbs(nbytes, r["median_ms"]),
                                           "frac_hbm": gbs(nbytes, r["median_ms"]) / PEAK_HBM_GBS}
         del sets, launches
@@ -331,6 +376,7 @@ def bench_rowops(torch, cf, warmup: int, runs: int) -> dict:
     launches = [lambda s=s: cf._lib.check(lib.cf_copy_bytes(
         s[0].data_ptr(), s[1].data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream)) for s in sets]
     r = summary(time_launches(torch, launches, warmup, runs))
+    with_kernel_time(torch, cf, r, launches, nbytes=2 * nbytes)
     out["copy_128MiB"] = {**r, "bytes": 2 * nbytes, "GB/s": gbs(2 * nbytes, r["median_ms"]),
                           "frac_hbm": gbs(2 * nbytes, r["median_ms"]) / PEAK_HBM_GBS}
     return out
@@ -356,6 +402,7 @@ def bench_lora(torch, cf, warmup: int, runs: int) -> dict:
                                          torch.cuda.current_stream().cuda_stream))
 
     f = summary(time_launches(torch, [fused], warmup, runs))
+    with_kernel_time(torch, cf, f, [fused], flops=flops, peak=PEAK_BF16_TFLOPS)
     out = {"lora_bf16_8192x4096x4096_r16": {**f, "flops": flops, "TFLOP/s": flops / (f["median_ms"] * 1e-3) / 1e12,
                                              "frac_mfma": flops / (f["median_ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}}
 
@@ -521,6 +568,7 @@ def bench_fp8(torch, cf, warmup: int, runs: int) -> dict:
 
         r = summary(time_launches(torch, [fp8], warmup, runs))
         flops = 2 * n ** 3
+        with_kernel_time(torch, cf, r, [fp8], flops=flops, peak=PEAK_FP8_TFLOPS)
         tflops = flops / (r["median_ms"] * 1e-3) / 1e12
         out[f"matmul_fp8_{n}"] = {**r, "TFLOP/s": tflops, "frac_fp8_peak": tflops / PEAK_FP8_TFLOPS}
         try:

@@ -89,6 +89,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_gelu": (_I32, [_P, _P, _I32, _I64, _P]),
     "cf_swiglu": (_I32, [_P, _P, _P, _I32, _I64, _P]),
     "cf_copy_bytes": (_I32, [_P, _P, _I64, _P]),
+    "cf_time_next_launch": (_I32, [_P, _P]),
     "cf_tensor_cores_available": (_I32, []),
     "cf_matmul_tensor_core_shape_supported": (_I32, [_I64, _I64, _I64]),
     "cf_matmul_tensor_core_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
@@ -170,3 +171,70 @@ def dtype_code(dtype: object) -> int:
     if dtype not in mapping:
         raise TypeError(f"no cf_dtype for {dtype}")
     return mapping[dtype]
+
+
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+
+
+@lru_cache(maxsize=1)
+def _hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime this library is linked against (already loaded)."""
+    load()
+    hip = ctypes.CDLL("libamdhip64.so.7", mode=ctypes.RTLD_GLOBAL)
+    hip.hipEventCreateWithFlags.argtypes = [_PP, ctypes.c_uint]
+    hip.hipEventDestroy.argtypes = [_P]
+    hip.hipEventSynchronize.argtypes = [_P]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), _P, _P]
+    for name in ("hipEventCreateWithFlags", "hipEventDestroy", "hipEventSynchronize",
+                 "hipEventElapsedTime"):
+        getattr(hip, name).restype = ctypes.c_int
+    return hip
+
+
+def _hip_check(error: int, what: str) -> None:
+    if error != 0:
+        raise RuntimeError(f"HIP error {error} in {what}")
+
+
+class DispatchTimer:
+    """A start/stop hipEvent pair that one kernel dispatch of this library
+    records itself (cf_time_next_launch): `elapsed_ms()` is that kernel's
+    execution time, the figure a kernel trace reports, with no event packets
+    queued around the launch. Call `arm()` right before the entry point.
+
+    The events skip the system-scope fence by default: with it, each timed
+    dispatch ends with a system-scope cache release, which measured 5.7 us
+    per step on MI355X (1.9 us without it), and timing needs no host-visible
+    ordering."""
+
+    def __init__(self, flags: int = HIP_EVENT_DISABLE_SYSTEM_FENCE) -> None:
+        hip = _hip_runtime()
+        self.start = ctypes.c_void_p()
+        self.stop = ctypes.c_void_p()
+        _hip_check(hip.hipEventCreateWithFlags(ctypes.byref(self.start), flags), "hipEventCreate")
+        _hip_check(hip.hipEventCreateWithFlags(ctypes.byref(self.stop), flags), "hipEventCreate")
+
+    def arm(self) -> None:
+        check(load().cf_time_next_launch(self.start, self.stop))
+
+    def elapsed_ms(self) -> float:
+        hip = _hip_runtime()
+        _hip_check(hip.hipEventSynchronize(self.stop), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        _hip_check(hip.hipEventElapsedTime(ctypes.byref(ms), self.start, self.stop),
+                   "hipEventElapsedTime")
+        return float(ms.value)
+
+    def close(self) -> None:
+        hip = _hip_runtime()
+        for ev in (self.start, self.stop):
+            if ev:
+                hip.hipEventDestroy(ev)
+        self.start = ctypes.c_void_p()
+        self.stop = ctypes.c_void_p()
+
+    def __del__(self) -> None:  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass

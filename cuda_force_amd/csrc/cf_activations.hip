@@ -131,14 +131,16 @@ cf_status launch(const void* a, const void* b, void* y, int64_t count, hipStream
         const int64_t grid = ceil_div<int64_t>(waves, kDefaultBlockSize / kWaveSize);
         CF_REQUIRE(grid < (1LL << 31), "%s: %lld elements exceed the launch limit", what,
                    static_cast<long long>(count));
-        elementwise_kernel<T, Op, kBinary><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            static_cast<const T*>(a), static_cast<const T*>(b), static_cast<T*>(y), count);
+        cf::launch(elementwise_kernel<T, Op, kBinary>, dim3(static_cast<unsigned>(grid)),
+                   dim3(kDefaultBlockSize), 0, stream, static_cast<const T*>(a),
+                   static_cast<const T*>(b), static_cast<T*>(y), count);
     } else {
         const int64_t wanted = ceil_div<int64_t>(count, kDefaultBlockSize);
         const int64_t cap = static_cast<int64_t>(cu_count()) * 32;
         const int64_t grid = wanted < cap ? wanted : cap;
-        elementwise_scalar_kernel<T, Op, kBinary><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            static_cast<const T*>(a), static_cast<const T*>(b), static_cast<T*>(y), count);
+        cf::launch(elementwise_scalar_kernel<T, Op, kBinary>, dim3(static_cast<unsigned>(grid)),
+                   dim3(kDefaultBlockSize), 0, stream, static_cast<const T*>(a),
+                   static_cast<const T*>(b), static_cast<T*>(y), count);
     }
     return check_launch(what, stream);
 }

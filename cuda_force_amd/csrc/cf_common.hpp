@@ -16,10 +16,13 @@
 // with 4 more reads of one lane per row.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
 #include <cstdint>
+#include <tuple>
+#include <utility>
 
 #include "../../include/cudaforge_hip.h"
 
@@ -374,6 +377,47 @@ cf_status check_launch(const char* what, hipStream_t stream);
 
 /// Compute units of the current device (cached per device, thread-safe).
 int cu_count();
+
+/// Events armed by cf_time_next_launch() for the calling thread's next
+/// kernel launch; both null when none is armed.
+struct LaunchEvents {
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+
+/// Hand out and disarm the calling thread's armed events.
+LaunchEvents take_launch_events();
+
+/// Keep a launch error that did not go through hipGetLastError for the next
+/// check_launch() on this thread.
+void note_launch_error(hipError_t error);
+
+/// Launch `kernel` on `stream`. When cf_time_next_launch() armed events on
+/// this thread, the dispatch itself records its start and completion on them
+/// (hipExtLaunchKernel), so their elapsed time is the kernel's own execution
+/// time, without the queue packets an event pair around the launch adds.
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes,
+                   hipStream_t stream, Args&&... args) {
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "argument count of the kernel");
+    const LaunchEvents events = take_launch_events();
+    if (events.start == nullptr && events.stop == nullptr) {
+        kernel<<<grid, block, lds_bytes, stream>>>(std::forward<Args>(args)...);
+        return;
+    }
+    std::tuple<KArgs...> values(std::forward<Args>(args)...);
+    void* pointers[sizeof...(KArgs)];
+    std::apply(
+        [&](auto&... v) {
+            int i = 0;
+            ((pointers[i++] = static_cast<void*>(&v)), ...);
+        },
+        values);
+    const hipError_t error =
+        hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, pointers, lds_bytes,
+                           stream, events.start, events.stop, 0);
+    if (error != hipSuccess) note_launch_error(error);
+}
 
 /// True when `dtype` is one of the three storage types.
 inline bool valid_dtype(cf_dtype dtype) {

@@ -516,9 +516,9 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
     args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
     const int grid = args.tiles_m * args.tiles_n;
     if (rank > 0) {
-        lora_fused_bf16_kernel<true, false><<<grid, kThreads, 0, stream>>>(args);
+        launch(lora_fused_bf16_kernel<true, false>, dim3(grid), dim3(kThreads), 0, stream, args);
     } else {
-        lora_fused_bf16_kernel<false, false><<<grid, kThreads, 0, stream>>>(args);
+        launch(lora_fused_bf16_kernel<false, false>, dim3(grid), dim3(kThreads), 0, stream, args);
     }
     return check_launch("launching the fused bf16 LoRA kernel", stream);
 }
@@ -535,7 +535,7 @@ cf_status launch_matmul_bf16_f32out(const void* x, const void* w, float* y, int6
     args.tiles_m = static_cast<int>(ceil_div<int64_t>(M, kBM));
     args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
     const int grid = args.tiles_m * args.tiles_n;
-    lora_fused_bf16_kernel<false, true><<<grid, kThreads, 0, stream>>>(args);
+    launch(lora_fused_bf16_kernel<false, true>, dim3(grid), dim3(kThreads), 0, stream, args);
     return check_launch("launching the bf16 MFMA matmul (fp32 output)", stream);
 }
 

@@ -386,7 +386,8 @@ cf_status cf_matmul_fp8(const void* x, const void* w, void* y, int64_t m, int64_
     args.tiles_m = static_cast<int>(cf::ceil_div<int64_t>(m, cf::kBM));
     args.tiles_n = static_cast<int>(cf::ceil_div<int64_t>(n, cf::kBN));
     auto s = static_cast<hipStream_t>(stream);
-    cf::matmul_fp8_kernel<<<args.tiles_m * args.tiles_n, cf::kThreads, 0, s>>>(args);
+    cf::launch(cf::matmul_fp8_kernel, dim3(args.tiles_m * args.tiles_n), dim3(cf::kThreads), 0, s,
+               args);
     return cf::check_launch("launching the fp8 MFMA matmul", s);
 }
 

@@ -370,15 +370,15 @@ void launch_wave(const void* x, const void* residual, const void* w, void* y, vo
     const int64_t grid = ceil_div<int64_t>(waves, kWavesPerBlock);
     const bool full_cols = cols / Storage<T>::kPerVec == static_cast<int64_t>(kVecs) * kWaveSize;
     if (full_cols) {
-        rmsnorm_wave_kernel<T, kVecs, kRows, kResidual, true>
-            <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-                static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
-                static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
+        launch(rmsnorm_wave_kernel<T, kVecs, kRows, kResidual, true>,
+               dim3(static_cast<unsigned>(grid)), dim3(kDefaultBlockSize), 0, stream,
+               static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
+               static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
     } else {
-        rmsnorm_wave_kernel<T, kVecs, kRows, kResidual, false>
-            <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-                static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
-                static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
+        launch(rmsnorm_wave_kernel<T, kVecs, kRows, kResidual, false>,
+               dim3(static_cast<unsigned>(grid)), dim3(kDefaultBlockSize), 0, stream,
+               static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
+               static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
     }
 }
 
@@ -401,17 +401,17 @@ cf_status dispatch(const void* x, const void* residual, const void* w, void* y,
                                     : 0;
     if (vec && tile_groups >= 16 * static_cast<int64_t>(cu_count())) {
         const auto grid = static_cast<unsigned>(tile_groups);
-        auto launch = [&](auto kernel) {
-            kernel<<<grid, kDefaultBlockSize, 0, stream>>>(
-                static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
-                static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
+        auto run = [&](auto kernel) {
+            launch(kernel, dim3(grid), dim3(kDefaultBlockSize), 0, stream,
+                   static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
+                   static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
         };
         if (row_vectors == 256) {
-            launch(rmsnorm_tile_kernel<T, 256, kResidual>);
+            run(rmsnorm_tile_kernel<T, 256, kResidual>);
         } else if (row_vectors == 512) {
-            launch(rmsnorm_tile_kernel<T, 512, kResidual>);
+            run(rmsnorm_tile_kernel<T, 512, kResidual>);
         } else {
-            launch(rmsnorm_tile_kernel<T, 1024, kResidual>);
+            run(rmsnorm_tile_kernel<T, 1024, kResidual>);
         }
     } else if (vec && vectors_per_lane <= 16) {
         if (vectors_per_lane <= 1) {
@@ -428,11 +428,10 @@ cf_status dispatch(const void* x, const void* residual, const void* w, void* y,
     } else {
         const int64_t max_blocks = static_cast<int64_t>(cu_count()) * 8;
         const int64_t grid = rows < max_blocks ? rows : max_blocks;
-        rmsnorm_block_kernel<T, kResidual>
-            <<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-                static_cast<const T*>(x), static_cast<const T*>(residual),
-                static_cast<const T*>(w), static_cast<T*>(y), static_cast<T*>(residual_out), rows,
-                cols, eps);
+        launch(rmsnorm_block_kernel<T, kResidual>, dim3(static_cast<unsigned>(grid)),
+               dim3(kDefaultBlockSize), 0, stream, static_cast<const T*>(x),
+               static_cast<const T*>(residual), static_cast<const T*>(w), static_cast<T*>(y),
+               static_cast<T*>(residual_out), rows, cols, eps);
     }
     return check_launch(kResidual ? "launching fused_residual_rmsnorm" : "launching rmsnorm",
                         stream);

@@ -357,11 +357,11 @@ cf_status launch_quantize(const void* x, int8_t* q, float* scales, int64_t count
     constexpr int kPer = Storage<T>::kPerVec;
     const bool vec = host_aligned(x, 16) && host_aligned(q, kPer);
     if (vec) {
-        quantize_kernel<T, true><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            static_cast<const T*>(x), q, scales, count);
+        launch(quantize_kernel<T, true>, dim3(static_cast<unsigned>(grid)), dim3(kDefaultBlockSize),
+               0, stream, static_cast<const T*>(x), q, scales, count);
     } else {
-        quantize_kernel<T, false><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            static_cast<const T*>(x), q, scales, count);
+        launch(quantize_kernel<T, false>, dim3(static_cast<unsigned>(grid)),
+               dim3(kDefaultBlockSize), 0, stream, static_cast<const T*>(x), q, scales, count);
     }
     return check_launch("launching quantize_int8", stream);
 }
@@ -373,11 +373,13 @@ cf_status launch_fake_quant(const void* x, void* y, int64_t count, hipStream_t s
                static_cast<long long>(count));
     const bool vec = host_aligned(x, 16) && host_aligned(y, 16);
     if (vec) {
-        fake_quant_kernel<T, true><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            static_cast<const T*>(x), static_cast<T*>(y), count);
+        launch(fake_quant_kernel<T, true>, dim3(static_cast<unsigned>(grid)),
+               dim3(kDefaultBlockSize), 0, stream, static_cast<const T*>(x), static_cast<T*>(y),
+               count);
     } else {
-        fake_quant_kernel<T, false><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            static_cast<const T*>(x), static_cast<T*>(y), count);
+        launch(fake_quant_kernel<T, false>, dim3(static_cast<unsigned>(grid)),
+               dim3(kDefaultBlockSize), 0, stream, static_cast<const T*>(x), static_cast<T*>(y),
+               count);
     }
     return check_launch("launching quantize_dequantize", stream);
 }
@@ -391,11 +393,11 @@ cf_status launch_dequantize(const int8_t* q, const float* scales, void* y, int64
     constexpr int kPer = Storage<T>::kPerVec;
     const bool vec = host_aligned(q, kPer) && host_aligned(y, 16);
     if (vec) {
-        dequantize_kernel<T, true><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            q, scales, static_cast<T*>(y), count);
+        launch(dequantize_kernel<T, true>, dim3(static_cast<unsigned>(grid)),
+               dim3(kDefaultBlockSize), 0, stream, q, scales, static_cast<T*>(y), count);
     } else {
-        dequantize_kernel<T, false><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-            q, scales, static_cast<T*>(y), count);
+        launch(dequantize_kernel<T, false>, dim3(static_cast<unsigned>(grid)),
+               dim3(kDefaultBlockSize), 0, stream, q, scales, static_cast<T*>(y), count);
     }
     return check_launch("launching dequantize_int8", stream);
 }

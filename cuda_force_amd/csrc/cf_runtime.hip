@@ -18,6 +18,8 @@ namespace {
 
 thread_local char g_last_error[512] = "no error";
 thread_local int g_last_hip_error = 0;
+thread_local LaunchEvents g_launch_events = {nullptr, nullptr};
+thread_local hipError_t g_pending_launch_error = hipSuccess;
 
 bool debug_sync_enabled() {
     static const bool enabled = [] {
@@ -45,8 +47,19 @@ cf_status fail_hip(hipError_t error, const char* what) {
     return CF_ERR_HIP;
 }
 
+LaunchEvents take_launch_events() {
+    const LaunchEvents events = g_launch_events;
+    g_launch_events = {nullptr, nullptr};
+    return events;
+}
+
+void note_launch_error(hipError_t error) { g_pending_launch_error = error; }
+
 cf_status check_launch(const char* what, hipStream_t stream) {
+    const hipError_t pending = g_pending_launch_error;
+    g_pending_launch_error = hipSuccess;
     const hipError_t launch = hipGetLastError();
+    if (pending != hipSuccess) return fail_hip(pending, what);
     if (launch != hipSuccess) return fail_hip(launch, what);
     if (debug_sync_enabled()) {
         const hipError_t done = hipStreamSynchronize(stream);
@@ -145,6 +158,13 @@ int cf_hip_error_is_sticky(int hip_error) {
 
 int cf_abi_version(void) { return 1; }
 
+cf_status cf_time_next_launch(void* start_event, void* stop_event) {
+    CF_REQUIRE((start_event == nullptr) == (stop_event == nullptr),
+               "cf_time_next_launch: give both events or neither");
+    cf::g_launch_events = {static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
+    return CF_OK;
+}
+
 cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream) {
     if (bytes <= 0) return CF_OK;
     CF_REQUIRE(src != nullptr && dst != nullptr, "cf_copy_bytes: null pointer");
@@ -155,8 +175,8 @@ cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream)
         const int64_t grid = cf::ceil_div<int64_t>(vectors, 256 * cf::kCopyUnroll);
         CF_REQUIRE(grid < (1LL << 31), "cf_copy_bytes: %lld bytes exceed the launch limit",
                    static_cast<long long>(bytes));
-        cf::copy16_kernel<<<static_cast<unsigned>(grid), 256, 0, s>>>(
-            static_cast<const uint4*>(src), static_cast<uint4*>(dst), vectors);
+        cf::launch(cf::copy16_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s,
+                   static_cast<const uint4*>(src), static_cast<uint4*>(dst), vectors);
     }
     const int64_t done = vectors * 16;
     const int64_t rest = bytes - done;

@@ -171,20 +171,20 @@ void launch_wave(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t
     const unsigned g = static_cast<unsigned>(grid);
     if (grid_rows == 1) {
         if (full) {
-            softmax_wave_kernel<Tin, Tout, kVecs, 1, true><<<g, kDefaultBlockSize, 0, stream>>>(
-                xin, out, rows, cols);
+            launch(softmax_wave_kernel<Tin, Tout, kVecs, 1, true>, dim3(g), dim3(kDefaultBlockSize),
+                   0, stream, xin, out, rows, cols);
         } else {
-            softmax_wave_kernel<Tin, Tout, kVecs, 1, false><<<g, kDefaultBlockSize, 0, stream>>>(
-                xin, out, rows, cols);
+            launch(softmax_wave_kernel<Tin, Tout, kVecs, 1, false>, dim3(g),
+                   dim3(kDefaultBlockSize), 0, stream, xin, out, rows, cols);
         }
         return;
     }
     if (full) {
-        softmax_wave_kernel<Tin, Tout, kVecs, kRows, true><<<g, kDefaultBlockSize, 0, stream>>>(
-            xin, out, rows, cols);
+        launch(softmax_wave_kernel<Tin, Tout, kVecs, kRows, true>, dim3(g), dim3(kDefaultBlockSize),
+               0, stream, xin, out, rows, cols);
     } else {
-        softmax_wave_kernel<Tin, Tout, kVecs, kRows, false><<<g, kDefaultBlockSize, 0, stream>>>(
-            xin, out, rows, cols);
+        launch(softmax_wave_kernel<Tin, Tout, kVecs, kRows, false>, dim3(g),
+               dim3(kDefaultBlockSize), 0, stream, xin, out, rows, cols);
     }
 }
 
@@ -208,9 +208,9 @@ cf_status dispatch(const void* x, void* y, int64_t rows, int64_t cols, hipStream
     } else {
         const int64_t max_blocks = static_cast<int64_t>(cu_count()) * 8;
         const int64_t grid = rows < max_blocks ? rows : max_blocks;
-        softmax_block_kernel<Tin, Tout><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0,
-                                          stream>>>(static_cast<const Tin*>(x),
-                                                    static_cast<Tout*>(y), rows, cols);
+        launch(softmax_block_kernel<Tin, Tout>, dim3(static_cast<unsigned>(grid)),
+               dim3(kDefaultBlockSize), 0, stream, static_cast<const Tin*>(x),
+               static_cast<Tout*>(y), rows, cols);
     }
     return check_launch("launching softmax", stream);
 }

@@ -302,6 +302,19 @@ cf_status cf_paged_attention(const void* query, const void* k_cache, const void*
  * measure the achievable HBM bandwidth next to the ops above. */
 cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream);
 
+/* Arms the calling thread's next kernel launch made by this library: that
+ * dispatch records its own start and completion timestamps on `start_event`
+ * and `stop_event` (hipEvent_t, created by the caller with timing enabled), so
+ * hipEventElapsedTime(start, stop) is the kernel's execution time as a kernel
+ * trace reports it, without the queue packets of an event pair recorded around
+ * the call. Both NULL disarms. Applies to entry points that launch a single
+ * kernel (quantise, dequantise, RMSNorm, fused residual RMSNorm, softmax,
+ * activations, the fused LoRA forward, the fp8 matmul, the byte copy); with a
+ * multi-kernel entry point only its first launch is timed. It has no
+ * counterpart in the reference, whose benchmarks bracket each launch with an
+ * event pair (benchmarks/benchmark_kernels.cu:59-79). */
+cf_status cf_time_next_launch(void* start_event, void* stop_event);
+
 /* ---- runtime: stream scheduler and caching pools ------------------------
  *
  * The C form of the reference's GpuScheduler / StreamLease

@@ -116,3 +116,11 @@ def test_paged_attention_argument_errors_need_no_device():
                                   1.0, null, 0, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_paged_attention(null, null, null, null, null, null, _lib.CF_F32, 1, 2, 2, 2048, 4, 1,
                                   1.0, null, 0, null) == _lib.CF_ERR_INVALID_ARGUMENT
+
+
+def test_time_next_launch_takes_both_events_or_neither(lib):
+    null = ctypes.c_void_p(0)
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: rejected before use
+    assert lib.cf_time_next_launch(fake, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_time_next_launch(null, fake) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_time_next_launch(null, null) == _lib.CF_OK

@@ -1,0 +1,61 @@
+"""Dispatch timing (cf_time_next_launch): a timed launch computes the same
+result as an untimed one, its elapsed time is the kernel's own (positive, and
+no longer than an event pair recorded around the same launch), and only the
+next launch on the thread is timed."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from cuda_force_amd import _lib
+from tests.gpu_util import call, stream
+
+pytestmark = pytest.mark.gpu
+
+
+def _rmsnorm(x, w, y):
+    call("cf_rmsnorm", x.data_ptr(), w.data_ptr(), y.data_ptr(), _lib.CF_BF16, x.shape[0], x.shape[1],
+         1e-6, stream())
+
+
+def test_timed_launch_matches_untimed_and_is_the_kernel_time():
+    print("case: dispatch timer on rmsnorm bf16 [4096, 4096]", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(4096, 4096, generator=gen, device="cuda").to(torch.bfloat16)
+    w = (1 + 0.02 * torch.randn(4096, generator=gen, device="cuda")).to(torch.bfloat16)
+    plain = torch.empty_like(x)
+    timed = torch.empty_like(x)
+    for _ in range(3):
+        _rmsnorm(x, w, plain)
+    torch.cuda.synchronize()
+
+    timer = _lib.DispatchTimer()
+    pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    pair[0].record()
+    timer.arm()
+    _rmsnorm(x, w, timed)
+    pair[1].record()
+    torch.cuda.synchronize()
+    kernel_ms = timer.elapsed_ms()
+    around_ms = pair[0].elapsed_time(pair[1])
+    timer.close()
+    assert torch.equal(plain.view(torch.int16), timed.view(torch.int16))
+    assert 0.0 < kernel_ms <= around_ms * 1.02 + 1e-3, (kernel_ms, around_ms)
+
+
+def test_only_the_next_launch_is_timed():
+    print("case: dispatch timer armed once, two launches", flush=True)
+    x = torch.ones(256, 1024, device="cuda", dtype=torch.bfloat16)
+    w = torch.ones(1024, device="cuda", dtype=torch.bfloat16)
+    y = torch.empty_like(x)
+    timer = _lib.DispatchTimer()
+    timer.arm()
+    _rmsnorm(x, w, y)
+    torch.cuda.synchronize()
+    first = timer.elapsed_ms()
+    _rmsnorm(x, w, y)  # not armed: must leave the events as they were
+    torch.cuda.synchronize()
+    assert timer.elapsed_ms() == first
+    timer.close()
+    assert torch.equal(y, torch.ones_like(y))
