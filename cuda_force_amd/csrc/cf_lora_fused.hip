@@ -34,8 +34,10 @@
 //     exchanged through LDS, bf16(scale * b) is read transposed from an LDS
 //     copy of b loaded at kernel start, and one v_mfma_f32_16x16x16_bf16 per
 //     16x16 block accumulates the adapter term into the base accumulators.
-//     The tile is rounded to bf16 and written with 8-byte stores (or kept
-//     in fp32, 16-byte stores, for the fp32-output matmul).
+//     The tile is rounded to bf16, staged per wave in LDS and written as
+//     whole 256-byte row pieces with non-temporal 16-byte stores (or kept in
+//     fp32 and stored from registers, 16 bytes per lane, for the fp32-output
+//     matmul).
 //   * Workgroup ids are remapped so the tiles dispatched to one XCD (ids are
 //     dealt round-robin over the 8 XCDs) form a band of 4 row-tiles sharing x
 //     row-panels in that XCD's L2.
@@ -74,6 +76,7 @@ constexpr int kOffB = kOffW + kStages * kStage;
 constexpr int kOffXa = kOffB + kTileB;
 constexpr int kLdsBytes = kOffXa + kXaBytes;             // 148 KiB
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 workgroup");
+static_assert(kThreads / 64 * 64 * 256 <= kOffB, "bf16 output staging stays clear of b and x @ a");
 
 // LDS bank behaviour these layouts are built for (measured on gfx950 with
 // SQ_LDS_BANK_CONFLICT): a ds_read_b64_tr_b16 serves lanes 0-31 and 32-63
@@ -460,7 +463,49 @@ void lora_fused_bf16_kernel(FusedArgs args) {
 
     // Store: acc[jb][i] lane holds y[row wm*64 + 16 rb(i) + lane%16]
     // [columns wn*128 + 16 jb + 4 g .. +3]; N is a multiple of 8, so a
-    // four-column group is entirely inside or outside the matrix.
+    // four- or eight-column group is entirely inside or outside the matrix.
+    if constexpr (!kOutF32) {
+        // bf16 output goes through LDS, so that each store instruction
+        // writes whole rows (16 lanes x 16 bytes = 256 contiguous bytes of a
+        // row, 4 rows per instruction) instead of 32-byte pieces of 16 rows.
+        // Each wave stages its own 64x128 sub-tile (16 KiB, rows of 256
+        // bytes) in the operand area, which every wave has left: the
+        // barrier after the x @ a exchange, or the one below, orders that.
+        // Chunk c (16 bytes) of row r sits at chunk c ^ (r & 15): the 8-byte
+        // writes of a half-wave (16 rows, one chunk each) and the 16-byte
+        // reads (whole rows) both spread over all banks.
+        if constexpr (!kAdapter) __syncthreads();
+        uint8_t* stage = lds + wave * (64 * 256);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 16 * ((i + 2 * wn) & 3) + jl;
+#pragma unroll
+            for (int jb = 0; jb < 8; ++jb) {
+                const int chunk = 2 * jb + (g >> 1);
+                uint2 packed;
+                packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
+                packed.y = f32_to_bf16_bits(acc[jb][i][2]) | (f32_to_bf16_bits(acc[jb][i][3]) << 16);
+                *reinterpret_cast<uint2*>(stage + row * 256 + ((chunk ^ (row & 15)) << 4) +
+                                          (g & 1) * 8) = packed;
+            }
+        }
+        // Only this wave reads what it wrote: LDS operations of a wave
+        // complete in order; the fence keeps the compiler from moving the
+        // reads above the writes.
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        const int c = lane & 15;
+        const int64_t col = n0 + wn * 128 + 8 * c;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int row = 4 * s + (lane >> 4);
+            const uint4 v =
+                *reinterpret_cast<const uint4*>(stage + row * 256 + ((c ^ (row & 15)) << 4));
+            const int64_t grow = m0 + wm * 64 + row;
+            if (grow < M && col < N) store_stream16(args.y + grow * N + col, v);
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t row = m0 + wm * 64 + 16 * ((i + 2 * wn) & 3) + jl;
