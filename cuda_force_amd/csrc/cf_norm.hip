@@ -9,9 +9,10 @@
 // sqrt and divide, the way ATen's CPU rsqrt computes it.
 //
 // Design (fast path for rows of 256, 512 or 1024 16-byte vectors with many
-// rows): rmsnorm_tile_kernel, where a workgroup owns 1-4 whole rows and each
-// of its load instructions reads 4 KiB of contiguous memory; row sums meet in
-// LDS. Otherwise one wavefront owns a row. The row is loaded once with
+// rows): rmsnorm_tile_kernel, where a workgroup of 256 or 512 threads owns
+// whole rows, each thread holds one to four 16-byte vectors, and each load
+// instruction of the workgroup reads 4 or 8 KiB of contiguous memory; row
+// sums meet in LDS. Otherwise one wavefront owns a row. The row is loaded once with
 // 16-byte loads into registers (a 4096-wide bf16 row is 8 loads per lane),
 // the sum of squares reduces with DPP inside the wave (no LDS, no barrier),
 // and the row is scaled and stored from the same registers, so HBM sees one
@@ -241,51 +242,54 @@ __device__ __forceinline__ bool finite16(const uint4& v) {
     }
 }
 
-/// Rows of exactly kV 16-byte vectors, kV in {256, 512, 1024}: a 256-thread
-/// workgroup owns 1024 / kV consecutive rows (16 KiB of bf16), and each of
-/// its four load instructions reads 4 KiB of contiguous memory (lane l of
-/// wave v takes vector 256 u + 64 v + l of the workgroup's span). This is the
-/// access pattern at which a plain copy runs fastest on MI355X; one wave per
-/// 8 KiB row with eight loads per lane measured ~5% slower. Row sums are
-/// reduced in each wave (DPP), then across the four waves through LDS in a
-/// fixed order. A workgroup that reaches past the last row loads the last
-/// row again in place of the missing ones and stores nothing for them.
-template <typename T, int kV, bool kResidual>
-__global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_tile_kernel(
+/// Rows of exactly kV 16-byte vectors, kV in {256, 512, 1024}: a workgroup
+/// of kThreads (256 or 512, dividing kV) threads owns kThreads * kLoads / kV
+/// consecutive rows, and each of its kLoads load instructions reads
+/// kThreads * 16 bytes of contiguous memory (thread t of the workgroup takes
+/// vector kThreads * u + t of the workgroup's span). Few loads per lane run
+/// fastest on MI355X: with 16-byte loads, 1-2 per lane before the first
+/// store stream at 77-79% of HBM peak, 4 at 76%, 8 at 50-70%. Row sums are
+/// reduced in each wave (DPP), then across the waves through LDS in a fixed
+/// order. A workgroup that reaches past the last row loads the last row
+/// again in place of the missing ones and stores nothing for them.
+template <typename T, int kV, int kLoads, int kThreads, bool kResidual>
+__global__ __launch_bounds__(kThreads) void rmsnorm_tile_kernel(
     const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ w,
     T* __restrict__ y, T* __restrict__ residual_out, int64_t rows, int64_t cols, float eps) {
     static_assert(kV == 256 || kV == 512 || kV == 1024, "row of 256, 512 or 1024 vectors");
-    static_assert(kDefaultBlockSize == 256, "four waves");
+    static_assert(kThreads == 256 || kThreads == 512, "four or eight waves");
+    static_assert(kV % kThreads == 0, "an instruction's vectors lie in one row");
+    static_assert((kThreads * kLoads) % kV == 0, "whole rows per workgroup");
     constexpr int kPer = Storage<T>::kPerVec;
-    constexpr int kLoads = 4;
-    constexpr int kRows = 256 * kLoads / kV;      // rows per workgroup: 4, 2, 1
-    constexpr int kWeights = kV / 256;            // weight vectors per thread: 1, 2, 4
+    constexpr int kWaves = kThreads / kWaveSize;
+    constexpr int kRows = kThreads * kLoads / kV;  // rows per workgroup
+    constexpr int kWeights = kV / kThreads;        // weight vectors per thread
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = tid / kWaveSize;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRows;
-    const bool whole = row0 + kRows <= rows;      // workgroup-uniform
-    __shared__ float partials[kWavesPerBlock][kRows];
+    const bool whole = row0 + kRows <= rows;       // workgroup-uniform
+    __shared__ float partials[kWaves][kRows];
 
     uint4 v[kLoads];
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
-        const int64_t r = row0 + (u * 256) / kV;
+        const int64_t r = row0 + (u * kThreads) / kV;
         const int64_t row = whole || r < rows ? r : rows - 1;
-        v[u] = load_stream16(x + row * cols + static_cast<int64_t>((u * 256) % kV + tid) * kPer);
+        v[u] = load_stream16(x + row * cols + static_cast<int64_t>((u * kThreads) % kV + tid) * kPer);
     }
     uint4 g[kWeights];
     bool finite = true;
 #pragma unroll
     for (int i = 0; i < kWeights; ++i) {
-        g[i] = reinterpret_cast<const uint4*>(w)[i * 256 + tid];
+        g[i] = reinterpret_cast<const uint4*>(w)[i * kThreads + tid];
         finite = finite && finite16<T>(g[i]);
     }
     if constexpr (kResidual) {
 #pragma unroll
         for (int u = 0; u < kLoads; ++u) {
-            const int64_t r = row0 + (u * 256) / kV;
+            const int64_t r = row0 + (u * kThreads) / kV;
             const int64_t off = (whole || r < rows ? r : rows - 1) * cols +
-                                static_cast<int64_t>((u * 256) % kV + tid) * kPer;
+                                static_cast<int64_t>((u * kThreads) % kV + tid) * kPer;
             float a[kPer];
             float b[kPer];
             unpack16<T>(v[u], a);
@@ -303,7 +307,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_tile_kernel(
 #pragma unroll
     for (int r = 0; r < kRows; ++r) part[r] = 0.0f;
 #pragma unroll
-    for (int u = 0; u < kLoads; ++u) part[(u * 256) / kV] += sum_squares16<T>(v[u]);
+    for (int u = 0; u < kLoads; ++u) part[(u * kThreads) / kV] += sum_squares16<T>(v[u]);
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         part[r] = wave_reduce_f32<AddF32>(part[r]);
@@ -314,19 +318,53 @@ __global__ __launch_bounds__(kDefaultBlockSize) void rmsnorm_tile_kernel(
     bool row_finite[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-        const float total = (partials[0][r] + partials[1][r]) + (partials[2][r] + partials[3][r]);
+        float total = (partials[0][r] + partials[1][r]) + (partials[2][r] + partials[3][r]);
+        if constexpr (kWaves == 8) {
+            total = total + ((partials[4][r] + partials[5][r]) + (partials[6][r] + partials[7][r]));
+        }
         scale[r] = inv_rms(total, cols, eps);
         row_finite[r] = finite && __builtin_isfinite(total);
     }
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
-        const int r = (u * 256) / kV;
+        const int r = (u * kThreads) / kV;
         if (whole || row0 + r < rows) {
-            const int64_t off = (row0 + r) * cols + static_cast<int64_t>((u * 256) % kV + tid) * kPer;
+            const int64_t off =
+                (row0 + r) * cols + static_cast<int64_t>((u * kThreads) % kV + tid) * kPer;
             store_stream16(y + off, scale16<T>(v[u], g[u % kWeights], scale[r], row_finite[r]));
         }
     }
 }
+
+/// Launch shape of the tile kernel for one row width.
+template <int V, int L, int Th>
+struct TileShape {
+    static constexpr int kV = V;
+    static constexpr int kLoads = L;
+    static constexpr int kThreads = Th;
+    static constexpr int kRows = Th * L / V;
+};
+/// Shapes measured on MI355X ([16384, 4096] and [32768, 2048] bf16): plain
+/// RMSNorm is fastest with two row vectors per lane in 256-thread
+/// workgroups (77.8% of HBM peak against 76.1% with four; one per lane in
+/// 512-thread workgroups 69%); the fused residual form, which loads x and
+/// the residual for each vector, with one vector per lane (80.1% in
+/// 512-thread workgroups against 76.3% with four per lane). Rows of 1024
+/// vectors keep four per lane.
+template <int kV, bool kResidual>
+struct TileFor;
+template <bool kResidual>
+struct TileFor<256, kResidual> {
+    using type = TileShape<256, kResidual ? 1 : 2, 256>;
+};
+template <bool kResidual>
+struct TileFor<512, kResidual> {
+    using type = std::conditional_t<kResidual, TileShape<512, 1, 512>, TileShape<512, 2, 256>>;
+};
+template <bool kResidual>
+struct TileFor<1024, kResidual> {
+    using type = TileShape<1024, 4, 256>;
+};
 
 /// Any shape and alignment: one workgroup per row, two passes over the row.
 template <typename T, bool kResidual>
@@ -392,26 +430,33 @@ cf_status dispatch(const void* x, const void* residual, const void* w, void* y,
     if (kResidual) vec = vec && host_aligned(residual, 16) && host_aligned(residual_out, 16);
     const int64_t vectors_per_lane = ceil_div<int64_t>(cols / kPer, kWaveSize);
     const int64_t row_vectors = cols / kPer;
-    // The tiled kernel wins once there are several rounds of workgroups
-    // (measured on [16384, 2048 / 4096 / 8192] bf16: 1-3 points of HBM
-    // peak); with a single round ([4096, 4096] bf16, 2048 workgroups) the
-    // wave kernel is faster.
-    const int64_t tile_groups = (row_vectors == 256 || row_vectors == 512 || row_vectors == 1024)
-                                    ? ceil_div<int64_t>(rows, 1024 / row_vectors)
-                                    : 0;
-    if (vec && tile_groups >= 16 * static_cast<int64_t>(cu_count())) {
+    // The tiled kernel wins once the matrix holds at least 16 x 1024
+    // 16-byte vectors per CU, several rounds of workgroups (measured on [16384,
+    // 2048 / 4096 / 8192] bf16: 1-3 points of HBM peak); below that
+    // ([4096, 4096] bf16) the wave kernel is faster.
+    using Tile256 = typename TileFor<256, kResidual>::type;
+    using Tile512 = typename TileFor<512, kResidual>::type;
+    using Tile1024 = typename TileFor<1024, kResidual>::type;
+    const int64_t tile_rows = row_vectors == 256    ? Tile256::kRows
+                              : row_vectors == 512  ? Tile512::kRows
+                              : row_vectors == 1024 ? Tile1024::kRows
+                                                    : 0;  // rows per tile workgroup
+    const int64_t tile_groups = tile_rows > 0 ? ceil_div<int64_t>(rows, tile_rows) : 0;
+    if (vec && tile_rows > 0 && rows * row_vectors >= 16 * 1024 * static_cast<int64_t>(cu_count())) {
         const auto grid = static_cast<unsigned>(tile_groups);
-        auto run = [&](auto kernel) {
-            launch(kernel, dim3(grid), dim3(kDefaultBlockSize), 0, stream,
-                   static_cast<const T*>(x), static_cast<const T*>(residual), static_cast<const T*>(w),
-                   static_cast<T*>(y), static_cast<T*>(residual_out), rows, cols, eps);
+        auto run = [&](auto shape) {
+            using S = decltype(shape);
+            launch(rmsnorm_tile_kernel<T, S::kV, S::kLoads, S::kThreads, kResidual>, dim3(grid),
+                   dim3(S::kThreads), 0, stream, static_cast<const T*>(x),
+                   static_cast<const T*>(residual), static_cast<const T*>(w), static_cast<T*>(y),
+                   static_cast<T*>(residual_out), rows, cols, eps);
         };
         if (row_vectors == 256) {
-            run(rmsnorm_tile_kernel<T, 256, kResidual>);
+            run(Tile256{});
         } else if (row_vectors == 512) {
-            run(rmsnorm_tile_kernel<T, 512, kResidual>);
+            run(Tile512{});
         } else {
-            run(rmsnorm_tile_kernel<T, 1024, kResidual>);
+            run(Tile1024{});
         }
     } else if (vec && vectors_per_lane <= 16) {
         if (vectors_per_lane <= 1) {

@@ -158,9 +158,13 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_block_kernel(const 
 
 template <typename Tin, typename Tout, int kVecs>
 void launch_wave(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t stream) {
-    // Rows per wave: up to 8 16-byte loads in flight per lane, but never so
-    // many rows per wave that fewer waves than SIMDs (4 per CU) would run.
-    constexpr int kRows = kVecs >= 8 ? 1 : 8 / kVecs;
+    // Rows per wave: two for rows of one 16-byte vector per lane, else one.
+    // More loads in flight per lane are slower, not faster: on [131072, 512]
+    // bf16 eight rows per wave (eight 16-byte loads per lane before the
+    // first store) ran at 70% of HBM peak, one or two at 78.7%; a plain
+    // copy shows the same (8 loads per lane 50%, 1-2 loads 77-79%). Never
+    // so many rows per wave that fewer waves than SIMDs (4 per CU) would run.
+    constexpr int kRows = kVecs >= 2 ? 1 : 2;
     const int64_t simds = static_cast<int64_t>(cu_count()) * 4;
     const int64_t grid_rows = ceil_div<int64_t>(rows, kRows) >= simds ? kRows : 1;
     const int64_t waves = ceil_div<int64_t>(rows, grid_rows);
