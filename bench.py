@@ -589,7 +589,9 @@ def bench_fp8(torch, cf, warmup: int, runs: int) -> dict:
 
 
 def bench_bulk_quant(torch, cf, warmup: int) -> dict:
-    """config 5: every weight of a 7B model, bf16 -> int8 + scales -> bf16."""
+    """config 5: every weight of a 7B model, bf16 -> int8 + scales -> bf16, through the
+    grouped entry points (aggregate) and one call per tensor (for comparison, and
+    per-tensor rates)."""
     gen = torch.Generator(device="cuda").manual_seed(5)
     shapes = [(4096, 4096)] * 4 + [(11008, 4096)] * 2 + [(4096, 11008)]
     lib = cf._lib.load()
@@ -614,8 +616,26 @@ def bench_bulk_quant(torch, cf, warmup: int) -> dict:
         for (_, t), q, s, y in zip(tensors, q_all, s_all, y_all):
             cf._lib.check(lib.cf_dequantize_int8(q.data_ptr(), s.data_ptr(), y.data_ptr(), cf._lib.CF_BF16, t.numel(), stream))
 
-    qt = summary(time_launches(torch, [quant_all], 1, 3))
-    dt = summary(time_launches(torch, [dequant_all], 1, 3))
+    # The same weight set through the grouped entry points: up to 48 tensors
+    # per launch (5 launches instead of 224).
+    ptr = cf._lib.pointer_array
+    x_ptrs = ptr([t.data_ptr() for _, t in tensors])
+    q_ptrs = ptr([q.data_ptr() for q in q_all])
+    s_ptrs = ptr([s.data_ptr() for s in s_all])
+    y_ptrs = ptr([y.data_ptr() for y in y_all])
+    counts = cf._lib.int64_array([t.numel() for _, t in tensors])
+
+    def quant_group():
+        cf._lib.check(lib.cf_quantize_int8_group(x_ptrs, cf._lib.CF_BF16, q_ptrs, s_ptrs, counts, len(tensors), stream))
+
+    def dequant_group():
+        cf._lib.check(lib.cf_dequantize_int8_group(q_ptrs, s_ptrs, y_ptrs, cf._lib.CF_BF16, counts, len(tensors),
+                                                   stream))
+
+    qt = summary(time_launches(torch, [quant_group], 1, 3))
+    dt = summary(time_launches(torch, [dequant_group], 1, 3))
+    qt1 = summary(time_launches(torch, [quant_all], 1, 3))
+    dt1 = summary(time_launches(torch, [dequant_all], 1, 3))
     qb = sum(bytes_quant(t.numel(), 2) for _, t in tensors)
     db = sum(bytes_dequant(t.numel(), 2) for _, t in tensors)
     for label in sorted({lbl for lbl, _ in tensors}):
@@ -631,10 +651,14 @@ def bench_bulk_quant(torch, cf, warmup: int) -> dict:
         per_shape[label] = {"quantize_GB/s": gbs(bytes_quant(n, 2), tq["median_ms"]),
                             "dequantize_GB/s": gbs(bytes_dequant(n, 2), td["median_ms"])}
     return {
-        "bulk_7b_quantize_bf16": {"elements": total_n, "bytes": qb, "ms": qt["median_ms"],
+        "bulk_7b_quantize_bf16": {"elements": total_n, "bytes": qb, "ms": qt["median_ms"], "entry": "grouped",
                                   "GB/s": gbs(qb, qt["median_ms"]), "frac_hbm": gbs(qb, qt["median_ms"]) / PEAK_HBM_GBS},
-        "bulk_7b_dequantize_bf16": {"elements": total_n, "bytes": db, "ms": dt["median_ms"],
+        "bulk_7b_dequantize_bf16": {"elements": total_n, "bytes": db, "ms": dt["median_ms"], "entry": "grouped",
                                     "GB/s": gbs(db, dt["median_ms"]), "frac_hbm": gbs(db, dt["median_ms"]) / PEAK_HBM_GBS},
+        "bulk_7b_quantize_bf16_per_tensor_calls": {
+            "ms": qt1["median_ms"], "GB/s": gbs(qb, qt1["median_ms"]), "frac_hbm": gbs(qb, qt1["median_ms"]) / PEAK_HBM_GBS},
+        "bulk_7b_dequantize_bf16_per_tensor_calls": {
+            "ms": dt1["median_ms"], "GB/s": gbs(db, dt1["median_ms"]), "frac_hbm": gbs(db, dt1["median_ms"]) / PEAK_HBM_GBS},
         "bulk_7b_per_tensor_warm": per_shape,
     }
 

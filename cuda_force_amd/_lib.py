@@ -70,6 +70,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_quant_scale_count": (_I64, [_I64]),
     "cf_quantize_int8": (_I32, [_P, _I32, _P, _P, _I64, _P]),
     "cf_dequantize_int8": (_I32, [_P, _P, _P, _I32, _I64, _P]),
+    "cf_quantize_int8_group": (_I32, [_P, _I32, _P, _P, _P, _I64, _P]),
+    "cf_dequantize_int8_group": (_I32, [_P, _P, _P, _I32, _P, _I64, _P]),
     "cf_quantize_dequantize": (_I32, [_P, _P, _I32, _I64, _P]),
     "cf_rmsnorm": (_I32, [_P, _P, _P, _I32, _I64, _I64, _F, _P]),
     "cf_fused_residual_rmsnorm": (_I32, [_P, _P, _P, _P, _P, _I32, _I64, _I64, _F, _P]),
@@ -174,6 +176,16 @@ def dtype_code(dtype: object) -> int:
 
 
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+
+
+def pointer_array(values) -> ctypes.Array:
+    """A host array of device pointers (ints) for the grouped entry points."""
+    return (ctypes.c_void_p * max(len(values), 1))(*values)
+
+
+def int64_array(values) -> ctypes.Array:
+    """A host array of int64 counts for the grouped entry points."""
+    return (ctypes.c_int64 * max(len(values), 1))(*values)
 
 
 @lru_cache(maxsize=1)

@@ -203,9 +203,13 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
 }
 
-/// fp32 -> fp16, round-to-nearest-even (v_cvt_f16_f32 under the default mode).
+/// fp32 -> fp16, round-to-nearest-even (v_cvt_f16_f32 under the default
+/// mode); a NaN becomes its sign over the quiet NaN 0x7E00, the rule of
+/// c10::Half's conversion (what `.to(torch.float16)` gives), which the
+/// hardware conversion does not follow for every NaN.
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
-    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+    const uint32_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+    return f != f ? (((__float_as_uint(f) >> 16) & 0x8000u) | 0x7E00u) : h;
 }
 
 /// Storage traits: element type, how many fit a 16-byte vector, conversions.

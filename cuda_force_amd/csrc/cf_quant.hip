@@ -121,14 +121,12 @@ __device__ __forceinline__ void load_lane(const T* __restrict__ x, int64_t e, in
 template <typename T, bool kVec, int kMode, bool kFull>
 __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __restrict__ q,
                                            float* __restrict__ scales, T* __restrict__ y,
-                                           int64_t count) {
+                                           int64_t count, int64_t wave) {
     constexpr int kPer = Storage<T>::kPerVec;                  // 4 (fp32) or 8 (16-bit)
     constexpr int kLanesPerBlock = kQuantBlockSize / kPer;     // 16 or 8
     constexpr int kBlocksPerStep = kWaveSize / kLanesPerBlock; // 4 or 8
 
     const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveSize) +
-                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
     const int64_t base_block = wave * (kBlocksPerStep * kUnroll);
     const int sub = lane / kLanesPerBlock;
     const int part = lane % kLanesPerBlock;
@@ -222,15 +220,23 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
     }
 }
 
-/// True when every element of this wave's quantisation blocks is below
+/// Index of the calling wave in the grid (wave-uniform).
+__device__ __forceinline__ int64_t grid_wave() {
+    return static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveSize) +
+           static_cast<int64_t>(threadIdx.x) / kWaveSize;
+}
+
+/// Quantisation blocks one wave covers.
+template <typename T>
+constexpr int64_t quant_blocks_per_wave() {
+    return (kWaveSize / (kQuantBlockSize / Storage<T>::kPerVec)) * kUnroll;
+}
+
+/// True when every element of wave `wave`'s quantisation blocks is below
 /// `count` (wave-uniform).
 template <typename T>
-__device__ __forceinline__ bool wave_is_full(int64_t count) {
-    constexpr int kPer = Storage<T>::kPerVec;
-    constexpr int64_t kBlocksPerWave = (kWaveSize / (kQuantBlockSize / kPer)) * kUnroll;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveSize) +
-                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
-    return (wave + 1) * kBlocksPerWave * kQuantBlockSize <= count;
+__device__ __forceinline__ bool wave_is_full(int64_t count, int64_t wave) {
+    return (wave + 1) * quant_blocks_per_wave<T>() * kQuantBlockSize <= count;
 }
 
 template <typename T, bool kVec>
@@ -238,10 +244,11 @@ __global__ __launch_bounds__(kDefaultBlockSize) void quantize_kernel(const T* __
                                                                      int8_t* __restrict__ q,
                                                                      float* __restrict__ scales,
                                                                      int64_t count) {
-    if (kVec && wave_is_full<T>(count)) {
-        quant_body<T, kVec, 0, true>(x, q, scales, nullptr, count);
+    const int64_t wave = grid_wave();
+    if (kVec && wave_is_full<T>(count, wave)) {
+        quant_body<T, kVec, 0, true>(x, q, scales, nullptr, count, wave);
     } else {
-        quant_body<T, kVec, 0, false>(x, q, scales, nullptr, count);
+        quant_body<T, kVec, 0, false>(x, q, scales, nullptr, count, wave);
     }
 }
 
@@ -249,10 +256,11 @@ template <typename T, bool kVec>
 __global__ __launch_bounds__(kDefaultBlockSize) void fake_quant_kernel(const T* __restrict__ x,
                                                                        T* __restrict__ y,
                                                                        int64_t count) {
-    if (kVec && wave_is_full<T>(count)) {
-        quant_body<T, kVec, 1, true>(x, nullptr, nullptr, y, count);
+    const int64_t wave = grid_wave();
+    if (kVec && wave_is_full<T>(count, wave)) {
+        quant_body<T, kVec, 1, true>(x, nullptr, nullptr, y, count, wave);
     } else {
-        quant_body<T, kVec, 1, false>(x, nullptr, nullptr, y, count);
+        quant_body<T, kVec, 1, false>(x, nullptr, nullptr, y, count, wave);
     }
 }
 
@@ -263,12 +271,11 @@ __global__ __launch_bounds__(kDefaultBlockSize) void fake_quant_kernel(const T* 
 template <typename Tout, bool kVec, bool kFull>
 __device__ __forceinline__ void dequantize_body(const int8_t* __restrict__ q,
                                                 const float* __restrict__ scales,
-                                                Tout* __restrict__ y, int64_t count) {
+                                                Tout* __restrict__ y, int64_t count,
+                                                int64_t wave) {
     constexpr int kPer = Storage<Tout>::kPerVec;
     constexpr int64_t kStep = static_cast<int64_t>(kWaveSize) * kPer;
     const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveSize) +
-                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
     const int64_t base = wave * kStep * kUnroll + static_cast<int64_t>(lane) * kPer;
 
     int codes[kUnroll][kPer];
@@ -314,18 +321,21 @@ __device__ __forceinline__ void dequantize_body(const int8_t* __restrict__ q,
     }
 }
 
+/// Elements one dequantising wave covers.
+template <typename Tout>
+constexpr int64_t dequant_elements_per_wave() {
+    return static_cast<int64_t>(kWaveSize) * Storage<Tout>::kPerVec * kUnroll;
+}
+
 template <typename Tout, bool kVec>
 __global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
     const int8_t* __restrict__ q, const float* __restrict__ scales, Tout* __restrict__ y,
     int64_t count) {
-    constexpr int64_t kPerWave =
-        static_cast<int64_t>(kWaveSize) * Storage<Tout>::kPerVec * kUnroll;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveSize) +
-                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
-    if (kVec && (wave + 1) * kPerWave <= count) {
-        dequantize_body<Tout, kVec, true>(q, scales, y, count);
+    const int64_t wave = grid_wave();
+    if (kVec && (wave + 1) * dequant_elements_per_wave<Tout>() <= count) {
+        dequantize_body<Tout, kVec, true>(q, scales, y, count, wave);
     } else {
-        dequantize_body<Tout, kVec, false>(q, scales, y, count);
+        dequantize_body<Tout, kVec, false>(q, scales, y, count, wave);
     }
 }
 
@@ -347,6 +357,81 @@ int64_t dequant_grid(int64_t count) {
 }
 
 constexpr int64_t kMaxGrid = 2147483647;
+
+// ---------------------------------------------------------------------------
+// Grouped launches: up to CF_QUANT_GROUP_MAX tensors per kernel, described in
+// the kernel arguments (no device-side staging, nothing allocated). Tensor t
+// owns grid waves [first_wave[t], first_wave[t + 1]); each wave finds its
+// tensor by a binary search over first_wave (scalar loads from the kernel
+// argument segment) and then runs the single-tensor body with its index
+// inside that tensor. Every tensor of a group is vector-aligned.
+// ---------------------------------------------------------------------------
+
+constexpr int kGroupMax = CF_QUANT_GROUP_MAX;
+
+struct QuantGroupArgs {
+    const void* x[kGroupMax];
+    int8_t* q[kGroupMax];
+    float* scales[kGroupMax];
+    int64_t count[kGroupMax];
+    int64_t first_wave[kGroupMax + 1];
+    int n;
+};
+
+struct DequantGroupArgs {
+    const int8_t* q[kGroupMax];
+    const float* scales[kGroupMax];
+    void* y[kGroupMax];
+    int64_t count[kGroupMax];
+    int64_t first_wave[kGroupMax + 1];
+    int n;
+};
+
+/// Index t with first_wave[t] <= wave < first_wave[t + 1] (wave-uniform;
+/// the caller has checked wave < first_wave[n]).
+__device__ __forceinline__ int group_member(const int64_t* first_wave, int n, int64_t wave) {
+    int lo = 0;
+    int hi = n;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (first_wave[mid] <= wave) {
+            lo = mid;
+        } else {
+            hi = mid;
+        }
+    }
+    return lo;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kDefaultBlockSize) void quantize_group_kernel(QuantGroupArgs args) {
+    const int64_t gw = grid_wave();
+    if (gw >= args.first_wave[args.n]) return;  // wave-uniform
+    const int t = group_member(args.first_wave, args.n, gw);
+    const int64_t wave = gw - args.first_wave[t];
+    const T* x = static_cast<const T*>(args.x[t]);
+    const int64_t count = args.count[t];
+    if (wave_is_full<T>(count, wave)) {
+        quant_body<T, true, 0, true>(x, args.q[t], args.scales[t], nullptr, count, wave);
+    } else {
+        quant_body<T, true, 0, false>(x, args.q[t], args.scales[t], nullptr, count, wave);
+    }
+}
+
+template <typename Tout>
+__global__ __launch_bounds__(kDefaultBlockSize) void dequantize_group_kernel(DequantGroupArgs args) {
+    const int64_t gw = grid_wave();
+    if (gw >= args.first_wave[args.n]) return;  // wave-uniform
+    const int t = group_member(args.first_wave, args.n, gw);
+    const int64_t wave = gw - args.first_wave[t];
+    Tout* y = static_cast<Tout*>(args.y[t]);
+    const int64_t count = args.count[t];
+    if ((wave + 1) * dequant_elements_per_wave<Tout>() <= count) {
+        dequantize_body<Tout, true, true>(args.q[t], args.scales[t], y, count, wave);
+    } else {
+        dequantize_body<Tout, true, false>(args.q[t], args.scales[t], y, count, wave);
+    }
+}
 
 template <typename T>
 cf_status launch_quantize(const void* x, int8_t* q, float* scales, int64_t count,
@@ -402,10 +487,129 @@ cf_status launch_dequantize(const int8_t* q, const float* scales, void* y, int64
     return check_launch("launching dequantize_int8", stream);
 }
 
+/// Send one group (if any) and empty it.
+template <typename Kernel, typename Args>
+cf_status flush_group(Kernel kernel, Args& args, int64_t& waves, const char* what,
+                      hipStream_t stream) {
+    if (args.n == 0) return CF_OK;
+    args.first_wave[args.n] = waves;
+    const int64_t grid = ceil_div<int64_t>(waves, kDefaultBlockSize / kWaveSize);
+    CF_REQUIRE(grid <= kMaxGrid, "%s: a group exceeds the launch limit", what);
+    launch(kernel, dim3(static_cast<unsigned>(grid)), dim3(kDefaultBlockSize), 0, stream, args);
+    args.n = 0;
+    waves = 0;
+    return check_launch(what, stream);
+}
+
+template <typename T>
+cf_status launch_quantize_group(const void* const* x, int8_t* const* q, float* const* scales,
+                                const int64_t* counts, int64_t n, hipStream_t stream) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    constexpr const char* kWhat = "launching the grouped quantize_int8";
+    QuantGroupArgs args;
+    args.n = 0;
+    int64_t waves = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t count = counts[i];
+        if (count <= 0) continue;
+        CF_REQUIRE(x[i] != nullptr && q[i] != nullptr && scales[i] != nullptr,
+                   "cf_quantize_int8_group: null pointer in tensor %lld", static_cast<long long>(i));
+        if (!host_aligned(x[i], 16) || !host_aligned(q[i], kPer)) {
+            const cf_status status = launch_quantize<T>(x[i], q[i], scales[i], count, stream);
+            if (status != CF_OK) return status;
+            continue;
+        }
+        const int64_t blocks = ceil_div<int64_t>(count, kQuantBlockSize);
+        args.x[args.n] = x[i];
+        args.q[args.n] = q[i];
+        args.scales[args.n] = scales[i];
+        args.count[args.n] = count;
+        args.first_wave[args.n] = waves;
+        waves += ceil_div<int64_t>(blocks, quant_blocks_per_wave<T>());
+        if (++args.n == kGroupMax) {
+            const cf_status status = flush_group(quantize_group_kernel<T>, args, waves, kWhat, stream);
+            if (status != CF_OK) return status;
+        }
+    }
+    return flush_group(quantize_group_kernel<T>, args, waves, kWhat, stream);
+}
+
+template <typename T>
+cf_status launch_dequantize_group(const int8_t* const* q, const float* const* scales,
+                                  void* const* y, const int64_t* counts, int64_t n,
+                                  hipStream_t stream) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    constexpr const char* kWhat = "launching the grouped dequantize_int8";
+    DequantGroupArgs args;
+    args.n = 0;
+    int64_t waves = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t count = counts[i];
+        if (count <= 0) continue;
+        CF_REQUIRE(q[i] != nullptr && scales[i] != nullptr && y[i] != nullptr,
+                   "cf_dequantize_int8_group: null pointer in tensor %lld", static_cast<long long>(i));
+        if (!host_aligned(q[i], kPer) || !host_aligned(y[i], 16)) {
+            const cf_status status = launch_dequantize<T>(q[i], scales[i], y[i], count, stream);
+            if (status != CF_OK) return status;
+            continue;
+        }
+        args.q[args.n] = q[i];
+        args.scales[args.n] = scales[i];
+        args.y[args.n] = y[i];
+        args.count[args.n] = count;
+        args.first_wave[args.n] = waves;
+        waves += ceil_div<int64_t>(count, dequant_elements_per_wave<T>());
+        if (++args.n == kGroupMax) {
+            const cf_status status =
+                flush_group(dequantize_group_kernel<T>, args, waves, kWhat, stream);
+            if (status != CF_OK) return status;
+        }
+    }
+    return flush_group(dequantize_group_kernel<T>, args, waves, kWhat, stream);
+}
+
 }  // namespace
 }  // namespace cf
 
 extern "C" {
+
+cf_status cf_quantize_int8_group(const void* const* x, cf_dtype x_dtype, int8_t* const* q,
+                                 float* const* scales, const int64_t* counts, int64_t n_tensors,
+                                 void* stream) {
+    if (n_tensors <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && q != nullptr && scales != nullptr && counts != nullptr,
+               "cf_quantize_int8_group: null array");
+    auto s = static_cast<hipStream_t>(stream);
+    switch (x_dtype) {
+        case CF_F32:
+            return cf::launch_quantize_group<float>(x, q, scales, counts, n_tensors, s);
+        case CF_BF16:
+            return cf::launch_quantize_group<cf::bf16_t>(x, q, scales, counts, n_tensors, s);
+        case CF_F16:
+            return cf::launch_quantize_group<cf::f16_t>(x, q, scales, counts, n_tensors, s);
+    }
+    return cf::fail(CF_ERR_UNSUPPORTED, "cf_quantize_int8_group: unknown input dtype %d",
+                    static_cast<int>(x_dtype));
+}
+
+cf_status cf_dequantize_int8_group(const int8_t* const* q, const float* const* scales,
+                                   void* const* y, cf_dtype y_dtype, const int64_t* counts,
+                                   int64_t n_tensors, void* stream) {
+    if (n_tensors <= 0) return CF_OK;
+    CF_REQUIRE(q != nullptr && scales != nullptr && y != nullptr && counts != nullptr,
+               "cf_dequantize_int8_group: null array");
+    auto s = static_cast<hipStream_t>(stream);
+    switch (y_dtype) {
+        case CF_F32:
+            return cf::launch_dequantize_group<float>(q, scales, y, counts, n_tensors, s);
+        case CF_BF16:
+            return cf::launch_dequantize_group<cf::bf16_t>(q, scales, y, counts, n_tensors, s);
+        case CF_F16:
+            return cf::launch_dequantize_group<cf::f16_t>(q, scales, y, counts, n_tensors, s);
+    }
+    return cf::fail(CF_ERR_UNSUPPORTED, "cf_dequantize_int8_group: unknown output dtype %d",
+                    static_cast<int>(y_dtype));
+}
 
 int64_t cf_quant_scale_count(int64_t count) {
     return count <= 0 ? 0 : cf::ceil_div<int64_t>(count, cf::kQuantBlockSize);

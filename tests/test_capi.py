@@ -124,3 +124,23 @@ def test_time_next_launch_takes_both_events_or_neither(lib):
     assert lib.cf_time_next_launch(fake, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_time_next_launch(null, fake) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_time_next_launch(null, null) == _lib.CF_OK
+
+
+def test_grouped_quantisation_host_checks(lib):
+    null = ctypes.c_void_p(0)
+    # Nothing to do: returns before touching anything.
+    assert lib.cf_quantize_int8_group(null, _lib.CF_F32, null, null, null, 0, null) == _lib.CF_OK
+    assert lib.cf_dequantize_int8_group(null, null, null, _lib.CF_BF16, null, -3, null) == _lib.CF_OK
+    # Missing arrays are argument errors.
+    assert lib.cf_quantize_int8_group(null, _lib.CF_F32, null, null, null, 2, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_dequantize_int8_group(null, null, null, _lib.CF_F32, null, 1, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    # Empty members are skipped (no launch, no pointer check); a null pointer
+    # in a non-empty member is rejected before any launch.
+    ptrs = _lib.pointer_array([0, 0])
+    counts = _lib.int64_array([0, -1])
+    assert lib.cf_quantize_int8_group(ptrs, _lib.CF_F32, ptrs, ptrs, counts, 2, null) == _lib.CF_OK
+    counts = _lib.int64_array([0, 64])
+    assert lib.cf_quantize_int8_group(ptrs, _lib.CF_F32, ptrs, ptrs, counts, 2, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert b"tensor 1" in lib.cf_last_error()
+    assert lib.cf_dequantize_int8_group(ptrs, ptrs, ptrs, _lib.CF_F32, counts, 2, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_quantize_int8_group(ptrs, 7, ptrs, ptrs, counts, 2, null) == _lib.CF_ERR_UNSUPPORTED
