@@ -789,7 +789,7 @@ def main(argv: list[str] | None = None) -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "rmsnorm_tile_kernel<bf16, 512>",
+            "kernel": "rmsnorm_tile_kernel<bf16, 512 vectors, 2 per lane, 256 threads>",
             "achieved": achieved,
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
