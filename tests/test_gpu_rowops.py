@@ -139,7 +139,8 @@ def test_rmsnorm_tiled_kernel_non_finite_bits():
     assert_close(y[finite_rows][:, cols_ok], exact[finite_rows][:, cols_ok], "bf16", "non-finite neighbours")
 
 
-@pytest.mark.parametrize("dtype,shape", [("bf16", (8193, 4096)), ("f32", (4097, 4096))], ids=str)
+@pytest.mark.parametrize("dtype,shape", [("bf16", (8193, 4096)), ("f32", (4097, 4096)),
+                                         ("bf16", (16385, 2048)), ("f16", (16385, 2048))], ids=str)
 def test_fused_residual_rmsnorm_tiled_kernel(dtype, shape):
     g.announce(f"fused residual rmsnorm tiled {dtype} {shape}")
     r = rng(shape[0] + 3)
@@ -255,6 +256,19 @@ def test_config2_softmax_full_size():
     masked = np.arange(2048)[None, :] > np.arange(1024)[:, None]
     assert (g.host_values(y, "bf16")[masked] == 0).all()
     np.testing.assert_allclose(g.host_values(y, "bf16").astype(np.float64).sum(axis=1), 1.0, atol=2e-2)
+
+
+@pytest.mark.parametrize("dtype,shape", [("bf16", (4099, 512)), ("f32", (4097, 256)), ("bf16", (2049, 384))],
+                         ids=str)
+def test_softmax_two_rows_per_wave(dtype, shape):
+    """Rows of one 16-byte vector per lane at more than 2 x 1024 rows take two
+    rows per wave; an odd row count leaves the last wave one row."""
+    rows, cols = shape
+    g.announce(f"softmax two rows per wave {dtype} {shape}")
+    x = g.storage_bits(causal(rows, cols, rows), dtype)
+    y = run_softmax(x, dtype, dtype)
+    picked = np.concatenate([np.arange(16), rng(rows).choice(rows, 128, replace=False), np.arange(rows - 16, rows)])
+    assert_close(y[picked], oracle.softmax(g.host_values(x[picked], dtype)), dtype, f"softmax {dtype} {shape}")
 
 
 def test_softmax_in_place():
