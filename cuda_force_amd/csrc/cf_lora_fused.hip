@@ -123,7 +123,10 @@ struct FusedArgs {
     float* xa_out;
     int64_t M;
     int64_t N;
-    int64_t K;
+    int64_t K;        // row length of x (row stride) and rows of w
+    int64_t k_steps;  // K-steps (kBK each) per workgroup: even, >= 2; split K
+                      // (fp32 output only): slice blockIdx.y covers K-steps
+                      // [blockIdx.y * k_steps, +k_steps)
     int64_t rank;
     float scale;
     int tiles_m;
@@ -158,6 +161,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     const int64_t M = args.M;
     const int64_t N = args.N;
     const int64_t K = args.K;
+    const int64_t k_first = static_cast<int64_t>(blockIdx.y) * args.k_steps * kBK;
     const int64_t rank = args.rank;
 
     // ---- HBM -> LDS roles (each load instruction fills 1 KiB of LDS, lane l
@@ -214,7 +218,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     // one burst after the barrier.
     auto issue_w = [&](int64_t kt, int piece) {
         const uint32_t stage = lds_addr + kOffW + static_cast<uint32_t>(kt % kStages) * kStage;
-        const int64_t k0 = kt * kBK;
+        const int64_t k0 = k_first + kt * kBK;
         if (piece < 4) {
             const int vw = (wave & 3) + 4 * (piece >> 1);
             dma16(wbuf, stage + (vw * 2 + (piece & 1)) * 1024, w_dma[piece],
@@ -228,7 +232,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         const uint32_t slot = lds_addr + static_cast<uint32_t>(pair % kXSlots) * kXPair;
         const int vw = (wave & 3) + 4 * (piece >> 2);
         dma16(xbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
-              static_cast<uint32_t>(pair * 4 * kBK));
+              static_cast<uint32_t>(k_first * 2 + pair * 4 * kBK));
     };
     constexpr int kWLoads = kAdapter ? 5 : 4;  // w (+ a) DMA per K-step per issuing wave
     constexpr int kXLoads = 8;                 // x DMA per pair of K-steps per issuing wave
@@ -328,7 +332,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     // the latter wait for nothing but the barriers (their vmcnt waits find
     // no DMA of their own in flight).
     auto run = [&](auto issuer) {
-    const int64_t k_tiles = K / kBK;  // even, >= 2
+    const int64_t k_tiles = args.k_steps;  // even, >= 2
     auto issue_w_all = [&](int64_t kt) {
 #pragma unroll
         for (int piece = 0; piece < kWLoads; ++piece) issue_w(kt, piece);
@@ -515,7 +519,10 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         for (int jb = 0; jb < 8; ++jb) {
             const int64_t col = n0 + wn * 128 + 16 * jb + 4 * g;
             if (kOutF32 && col < N) {
-                *reinterpret_cast<f32x4_t*>(args.y32 + row * N + col) = acc[jb][i];
+                // Split K: slice blockIdx.y of the K range writes its own
+                // partial product.
+                *reinterpret_cast<f32x4_t*>(args.y32 + static_cast<int64_t>(blockIdx.y) * M * N +
+                                            row * N + col) = acc[jb][i];
             } else if (col < N) {
                 uint2 packed;
                 packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
@@ -555,6 +562,7 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
     args.M = M;
     args.N = N;
     args.K = K;
+    args.k_steps = K / kBK;
     args.rank = rank;
     args.scale = scale;
     args.tiles_m = static_cast<int>(ceil_div<int64_t>(M, kBM));
@@ -569,7 +577,9 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
 }
 
 cf_status launch_matmul_bf16_f32out(const void* x, const void* w, float* y, int64_t M, int64_t N,
-                                    int64_t K, hipStream_t stream) {
+                                    int64_t K, int splits, hipStream_t stream) {
+    CF_REQUIRE(splits >= 1 && K % (splits * 2 * kBK) == 0,
+               "bf16 MFMA matmul: K = %lld does not split %d ways", static_cast<long long>(K), splits);
     FusedArgs args{};
     args.x = static_cast<const uint16_t*>(x);
     args.w = static_cast<const uint16_t*>(w);
@@ -577,10 +587,11 @@ cf_status launch_matmul_bf16_f32out(const void* x, const void* w, float* y, int6
     args.M = M;
     args.N = N;
     args.K = K;
+    args.k_steps = K / kBK / splits;
     args.tiles_m = static_cast<int>(ceil_div<int64_t>(M, kBM));
     args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
     const int grid = args.tiles_m * args.tiles_n;
-    launch(lora_fused_bf16_kernel<false, true>, dim3(grid), dim3(kThreads), 0, stream, args);
+    launch(lora_fused_bf16_kernel<false, true>, dim3(grid, splits), dim3(kThreads), 0, stream, args);
     return check_launch("launching the bf16 MFMA matmul (fp32 output)", stream);
 }
 

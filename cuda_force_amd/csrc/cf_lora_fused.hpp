@@ -20,8 +20,10 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
 
 /// y (fp32) = x @ w for bf16 x [M, K] and w [K, N] on the same kernel
 /// (rank 0, fp32 stores); same eligibility as lora_fused_eligible with rank 0
-/// and a 16-byte aligned y.
+/// and a 16-byte aligned y. With splits > 1 (K a multiple of 64 * splits)
+/// the K range is cut into `splits` slices and y holds splits consecutive
+/// [M, N] partial products, slice s's at y + s * M * N, for the caller to sum.
 cf_status launch_matmul_bf16_f32out(const void* x, const void* w, float* y, int64_t M, int64_t N,
-                                    int64_t K, hipStream_t stream);
+                                    int64_t K, int splits, hipStream_t stream);
 
 }  // namespace cf

@@ -19,6 +19,13 @@
 // is more accurate than TF32 (about 16 significant bits per product against
 // 11) at three bf16 MFMA passes; A' and B' live in a caller workspace.
 //
+// Small outputs split K: with few 256 x 256 output tiles (1024 x 1024 is 16
+// tiles, 16 of 256 CUs), the K' range is cut into up to 8 slices (at most 256
+// workgroups); each slice writes an fp32 partial product into the workspace
+// and sum_splits_kernel adds them in slice order (the result is
+// deterministic and independent of the device). Both operand splits run as
+// one launch.
+//
 // Shapes: any m and k; n a multiple of 8 (16-byte output rows), and the
 // tensors 16-byte aligned. The reference accepted m, n multiples of 16 and k
 // a multiple of 8; every shape it took is taken here.
@@ -28,68 +35,113 @@
 namespace cf {
 namespace {
 
-constexpr int64_t kPad = 64;  // K granule of the MFMA kernel
+constexpr int64_t kPad = 64;          // K granule of the MFMA kernel
+constexpr int64_t kTile = 256;        // output tile edge of the MFMA kernel
+// Measured on MI355X: 1024^3 runs fastest with 8 slices (128 workgroups;
+// 16 slices: 10% slower), 2048^3 with 4 (256 workgroups; 2 slices: 17%
+// slower).
+constexpr int64_t kSplitTarget = 256;  // workgroups split K may fill
+constexpr int kMaxSplits = 8;
 
 int64_t padded_k(int64_t k) { return ceil_div<int64_t>(k, kPad) * kPad; }
+
+/// Slices of the K' = 3 kp range: the largest power of two up to 8 that
+/// divides K' into whole granules and keeps tiles x slices <= 256. A
+/// function of the shape alone.
+int k_splits(int64_t m, int64_t n, int64_t kk) {
+    const int64_t tiles = ceil_div<int64_t>(m, kTile) * ceil_div<int64_t>(n, kTile);
+    const int64_t granules = kk / kPad;
+    int splits = 1;
+    for (int s = 2; s <= kMaxSplits; s *= 2) {
+        if (tiles * s <= kSplitTarget && granules % s == 0) splits = s;
+    }
+    return splits;
+}
+
+/// c = sum over slices of part[s] (s = 0, 1, ...), four floats per thread.
+__global__ void sum_splits_kernel(const float4* __restrict__ part, float4* __restrict__ c,
+                                  int64_t quads, int splits) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < quads;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        float4 total = part[i];
+        for (int s = 1; s < splits; ++s) {
+            const float4 v = part[s * quads + i];
+            total.x += v.x;
+            total.y += v.y;
+            total.z += v.z;
+            total.w += v.w;
+        }
+        c[i] = total;
+    }
+}
 
 __device__ __forceinline__ void split_bf16(float a, uint32_t& hi, uint32_t& lo) {
     hi = f32_to_bf16_bits(a);
     lo = f32_to_bf16_bits(a - __uint_as_float(hi << 16));
 }
 
-/// A' [m][3 kp]: thread -> 4 consecutive columns of one row.
-__global__ void split_rows_kernel(const float* __restrict__ a, uint16_t* __restrict__ out, int64_t m,
-                                  int64_t k, int64_t kp) {
+/// A' [m][3 kp] element quad q (4 consecutive columns of one row).
+__device__ __forceinline__ void split_row_quad(const float* __restrict__ a, uint16_t* __restrict__ out,
+                                               int64_t k, int64_t kp, int64_t q) {
     const int64_t quads_per_row = 3 * kp / 4;
-    const int64_t total = m * quads_per_row;
-    for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
-         idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t row = idx / quads_per_row;
-        const int64_t col = (idx % quads_per_row) * 4;
-        const int64_t part = col / kp;  // 0, 1: hi; 2: lo
-        const int64_t j = col % kp;
-        uint32_t bits[4];
+    const int64_t row = q / quads_per_row;
+    const int64_t col = (q % quads_per_row) * 4;
+    const int64_t part = col / kp;  // 0, 1: hi; 2: lo
+    const int64_t j = col % kp;
+    uint32_t bits[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float v = j + e < k ? a[row * k + j + e] : 0.0f;
-            uint32_t hi;
-            uint32_t lo;
-            split_bf16(v, hi, lo);
-            bits[e] = part == 2 ? lo : hi;
-        }
-        uint2 packed;
-        packed.x = bits[0] | (bits[1] << 16);
-        packed.y = bits[2] | (bits[3] << 16);
-        *reinterpret_cast<uint2*>(out + row * 3 * kp + col) = packed;
+    for (int e = 0; e < 4; ++e) {
+        const float v = j + e < k ? a[row * k + j + e] : 0.0f;
+        uint32_t hi;
+        uint32_t lo;
+        split_bf16(v, hi, lo);
+        bits[e] = part == 2 ? lo : hi;
     }
+    uint2 packed;
+    packed.x = bits[0] | (bits[1] << 16);
+    packed.y = bits[2] | (bits[3] << 16);
+    *reinterpret_cast<uint2*>(out + row * 3 * kp + col) = packed;
 }
 
-/// B' [3 kp][n]: thread -> 4 consecutive columns of one row.
-__global__ void split_cols_kernel(const float* __restrict__ b, uint16_t* __restrict__ out, int64_t k,
-                                  int64_t n, int64_t kp) {
+/// B' [3 kp][n] element quad q (4 consecutive columns of one row).
+__device__ __forceinline__ void split_col_quad(const float* __restrict__ b, uint16_t* __restrict__ out,
+                                               int64_t k, int64_t n, int64_t kp, int64_t q) {
     const int64_t quads_per_row = n / 4;
-    const int64_t total = 3 * kp * quads_per_row;
-    for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
-         idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t row = idx / quads_per_row;  // 0 .. 3 kp - 1
-        const int64_t col = (idx % quads_per_row) * 4;
-        const int64_t part = row / kp;  // 0, 2: hi; 1: lo
-        const int64_t j = row % kp;
-        float4 v = float4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (j < k) v = *reinterpret_cast<const float4*>(b + j * n + col);
-        const float vals[4] = {v.x, v.y, v.z, v.w};
-        uint32_t bits[4];
+    const int64_t row = q / quads_per_row;  // 0 .. 3 kp - 1
+    const int64_t col = (q % quads_per_row) * 4;
+    const int64_t part = row / kp;  // 0, 2: hi; 1: lo
+    const int64_t j = row % kp;
+    float4 v = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (j < k) v = *reinterpret_cast<const float4*>(b + j * n + col);
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+    uint32_t bits[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            uint32_t hi;
-            uint32_t lo;
-            split_bf16(vals[e], hi, lo);
-            bits[e] = part == 1 ? lo : hi;
+    for (int e = 0; e < 4; ++e) {
+        uint32_t hi;
+        uint32_t lo;
+        split_bf16(vals[e], hi, lo);
+        bits[e] = part == 1 ? lo : hi;
+    }
+    uint2 packed;
+    packed.x = bits[0] | (bits[1] << 16);
+    packed.y = bits[2] | (bits[3] << 16);
+    *reinterpret_cast<uint2*>(out + row * n + col) = packed;
+}
+
+/// Both operand splits in one launch: quads [0, a_quads) of the grid-stride
+/// range are A', the rest B'.
+__global__ void split_operands_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                      uint16_t* __restrict__ a_out, uint16_t* __restrict__ b_out,
+                                      int64_t m, int64_t n, int64_t k, int64_t kp) {
+    const int64_t a_quads = m * 3 * kp / 4;
+    const int64_t total = a_quads + 3 * kp * n / 4;
+    for (int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; q < total;
+         q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        if (q < a_quads) {
+            split_row_quad(a, a_out, k, kp, q);
+        } else {
+            split_col_quad(b, b_out, k, n, kp, q - a_quads);
         }
-        uint2 packed;
-        packed.x = bits[0] | (bits[1] << 16);
-        packed.y = bits[2] | (bits[3] << 16);
-        *reinterpret_cast<uint2*>(out + row * n + col) = packed;
     }
 }
 
@@ -117,7 +169,10 @@ size_t cf_matmul_tensor_core_workspace_bytes(int64_t m, int64_t n, int64_t k) {
     if (!cf_matmul_tensor_core_shape_supported(m, n, k)) return 0;
     const int64_t kk = 3 * cf::padded_k(k);
     const size_t a_bytes = static_cast<size_t>(m * kk) * 2;
-    return ((a_bytes + 255) / 256) * 256 + static_cast<size_t>(kk * n) * 2;
+    const size_t b_bytes = static_cast<size_t>(kk * n) * 2;
+    const int splits = cf::k_splits(m, n, kk);
+    const size_t part_bytes = splits > 1 ? static_cast<size_t>(splits) * m * n * 4 : 0;
+    return ((a_bytes + 255) / 256) * 256 + ((b_bytes + 255) / 256) * 256 + part_bytes;
 }
 
 cf_status cf_matmul_tensor_core(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
@@ -140,14 +195,24 @@ cf_status cf_matmul_tensor_core(const float* a, const float* b, float* c, int64_
     }
     const int64_t kp = cf::padded_k(k);
     const size_t a_bytes = static_cast<size_t>(m * 3 * kp) * 2;
+    const size_t b_bytes = static_cast<size_t>(3 * kp * n) * 2;
     auto* a_split = static_cast<uint16_t*>(workspace);
     auto* b_split = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(workspace) + ((a_bytes + 255) / 256) * 256);
+    auto* partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ((a_bytes + 255) / 256) * 256 +
+                                              ((b_bytes + 255) / 256) * 256);
+    const int splits = cf::k_splits(m, n, 3 * kp);
     auto s = static_cast<hipStream_t>(stream);
-    cf::split_rows_kernel<<<cf::split_grid(m * 3 * kp / 4), cf::kDefaultBlockSize, 0, s>>>(a, a_split, m, k, kp);
-    cf::split_cols_kernel<<<cf::split_grid(3 * kp * n / 4), cf::kDefaultBlockSize, 0, s>>>(b, b_split, k, n, kp);
+    cf::launch(cf::split_operands_kernel, dim3(cf::split_grid(m * 3 * kp / 4 + 3 * kp * n / 4)),
+               dim3(cf::kDefaultBlockSize), 0, s, a, b, a_split, b_split, m, n, k, kp);
     const cf_status split = cf::check_launch("splitting the fp32 operands into bf16 parts", s);
     if (split != CF_OK) return split;
-    return cf::launch_matmul_bf16_f32out(a_split, b_split, c, m, n, 3 * kp, s);
+    if (splits == 1) return cf::launch_matmul_bf16_f32out(a_split, b_split, c, m, n, 3 * kp, 1, s);
+    const cf_status gemm = cf::launch_matmul_bf16_f32out(a_split, b_split, partials, m, n, 3 * kp, splits, s);
+    if (gemm != CF_OK) return gemm;
+    const int64_t quads = m * n / 4;  // n is a multiple of 8
+    cf::launch(cf::sum_splits_kernel, dim3(cf::split_grid(quads)), dim3(cf::kDefaultBlockSize), 0, s,
+               reinterpret_cast<const float4*>(partials), reinterpret_cast<float4*>(c), quads, splits);
+    return cf::check_launch("summing the split-K partial products", s);
 }
 
 }  // extern "C"

@@ -263,8 +263,11 @@ int cf_tensor_cores_available(void);
  * (cuda/include/cudaforge/tensor_core_matmul.cuh:51). */
 int cf_matmul_tensor_core_shape_supported(int64_t m, int64_t n, int64_t k);
 
-/* Workspace for the bf16 operand parts (0 for an unsupported shape). It has
- * no counterpart in the reference, whose TF32 kernel read fp32 directly. */
+/* Workspace for the bf16 operand parts and, for outputs of at most 128
+ * 256 x 256 tiles, the fp32 partial products of the split reduction range
+ * (2-8 slices)
+ * (0 for an unsupported shape). It has no counterpart in the reference, whose
+ * TF32 kernel read fp32 directly. */
 size_t cf_matmul_tensor_core_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
 /* c[m, n] = a[m, k] b[k, n], row-major fp32, on the bf16 MFMA units: each

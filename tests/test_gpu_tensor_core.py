@@ -111,3 +111,21 @@ def test_large_square():
     rows = [0, 1777, 4095]
     expected = a[rows].double() @ b.double()
     assert (got[rows].double() - expected).abs().max().item() <= 1e-4 * math.sqrt(n)
+
+
+@pytest.mark.parametrize("shape", [(1024, 1024, 1024), (2048, 1024, 2048), (512, 256, 4096)], ids=str)
+def test_split_reduction_range_is_accurate_and_deterministic(shape):
+    """Outputs of fewer than 128 tiles cut K' = 3 kp into 2-16 slices whose fp32
+    partial products are summed in slice order: as accurate as one pass, and
+    bit-identical from call to call."""
+    m, n, k = shape
+    announce(f"tensor-core matmul split K {shape}")
+    gen = torch.Generator(device="cuda").manual_seed(k + 3)
+    a = torch.randn(m, k, generator=gen, device="cuda")
+    b = torch.randn(k, n, generator=gen, device="cuda")
+    got = tensor_core(a, b)
+    again = tensor_core(a, b)
+    assert torch.equal(got.view(torch.int32), again.view(torch.int32))
+    rows = [0, m // 3, m - 1]
+    expected = a[rows].double() @ b.double()
+    assert (got[rows].double() - expected).abs().max().item() <= 1e-4 * math.sqrt(k)
