@@ -14,8 +14,9 @@
 //      64-row chunk goes HBM -> registers -> LDS; G partial rows = chunk @
 //      b^T (16x16x32 MFMA, row fragments by ds_read_b128, b fragments held in
 //      registers) and grad_b partials += bf16(xa)^T-chunk @ chunk (16x16x32
-//      MFMA; the xa fragments are read from the fp32 xa and rounded in
-//      registers, the m-contiguous operand by ds_read_b64_tr_b16). Partials
+//      MFMA; the chunk's fp32 xa arrives with one 16-byte load per thread
+//      and is rounded and transposed into LDS, the m-contiguous operand is
+//      read by ds_read_b64_tr_b16). Partials
 //      go to fp32 workspaces, one slice per 256-column tile (G) and per
 //      256-row tile (grad_b).
 //   2. One launch sums both in a fixed order: grad_b (times scale, cast) and
@@ -42,6 +43,7 @@ constexpr int kRankPad = 16;     // adapter rank padded to one MFMA dimension
 constexpr int kRowBytes = kTileCols * 2;
 constexpr int kPiecesPerThread = kChunkRows * kTileCols * 2 / 16 / kThreads;  // 8
 constexpr uint32_t kOutOfRange = 0x80000000u;
+constexpr int kXatStride = kChunkRows + 8;  // bf16 per row of the transposed xa chunk
 
 /// Chunk swizzle of the staged tile (512-byte rows of 32 16-byte chunks).
 /// Even, so transposed reads keep their 32-byte column pairs; distinct over
@@ -91,6 +93,9 @@ struct ColumnArgs {
 template <bool kRowDot>
 __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[kChunkRows * kRowBytes];  // 32 KiB
+    // dy pass: the chunk's xa, rounded to bf16 and transposed ([16 j][64 m],
+    // rows padded by 16 bytes); rows j >= rank stay zero.
+    __shared__ __attribute__((aligned(16))) uint16_t xat[kRowDot ? kRankPad : 1][kXatStride];
 
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & 63;
@@ -112,6 +117,25 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
     const int64_t piece_col = n0 + 8 * piece_chunk;
     const bool col_ok = piece_col < C;
     uint4 staged[kPiecesPerThread];
+    // dy pass: thread t also loads bytes 16 t .. +15 of the chunk's xa rows
+    // (64 x rank fp32, contiguous), i.e. flat elements 4 t .. 4 t + 3:
+    // element q is xa[row0 + xa_row[q]][xa_col[q]].
+    uint4 staged_xa = make_uint4(0u, 0u, 0u, 0u);
+    int xa_row[4];
+    int xa_col[4];
+    if constexpr (kRowDot) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int idx = 4 * tid + q;
+            xa_row[q] = idx / static_cast<int>(args.rank);
+            xa_col[q] = idx % static_cast<int>(args.rank);
+        }
+        // Rows j >= rank of the transposed chunk are never written: zero
+        // them once (the loop's first barrier orders this before any read).
+        for (int i = tid; i < kRankPad * kXatStride; i += kThreads) (&xat[0][0])[i] = 0;
+    }
+    const __amdgpu_buffer_rsrc_t xabuf = make_buffer(
+        args.xa, static_cast<uint32_t>(kRowDot ? args.M * args.rank * 4 : 0));
     auto load_chunk = [&](int64_t row0) {
 #pragma unroll
         for (int i = 0; i < kPiecesPerThread; ++i) {
@@ -120,12 +144,29 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
                 col_ok ? static_cast<uint32_t>((row * C + piece_col) * 2) : kOutOfRange;
             staged[i] = buffer_load16(vbuf, off, 0);
         }
+        if constexpr (kRowDot) {
+            // Past the chunk's kChunkRows x rank elements (rank < 16), or past
+            // M: zeros.
+            const uint32_t off = 4 * tid < kChunkRows * args.rank
+                                     ? static_cast<uint32_t>((row0 * args.rank + 4 * tid) * 4)
+                                     : kOutOfRange;
+            staged_xa = buffer_load16(xabuf, off, 0);
+        }
     };
     auto store_chunk = [&]() {
 #pragma unroll
         for (int i = 0; i < kPiecesPerThread; ++i) {
             const int row = 8 * i + (tid >> 5);
             *reinterpret_cast<uint4*>(tile + tile_offset(row, piece_chunk)) = staged[i];
+        }
+        if constexpr (kRowDot) {
+            if (4 * tid < kChunkRows * args.rank) {
+                const uint32_t v[4] = {staged_xa.x, staged_xa.y, staged_xa.z, staged_xa.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    xat[xa_col[q]][xa_row[q]] = static_cast<uint16_t>(f32_to_bf16_bits(__uint_as_float(v[q])));
+                }
+            }
         }
     };
 
@@ -164,24 +205,14 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
         if (chunk + 1 < kTileRows / kChunkRows) load_chunk(row0 + kChunkRows);
 
         // pt fragments: pt[j = lane % 16][row0 + 32 ms + 8 (lane / 16) .. +7].
-        // The dy pass reads them straight from xa ([M, rank] fp32, eight
-        // rows apart by `rank`), rounding to bf16 as the transposed copy would;
-        // rows past M and columns past the rank read as zero.
+        // The dy pass reads them from the transposed bf16 copy of the chunk's
+        // xa in LDS (rounded as the transposed copy of the x pass is); rows
+        // past M and columns past the rank are zero.
         bf16x8_t ptfrag[2];
 #pragma unroll
         for (int ms = 0; ms < 2; ++ms) {
             if constexpr (kRowDot) {
-                uint32_t bits[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int64_t m = row0 + 32 * ms + 8 * g + e;
-                    const uint32_t off =
-                        jl < args.rank ? static_cast<uint32_t>((m * args.rank + jl) * 4) : kOutOfRange;
-                    bits[e] = f32_to_bf16_bits(__uint_as_float(buffer_load4(ptbuf, off, 0)));
-                }
-                const uint4 packed = make_uint4(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16),
-                                                bits[4] | (bits[5] << 16), bits[6] | (bits[7] << 16));
-                ptfrag[ms] = as_bf16x8(packed);
+                ptfrag[ms] = *reinterpret_cast<const bf16x8_t*>(&xat[jl][32 * ms + 8 * g]);
             } else {
                 const uint32_t off =
                     static_cast<uint32_t>((jl * args.Mp + row0 + 32 * ms + 8 * g) * 2);
