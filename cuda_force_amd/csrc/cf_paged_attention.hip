@@ -176,14 +176,24 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(PagedArgs a) {
                                              ? group - static_cast<int64_t>(hgroup) * kGroup
                                              : kGroup);
 
-    float q[kGroup][kVals];
+    // fp32: q is widened and pre-scaled. bf16: q stays as packed pairs and
+    // a score is four v_dot2_f32_bf16 on the raw K piece (products of bf16
+    // values are exact in fp32, sums in fp32), scaled after the lane sum -
+    // no widening of K, a quarter of the multiply instructions.
+    constexpr bool kPacked = !std::is_same<T, float>::value;
+    float q[kGroup][kPacked ? 1 : kVals];
+    u32x4_t qp[kGroup];
 #pragma unroll
     for (int g = 0; g < kGroup; ++g) {
         const int64_t head = head0 + (g < n_heads ? g : 0);  // in range even when unused
         const u32x4_t raw = load16(a.query, ((seq * a.heads + head) * kDim + kVals * piece) * sizeof(T));
-        widen<T>(raw, q[g]);
+        if constexpr (kPacked) {
+            qp[g] = g < n_heads ? raw : u32x4_t{0u, 0u, 0u, 0u};
+        } else {
+            widen<T>(raw, q[g]);
 #pragma unroll
-        for (int e = 0; e < kVals; ++e) q[g][e] = g < n_heads ? q[g][e] * a.scale : 0.0f;
+            for (int e = 0; e < kVals; ++e) q[g][e] = g < n_heads ? q[g][e] * a.scale : 0.0f;
+        }
     }
 
     HeadState<kVals> st[kGroup];
@@ -249,15 +259,31 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(PagedArgs a) {
         float score[kGroup][kStepsPerLoad];
 #pragma unroll
         for (int u = 0; u < kStepsPerLoad; ++u) {
-            float k[kVals];
-            widen<T>(raw[u][0], k);
+            float k[kPacked ? 1 : kVals];
+            if constexpr (!kPacked) widen<T>(raw[u][0], k);
             const bool valid = t0 + u * kTokensPerStep + slot < w_hi;
 #pragma unroll
             for (int g = 0; g < kGroup; ++g) {
-                float part = q[g][0] * k[0];
+                float part;
+                if constexpr (kPacked) {
+                    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+                    part = 0.0f;
 #pragma unroll
-                for (int e = 1; e < kVals; ++e) part = fmaf(q[g][e], k[e], part);
-                part = lanes_sum<kLanes>(part);
+                    for (int e = 0; e < 4; ++e) {
+                        // Through plain words: a bit_cast of a vector element
+                        // subscript read element 0 for every e.
+                        const uint32_t qw = qp[g][e];
+                        const uint32_t kw = raw[u][0][e];
+                        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, qw),
+                                                              __builtin_bit_cast(bf16x2_v, kw), part, false);
+                    }
+                    part = lanes_sum<kLanes>(part) * a.scale;
+                } else {
+                    part = q[g][0] * k[0];
+#pragma unroll
+                    for (int e = 1; e < kVals; ++e) part = fmaf(q[g][e], k[e], part);
+                    part = lanes_sum<kLanes>(part);
+                }
                 score[g][u] = valid ? part : -INFINITY;
             }
         }
