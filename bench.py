@@ -23,8 +23,8 @@ launch (an event pair around it also times the dispatch and completion
 packets, ~2.5 us on a 45 us kernel). `traffic` is the HBM bytes
 per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed under
 profiles/ (null when absent). `cpu_baseline` times the reference's own CPU
-operators (oracle/_ref, built from the reference source) on a bounded sample
-of the same workload on this host's cores.
+operators (oracle/_ref, built from the reference source) on the same step,
+each op for about --cpu-seconds of CPU work, on this host's cores.
 
 `breakdown` reports every other configuration (`--configs` selects them):
 median over 5 batches of back-to-back launches timed by HIP events, after at
@@ -664,14 +664,15 @@ def bench_bulk_quant(torch, cf, warmup: int) -> dict:
 
 
 def cpu_baseline(seconds: float) -> dict | None:
-    """The reference's CPU operators (oracle/_ref) on a bounded sample of configs[1]."""
+    """The reference's CPU operators (oracle/_ref) on configs[1]'s step, each op timed
+    for about `seconds` of CPU work."""
     from oracle import ref_runner
 
     if not ref_runner.available():
         return None
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     results = {}
-    for op, shape in (("rmsnorm", [1024, 4096]), ("softmax", [1024, 2048])):
+    for op, shape in (("rmsnorm", [16384, 4096]), ("softmax", [1024, 2048])):
         proc = subprocess.run(
             [sys.executable, "-m", "oracle.ref_runner", "time", op, "--shape", *map(str, shape),
              "--dtype", "bf16", "--seconds", str(seconds), "--threads", str(threads)],
@@ -681,7 +682,7 @@ def cpu_baseline(seconds: float) -> dict | None:
             log(f"cpu baseline for {op} failed: {proc.stderr[-400:]}")
             return None
         results[op] = json.loads(proc.stdout.strip().splitlines()[-1])
-    rms_bytes = bytes_rmsnorm(1024, 4096, 2)
+    rms_bytes = bytes_rmsnorm(16384, 4096, 2)
     sm_bytes = bytes_softmax(1024, 2048, 2)
     total_s = results["rmsnorm"]["median_s"] + results["softmax"]["median_s"]
     return {
@@ -690,8 +691,8 @@ def cpu_baseline(seconds: float) -> dict | None:
         "cores": results["rmsnorm"]["threads"],
         "kind": "reference",
         "sample": ("reference CPU operators (cpp/src/bindings.cpp rmsnorm_cpu + softmax_cpu via ATen) on "
-                   "RMSNorm bf16 [1024, 4096] (1/16 of the config's rows) + causal softmax bf16 "
-                   f"[1024, 2048]; median of >=5 runs per op over ~{seconds:.0f} s each"),
+                   "the configs[1] step itself: RMSNorm bf16 [16384, 4096] + softmax bf16 [1024, 2048]; "
+                   f"median of the calls made in ~{seconds:.0f} s per op (at least 5)"),
         "rmsnorm_median_s": results["rmsnorm"]["median_s"],
         "softmax_median_s": results["softmax"]["median_s"],
         "host_cpu_count": results["rmsnorm"]["cpu_count"],

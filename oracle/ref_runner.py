@@ -144,7 +144,7 @@ def time_reference(op: str, shape: list[int], dtype: str, seconds: float, thread
         fn()
     samples = []
     started = time.perf_counter()
-    while len(samples) < 5 or (time.perf_counter() - started < seconds and len(samples) < 50):
+    while len(samples) < 5 or time.perf_counter() - started < seconds:
         t0 = time.perf_counter()
         fn()
         samples.append(time.perf_counter() - t0)
