@@ -35,6 +35,7 @@ timed by their own start/end timestamps (`kernel_median_ms`, the kernel-trace
 figure; `kernel_frac_*` is computed from it): config 1
 quantise/dequantise, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
 hipBLASLt's plain GEMM through torch for context) and its adapter backward,
+`reduce` the two-stage sum (16M and 256M fp32) and per-row sums,
 config 4 the Llama block forward (tokens/s end to end, per-operator event
 times and TFLOP/s), `paged` the paged-attention decode at the reference's
 benchmark shapes, `tensorcore` the fp32 matmul on the bf16 MFMA units, `fp8`
@@ -382,6 +383,41 @@ def bench_rowops(torch, cf, warmup: int, runs: int) -> dict:
     return out
 
 
+def bench_reduce(torch, cf, warmup: int, runs: int) -> dict:
+    """Rows a9-a11: the deterministic two-stage sum at the reference's benchmark
+    size (16M fp32, README's reduction table) and at 256M, and per-row sums of a
+    [16384, 4096] fp32 matrix. 4 bytes read per element; the output is a few bytes."""
+    gen = torch.Generator(device="cuda").manual_seed(10)
+    lib = cf._lib.load()
+    out = {}
+    for n, label in ((1 << 24, "sum_f32_16M"), (1 << 28, "sum_f32_256M")):
+        nbytes = 4 * n
+        sets = [torch.randn(n, generator=gen, device="cuda") for _ in range(sets_for(nbytes))]
+        ws_bytes = lib.cf_reduce_sum_workspace_bytes(n)
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
+        res = torch.empty(1, device="cuda")
+        launches = [lambda x=x: cf._lib.check(lib.cf_reduce_sum(
+            x.data_ptr(), cf._lib.CF_F32, res.data_ptr(), n, ws.data_ptr(), ws_bytes, 0,
+            torch.cuda.current_stream().cuda_stream)) for x in sets]
+        r = summary(time_launches(torch, launches, warmup, runs))
+        out[label] = {**r, "bytes": nbytes, "launches": 2, "GB/s": gbs(nbytes, r["median_ms"]),
+                      "frac_hbm": gbs(nbytes, r["median_ms"]) / PEAK_HBM_GBS}
+        del sets
+        torch.cuda.empty_cache()
+    rows, cols = 16384, 4096
+    nbytes = rows * cols * 4 + rows * 4
+    sets = [torch.randn(rows, cols, generator=gen, device="cuda") for _ in range(sets_for(nbytes))]
+    res = torch.empty(rows, device="cuda")
+    launches = [lambda x=x: cf._lib.check(lib.cf_row_sum(
+        x.data_ptr(), cf._lib.CF_F32, res.data_ptr(), rows, cols,
+        torch.cuda.current_stream().cuda_stream)) for x in sets]
+    r = summary(time_launches(torch, launches, warmup, runs))
+    with_kernel_time(torch, cf, r, launches, nbytes=nbytes)
+    out["row_sum_f32_16384x4096"] = {**r, "bytes": nbytes, "GB/s": gbs(nbytes, r["median_ms"]),
+                                     "frac_hbm": gbs(nbytes, r["median_ms"]) / PEAK_HBM_GBS}
+    return out
+
+
 def bench_lora(torch, cf, warmup: int, runs: int) -> dict:
     """config 3: fused LoRA bf16 8192x4096x4096 r16, alpha 32; adapter backward."""
     gen = torch.Generator(device="cuda").manual_seed(4)
@@ -717,7 +753,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--quick", action="store_true", help="skip the breakdown (main step only)")
-    parser.add_argument("--configs", default="1,2,3,4,5,paged,tensorcore,fp8",
+    parser.add_argument("--configs", default="1,2,reduce,3,4,5,paged,tensorcore,fp8",
                         help="breakdown configs to run (comma-separated: 1-5, paged, tensorcore)")
     parser.add_argument("--detail", default="", help="also write the full result JSON here")
     args = parser.parse_args(argv)
@@ -752,6 +788,7 @@ def main(argv: list[str] | None = None) -> int:
                   for c in args.configs.split(",") if c.strip()}
         for name, fn in (("config1", lambda: bench_quant(torch, cf, args.warmup, args.runs)),
                          ("config2", lambda: bench_rowops(torch, cf, args.warmup, args.runs)),
+                         ("reduce", lambda: bench_reduce(torch, cf, args.warmup, args.runs)),
                          ("config3", lambda: bench_lora(torch, cf, args.warmup, args.runs)),
                          ("config4", lambda: bench_block(torch, cf, 20, args.runs)),
                          ("config5", lambda: bench_bulk_quant(torch, cf, 3)),

@@ -230,17 +230,17 @@ cf_status column_reduce(const float* p, const void* v, void* out, bool transpose
     const dim3 grid(static_cast<unsigned>(ceil_div<int64_t>(cols, kWaveSize)),
                     static_cast<unsigned>(chunks));
     for (int64_t q0 = 0; q0 < rank; q0 += 16) {
-        column_reduce_kernel<T><<<grid, kColThreads, 0, stream>>>(p, static_cast<const T*>(v), part,
-                                                                 rows, cols, rank, q0);
+        launch(column_reduce_kernel<T>, dim3(grid), dim3(kColThreads), 0, stream, p,
+               static_cast<const T*>(v), part, rows, cols, rank, q0);
     }
     const int64_t total = rank * cols;
     const unsigned fgrid = static_cast<unsigned>(ceil_div<int64_t>(total, kDefaultBlockSize));
     if (transposed) {
-        column_finish_kernel<T, true><<<fgrid, kDefaultBlockSize, 0, stream>>>(
-            part, static_cast<T*>(out), chunks, rank, cols, scale);
+        launch(column_finish_kernel<T, true>, dim3(fgrid), dim3(kDefaultBlockSize), 0, stream, part,
+               static_cast<T*>(out), chunks, rank, cols, scale);
     } else {
-        column_finish_kernel<T, false><<<fgrid, kDefaultBlockSize, 0, stream>>>(
-            part, static_cast<T*>(out), chunks, rank, cols, scale);
+        launch(column_finish_kernel<T, false>, dim3(fgrid), dim3(kDefaultBlockSize), 0, stream,
+               part, static_cast<T*>(out), chunks, rank, cols, scale);
     }
     return check_launch("launching the LoRA backward column reduction", stream);
 }
@@ -251,14 +251,14 @@ cf_status zero_gradients(void* grad_a, void* grad_b, int64_t in_features, int64_
     if (in_features > 0) {
         const unsigned grid =
             static_cast<unsigned>(ceil_div<int64_t>(rank * in_features, kDefaultBlockSize));
-        column_finish_kernel<T, true><<<grid, kDefaultBlockSize, 0, stream>>>(
-            nullptr, static_cast<T*>(grad_a), 0, rank, in_features, 1.0f);
+        launch(column_finish_kernel<T, true>, dim3(grid), dim3(kDefaultBlockSize), 0, stream,
+               nullptr, static_cast<T*>(grad_a), 0, rank, in_features, 1.0f);
     }
     if (out_features > 0) {
         const unsigned grid =
             static_cast<unsigned>(ceil_div<int64_t>(rank * out_features, kDefaultBlockSize));
-        column_finish_kernel<T, false><<<grid, kDefaultBlockSize, 0, stream>>>(
-            nullptr, static_cast<T*>(grad_b), 0, rank, out_features, 1.0f);
+        launch(column_finish_kernel<T, false>, dim3(grid), dim3(kDefaultBlockSize), 0, stream,
+               nullptr, static_cast<T*>(grad_b), 0, rank, out_features, 1.0f);
     }
     return check_launch("zeroing the LoRA gradients", stream);
 }
@@ -269,9 +269,9 @@ void launch_row_dot(const void* x, const void* p, float* out, int64_t rows, int6
     const int64_t max_waves = static_cast<int64_t>(cu_count()) * 16;
     const int64_t waves = rows < max_waves ? rows : max_waves;
     const int64_t grid = ceil_div<int64_t>(waves, kDefaultBlockSize / kWaveSize);
-    row_dot_kernel<T><<<static_cast<unsigned>(grid), kDefaultBlockSize, 0, stream>>>(
-        static_cast<const T*>(x), static_cast<const T*>(p), out, rows, inner, rank, k_stride,
-        q_stride);
+    launch(row_dot_kernel<T>, dim3(static_cast<unsigned>(grid)), dim3(kDefaultBlockSize), 0, stream,
+           static_cast<const T*>(x), static_cast<const T*>(p), out, rows, inner, rank, k_stride,
+           q_stride);
 }
 
 template <typename T>
@@ -283,9 +283,9 @@ cf_status launch_generic(const void* x, const void* w, const void* a, const void
     }
     const dim3 grid(static_cast<unsigned>(ceil_div<int64_t>(N, kGT)),
                     static_cast<unsigned>(ceil_div<int64_t>(M, kGT)));
-    tiled_gemm_kernel<T><<<grid, kDefaultBlockSize, 0, stream>>>(
-        static_cast<const T*>(x), static_cast<const T*>(w), rank > 0 ? xa : nullptr,
-        static_cast<const T*>(b), static_cast<T*>(y), M, N, K, rank, scale);
+    launch(tiled_gemm_kernel<T>, dim3(grid), dim3(kDefaultBlockSize), 0, stream,
+           static_cast<const T*>(x), static_cast<const T*>(w),
+           rank > 0 ? xa : nullptr, static_cast<const T*>(b), static_cast<T*>(y), M, N, K, rank, scale);
     return check_launch("launching the tiled LoRA GEMM", stream);
 }
 

@@ -399,12 +399,13 @@ cf_status launch_lora_backward_fast(const void* x, const void* dy, const void* b
     dy_pass.C = N;
     dy_pass.rank = rank;
     const int64_t n_tiles = ceil_div<int64_t>(N, kTileCols);
-    column_mfma_kernel<true><<<dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(row_tiles)),
-                               kThreads, 0, stream>>>(dy_pass);
+    launch(column_mfma_kernel<true>,
+           dim3(dim3(static_cast<unsigned>(n_tiles), static_cast<unsigned>(row_tiles))),
+           dim3(kThreads), 0, stream, dy_pass);
     const int64_t grad_b_blocks = ceil_div<int64_t>(rank * N, kThreads);
-    after_dy_kernel<<<static_cast<unsigned>(grad_b_blocks + small_grid), kThreads, 0, stream>>>(
-        ws.colpart, static_cast<uint16_t*>(grad_b), ws.gpart, ws.gt, grad_b_blocks, row_tiles, rank, N,
-        scale, Mp, n_tiles);
+    launch(after_dy_kernel, dim3(static_cast<unsigned>(grad_b_blocks + small_grid)), dim3(kThreads),
+           0, stream, ws.colpart, static_cast<uint16_t*>(grad_b), ws.gpart, ws.gt, grad_b_blocks,
+           row_tiles, rank, N, scale, Mp, n_tiles);
 
     ColumnArgs x_pass;
     x_pass.v = static_cast<const uint16_t*>(x);
@@ -418,11 +419,12 @@ cf_status launch_lora_backward_fast(const void* x, const void* dy, const void* b
     x_pass.C = K;
     x_pass.rank = rank;
     const int64_t k_tiles = ceil_div<int64_t>(K, kTileCols);
-    column_mfma_kernel<false><<<dim3(static_cast<unsigned>(k_tiles), static_cast<unsigned>(row_tiles)),
-                                kThreads, 0, stream>>>(x_pass);
-    finish_grad_a_kernel<<<static_cast<unsigned>(ceil_div<int64_t>(rank * K, kThreads)), kThreads, 0,
-                           stream>>>(ws.colpart, static_cast<uint16_t*>(grad_a), row_tiles, rank, K,
-                                     scale);
+    launch(column_mfma_kernel<false>,
+           dim3(dim3(static_cast<unsigned>(k_tiles), static_cast<unsigned>(row_tiles))),
+           dim3(kThreads), 0, stream, x_pass);
+    launch(finish_grad_a_kernel, dim3(static_cast<unsigned>(ceil_div<int64_t>(rank * K, kThreads))),
+           dim3(kThreads), 0, stream, ws.colpart, static_cast<uint16_t*>(grad_a), row_tiles, rank,
+           K, scale);
     return check_launch("launching the bf16 LoRA backward", stream);
 }
 

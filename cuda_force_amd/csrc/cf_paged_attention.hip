@@ -538,10 +538,10 @@ template <typename T, int kLanes>
 void launch_streaming(const PagedArgs& args, int gs, int64_t workgroups, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(workgroups));
     switch (gs) {
-        case 1: paged_decode_kernel<T, kLanes, 1><<<grid, kThreads, 0, stream>>>(args); break;
-        case 2: paged_decode_kernel<T, kLanes, 2><<<grid, kThreads, 0, stream>>>(args); break;
-        case 4: paged_decode_kernel<T, kLanes, 4><<<grid, kThreads, 0, stream>>>(args); break;
-        default: paged_decode_kernel<T, kLanes, 8><<<grid, kThreads, 0, stream>>>(args); break;
+        case 1: launch(paged_decode_kernel<T, kLanes, 1>, dim3(grid), dim3(kThreads), 0, stream, args); break;
+        case 2: launch(paged_decode_kernel<T, kLanes, 2>, dim3(grid), dim3(kThreads), 0, stream, args); break;
+        case 4: launch(paged_decode_kernel<T, kLanes, 4>, dim3(grid), dim3(kThreads), 0, stream, args); break;
+        default: launch(paged_decode_kernel<T, kLanes, 8>, dim3(grid), dim3(kThreads), 0, stream, args); break;
     }
 }
 
@@ -551,15 +551,15 @@ void launch_typed(const PagedArgs& args, const Plan& plan, int64_t sequences, hi
         const int64_t per = (args.head_dim + kWaveSize - 1) / kWaveSize;
         const dim3 grid(static_cast<unsigned>(sequences * args.heads));
         if (per <= 1) {
-            paged_decode_wide_kernel<T, 1><<<grid, kWaveSize, 0, stream>>>(args);
+            launch(paged_decode_wide_kernel<T, 1>, dim3(grid), dim3(kWaveSize), 0, stream, args);
         } else if (per <= 2) {
-            paged_decode_wide_kernel<T, 2><<<grid, kWaveSize, 0, stream>>>(args);
+            launch(paged_decode_wide_kernel<T, 2>, dim3(grid), dim3(kWaveSize), 0, stream, args);
         } else if (per <= 4) {
-            paged_decode_wide_kernel<T, 4><<<grid, kWaveSize, 0, stream>>>(args);
+            launch(paged_decode_wide_kernel<T, 4>, dim3(grid), dim3(kWaveSize), 0, stream, args);
         } else if (per <= 8) {
-            paged_decode_wide_kernel<T, 8><<<grid, kWaveSize, 0, stream>>>(args);
+            launch(paged_decode_wide_kernel<T, 8>, dim3(grid), dim3(kWaveSize), 0, stream, args);
         } else {
-            paged_decode_wide_kernel<T, 16><<<grid, kWaveSize, 0, stream>>>(args);
+            launch(paged_decode_wide_kernel<T, 16>, dim3(grid), dim3(kWaveSize), 0, stream, args);
         }
         return;
     }
@@ -574,8 +574,8 @@ void launch_typed(const PagedArgs& args, const Plan& plan, int64_t sequences, hi
         default: launch_streaming<T, 64>(args, plan.gs, workgroups, stream); break;
     }
     if (plan.splits > 1) {
-        paged_combine_kernel<T><<<dim3(static_cast<unsigned>(sequences * args.heads)), kWaveSize, 0,
-                                  stream>>>(args);
+        launch(paged_combine_kernel<T>, dim3(dim3(static_cast<unsigned>(sequences * args.heads))),
+               dim3(kWaveSize), 0, stream, args);
     }
 }
 

@@ -183,8 +183,9 @@ cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream)
     if (rest > 0) {
         const int64_t wanted = cf::ceil_div<int64_t>(rest, 256);
         const int grid = static_cast<int>(wanted < 65536 ? wanted : 65536);
-        cf::copy_tail_kernel<<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(src) + done,
-                                                  static_cast<uint8_t*>(dst) + done, rest);
+        cf::launch(cf::copy_tail_kernel, dim3(grid), dim3(256), 0, s,
+                   static_cast<const uint8_t*>(src) + done, static_cast<uint8_t*>(dst) + done,
+                   rest);
     }
     return cf::check_launch("launching the byte copy", s);
 }

@@ -339,12 +339,13 @@ cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream)
  * and `stop_event` (hipEvent_t, created by the caller with timing enabled), so
  * hipEventElapsedTime(start, stop) is the kernel's execution time as a kernel
  * trace reports it, without the queue packets of an event pair recorded around
- * the call. Both NULL disarms. Applies to entry points that launch a single
- * kernel (quantise, dequantise, RMSNorm, fused residual RMSNorm, softmax,
- * activations, the fused LoRA forward, the fp8 matmul, the byte copy); with a
- * multi-kernel entry point only its first launch is timed. It has no
- * counterpart in the reference, whose benchmarks bracket each launch with an
- * event pair (benchmarks/benchmark_kernels.cu:59-79). */
+ * the call. Every kernel of the library launches through this hook; for an
+ * entry point that launches several kernels (the two-stage sum, the adapter
+ * backward, split-K matmuls, context-split paged attention) the first one is
+ * timed. An entry point that returns without launching leaves the events
+ * armed for the next launch. Both NULL disarms. It has no counterpart in the
+ * reference, whose benchmarks bracket each launch with an event pair
+ * (benchmarks/benchmark_kernels.cu:59-79). */
 cf_status cf_time_next_launch(void* start_event, void* stop_event);
 
 /* ---- runtime: stream scheduler and caching pools ------------------------
