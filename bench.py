@@ -31,8 +31,9 @@ median over 5 batches of back-to-back launches timed by HIP events, after at
 least 0.3 s of warm-up, with cache-cold rotation (`median_ms`: launch-to-launch
 time, which for kernels of a few microseconds is the host's launch rate), and
 for entry points that launch one kernel also the median of 25 dispatches
-timed by their own start/end timestamps (`kernel_median_ms`, the kernel-trace
-figure; `kernel_frac_*` is computed from it): config 1
+timed by their own start/end timestamps, launched back to back
+(`kernel_median_ms`, the kernel-trace figure; `kernel_frac_*` is computed from
+it): config 1
 quantise/dequantise, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
 hipBLASLt's plain GEMM through torch for context) and its adapter backward,
 `reduce` the two-stage sum (16M and 256M fp32) and per-row sums,
@@ -142,9 +143,13 @@ def time_launches(torch, launches, warmup: int, runs: int, batches: int = 5) -> 
 
 
 def kernel_times(torch, cf, launches, count: int = KERNEL_SAMPLES) -> list[float]:
-    """Execution time (ms) of `count` back-to-back dispatches, cycling over
-    `launches`, each timed by the start/end timestamps of its own dispatch
-    (cf_time_next_launch). Only for entry points that launch one kernel."""
+    """Execution time (ms) of `count` dispatches, cycling over `launches`,
+    each timed by the start/end timestamps of its own dispatch
+    (cf_time_next_launch), launched back to back. For kernels of ~15 us or
+    less the median can read 10-30% long on some runs (the Python launch loop
+    then falls behind the GPU and some dispatches start from an idle queue);
+    the kernel-trace averages in profiles/ are the reference figures there.
+    Only for entry points that launch one kernel."""
     timers = [cf._lib.DispatchTimer() for _ in range(count)]
     torch.cuda.synchronize()
     for i, timer in enumerate(timers):
@@ -273,7 +278,8 @@ def bench_main_step(torch, cf, steps: int, warmup: int) -> dict:
 
 
 def bench_quant(torch, cf, warmup: int, runs: int) -> dict:
-    """config 1: quantise fp32 [4096, 4096] (1% outliers x20), then dequantise."""
+    """config 1: quantise fp32 [4096, 4096] (1% outliers x20), then dequantise; with the
+    streaming ceiling of the quantiser's traffic mix (cf_stream_bytes) for context."""
     gen = torch.Generator(device="cuda").manual_seed(1)
     n = 4096 * 4096
     qb = bytes_quant(n, 4)
@@ -297,6 +303,14 @@ def bench_quant(torch, cf, warmup: int, runs: int) -> dict:
 
     q = summary(time_launches(torch, [quant(s) for s in sets], warmup, runs))
     with_kernel_time(torch, cf, q, [quant(s) for s in sets], nbytes=qb)
+    # The streaming ceiling of the quantiser's own traffic mix at this size:
+    # read 64 MiB, write a quarter of it, same load pattern, no arithmetic.
+    def stream(s):
+        return lambda: cf._lib.check(lib.cf_stream_bytes(
+            s[0].data_ptr(), s[3].data_ptr(), n * 4, 4, torch.cuda.current_stream().cuda_stream))
+
+    ceiling = summary(time_launches(torch, [stream(s) for s in sets], warmup, runs))
+    with_kernel_time(torch, cf, ceiling, [stream(s) for s in sets], nbytes=n * 5)
     d = summary(time_launches(torch, [dequant(s) for s in sets], warmup, runs))
     with_kernel_time(torch, cf, d, [dequant(s) for s in sets], nbytes=bytes_dequant(n, 4))
     return {
@@ -305,6 +319,9 @@ def bench_quant(torch, cf, warmup: int, runs: int) -> dict:
         "dequantize_f32_4096x4096": {**d, "GB/s": gbs(bytes_dequant(n, 4), d["median_ms"]),
                                      "bytes": bytes_dequant(n, 4),
                                      "frac_hbm": gbs(bytes_dequant(n, 4), d["median_ms"]) / PEAK_HBM_GBS},
+        "stream_ceiling_read64MiB_write16MiB_context": {
+            **ceiling, "bytes": n * 5, "GB/s": gbs(n * 5, ceiling["median_ms"]),
+            "frac_hbm": gbs(n * 5, ceiling["median_ms"]) / PEAK_HBM_GBS},
     }
 
 

@@ -91,6 +91,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_gelu": (_I32, [_P, _P, _I32, _I64, _P]),
     "cf_swiglu": (_I32, [_P, _P, _P, _I32, _I64, _P]),
     "cf_copy_bytes": (_I32, [_P, _P, _I64, _P]),
+    "cf_stream_bytes": (_I32, [_P, _P, _I64, _I32, _P]),
     "cf_time_next_launch": (_I32, [_P, _P]),
     "cf_tensor_cores_available": (_I32, []),
     "cf_matmul_tensor_core_shape_supported": (_I32, [_I64, _I64, _I64]),

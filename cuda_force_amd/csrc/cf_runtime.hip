@@ -124,6 +124,32 @@ __global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ s
     }
 }
 
+/// Read-mostly stream with the quantiser's access pattern: each lane loads
+/// four 16-byte vectors (one 1 KiB piece per wave instruction, as the fp32
+/// quantiser does) and writes 16 / kDivisor bytes derived from each, so
+/// the kernel reads `vectors` x 16 bytes and writes a kDivisor-th of that.
+/// Only whole workgroup chunks are processed.
+template <int kDivisor>
+__global__ __launch_bounds__(256) void stream_kernel(const uint4* __restrict__ src,
+                                                     uint8_t* __restrict__ dst) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * kCopyUnroll + threadIdx.x;
+    uint4 v[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) v[u] = load_stream16(src + base + u * 256);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+        const int64_t i = base + u * 256;
+        if constexpr (kDivisor == 1) {
+            store_stream16(dst + 16 * i, v[u]);
+        } else if constexpr (kDivisor == 2) {
+            store_stream8(dst + 8 * i, make_uint2(v[u].x ^ v[u].y, v[u].z ^ v[u].w));
+        } else {
+            store_stream4(dst + 4 * i, v[u].x ^ v[u].y ^ v[u].z ^ v[u].w);
+        }
+    }
+}
+
 __global__ void copy_tail_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                  int64_t bytes) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -163,6 +189,33 @@ cf_status cf_time_next_launch(void* start_event, void* stop_event) {
                "cf_time_next_launch: give both events or neither");
     cf::g_launch_events = {static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
     return CF_OK;
+}
+
+cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int divisor, void* stream) {
+    if (read_bytes <= 0) return CF_OK;
+    CF_REQUIRE(src != nullptr && dst != nullptr, "cf_stream_bytes: null pointer");
+    CF_REQUIRE(divisor == 1 || divisor == 2 || divisor == 4, "cf_stream_bytes: divisor %d is not 1, 2 or 4",
+               divisor);
+    constexpr int64_t kChunk = 256 * cf::kCopyUnroll * 16;
+    CF_REQUIRE(read_bytes % kChunk == 0, "cf_stream_bytes: %lld bytes are not a multiple of %lld",
+               static_cast<long long>(read_bytes), static_cast<long long>(kChunk));
+    CF_REQUIRE(cf::host_aligned(src, 16) && cf::host_aligned(dst, 16),
+               "cf_stream_bytes: src and dst must be 16-byte aligned");
+    const int64_t grid = read_bytes / kChunk;
+    CF_REQUIRE(grid < (1LL << 31), "cf_stream_bytes: %lld bytes exceed the launch limit",
+               static_cast<long long>(read_bytes));
+    auto s = static_cast<hipStream_t>(stream);
+    const dim3 g(static_cast<unsigned>(grid));
+    const auto* in = static_cast<const uint4*>(src);
+    auto* out = static_cast<uint8_t*>(dst);
+    if (divisor == 1) {
+        cf::launch(cf::stream_kernel<1>, g, dim3(256), 0, s, in, out);
+    } else if (divisor == 2) {
+        cf::launch(cf::stream_kernel<2>, g, dim3(256), 0, s, in, out);
+    } else {
+        cf::launch(cf::stream_kernel<4>, g, dim3(256), 0, s, in, out);
+    }
+    return cf::check_launch("launching the byte stream", s);
 }
 
 cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream) {

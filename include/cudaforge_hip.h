@@ -334,6 +334,15 @@ cf_status cf_paged_attention(const void* query, const void* k_cache, const void*
  * measure the achievable HBM bandwidth next to the ops above. */
 cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream);
 
+/* Reads `read_bytes` from `src` and writes read_bytes / `divisor` bytes
+ * derived from them to `dst` (divisor 1, 2 or 4), with the fp32 quantiser's
+ * access pattern (four 16-byte loads per lane, then the stores; one-shot
+ * grid). read_bytes must be a multiple of 16 KiB and both pointers 16-byte
+ * aligned. It has no counterpart in the reference: it measures the streaming
+ * ceiling of a traffic mix (divisor 4 is the fp32 quantiser's 4 : 1) next to
+ * the kernels that move it. */
+cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int divisor, void* stream);
+
 /* Arms the calling thread's next kernel launch made by this library: that
  * dispatch records its own start and completion timestamps on `start_event`
  * and `stop_event` (hipEvent_t, created by the caller with timing enabled), so

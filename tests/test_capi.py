@@ -144,3 +144,12 @@ def test_grouped_quantisation_host_checks(lib):
     assert b"tensor 1" in lib.cf_last_error()
     assert lib.cf_dequantize_int8_group(ptrs, ptrs, ptrs, _lib.CF_F32, counts, 2, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_quantize_int8_group(ptrs, 7, ptrs, ptrs, counts, 2, null) == _lib.CF_ERR_UNSUPPORTED
+
+
+def test_stream_bytes_host_checks(lib):
+    null = ctypes.c_void_p(0)
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: rejected before any launch
+    assert lib.cf_stream_bytes(null, null, 0, 4, null) == _lib.CF_OK
+    assert lib.cf_stream_bytes(fake, fake, 16384, 3, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_stream_bytes(fake, fake, 1000, 4, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_stream_bytes(null, fake, 16384, 4, null) == _lib.CF_ERR_INVALID_ARGUMENT

@@ -59,3 +59,22 @@ def test_only_the_next_launch_is_timed():
     assert timer.elapsed_ms() == first
     timer.close()
     assert torch.equal(y, torch.ones_like(y))
+
+
+@pytest.mark.parametrize("divisor", [1, 2, 4])
+def test_stream_bytes_writes_what_it_read(divisor):
+    """The streaming-ceiling kernel: divisor 1 copies; 2 and 4 write the xor of
+    each 16-byte vector's halves / words."""
+    print(f"case: cf_stream_bytes divisor {divisor}", flush=True)
+    src = torch.randint(0, 1 << 31, (1 << 14,), dtype=torch.int32, device="cuda")  # 64 KiB
+    dst = torch.zeros(src.numel() // divisor, dtype=torch.int32, device="cuda")
+    call("cf_stream_bytes", src.data_ptr(), dst.data_ptr(), src.numel() * 4, divisor, stream())
+    torch.cuda.synchronize()
+    v = src.view(-1, 4)
+    if divisor == 1:
+        want = src
+    elif divisor == 2:
+        want = torch.stack([v[:, 0] ^ v[:, 1], v[:, 2] ^ v[:, 3]], dim=1).reshape(-1)
+    else:
+        want = v[:, 0] ^ v[:, 1] ^ v[:, 2] ^ v[:, 3]
+    assert torch.equal(dst, want)
