@@ -28,7 +28,8 @@
 //     l % 32 from an N-major tile, transposed on the way out of LDS by four
 //     ds_read_b64_tr_b8 (each hands a lane 8 k values of one column). Both
 //     tiles are swizzled so every read is free of bank conflicts.
-//   * Epilogue: scale, round to bf16, 8-byte stores.
+//   * Epilogue: scale, round to bf16, staged per wave in LDS and stored as
+//     whole 256-byte row pieces.
 //   * Workgroup ids are remapped so that the tiles of one XCD share x
 //     row-panels in its L2 (tile_of).
 //
@@ -60,6 +61,7 @@ constexpr int kTileW = kBK * kBN;             // 16 KiB: [64 k][256 n]
 constexpr int kOffW = kXSlots * kXPair;
 constexpr int kLdsBytes = kOffW + kStages * kTileW;  // 128 KiB
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 workgroup");
+static_assert(kThreads / 64 * 64 * 256 <= kLdsBytes, "output staging fits the operand area");
 
 constexpr int kUnitScale = 127;  // E8M0 code of 2^0
 
@@ -323,29 +325,48 @@ void matmul_fp8_kernel(Fp8Args args) {
 
     // Store: acc[jb][i] element t of lane l is y[row wm*64 + 32 i + l % 32]
     // [column wn*128 + 32 jb + 8 (t / 4) + 4 (l / 32) + t % 4]; N is a
-    // multiple of 16, so a four-column run is entirely inside or outside.
+    // multiple of 16, so an eight-column run is entirely inside or outside.
+    // The tile goes through LDS so that each store instruction writes whole
+    // rows (16 lanes x 16 bytes = 256 contiguous bytes, 4 rows per
+    // instruction) instead of 16 bytes of each of 32 rows: each wave stages
+    // its 64 x 128 bf16 sub-tile (16 KiB, rows of 256 bytes) in the operand
+    // area once every wave is past the K-loop. Chunk c (16 bytes) of row r
+    // sits at chunk c ^ (r & 15), and rows with bit 4 set swap the two 8-byte
+    // halves of their chunks: a half-wave's 8-byte writes (32 rows, one half
+    // each) then cover all banks, and the 16-byte reads of whole rows too.
+    __syncthreads();
     const float scale = args.scale;
+    uint8_t* stage = lds + wave * (64 * 256);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int64_t row = m0 + wm * 64 + 32 * i + (lane & 31);
-        if (row >= M) continue;
-        uint16_t* yrow = args.y + row * N;
+        const int r = 32 * i + (lane & 31);
+        const int flip = (r >> 4) & 1;
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
+            const f32x16_t& a = acc[jb][i];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int64_t col = n0 + wn * 128 + 32 * jb + 8 * q + 4 * h;
-                if (col < N) {
-                    const f32x16_t& a = acc[jb][i];
-                    uint2 packed;
-                    packed.x = f32_to_bf16_bits(scale * a[4 * q]) |
-                               (f32_to_bf16_bits(scale * a[4 * q + 1]) << 16);
-                    packed.y = f32_to_bf16_bits(scale * a[4 * q + 2]) |
-                               (f32_to_bf16_bits(scale * a[4 * q + 3]) << 16);
-                    *reinterpret_cast<uint2*>(yrow + col) = packed;
-                }
+                const int c = 4 * jb + q;
+                uint2 packed;
+                packed.x = f32_to_bf16_bits(scale * a[4 * q]) | (f32_to_bf16_bits(scale * a[4 * q + 1]) << 16);
+                packed.y = f32_to_bf16_bits(scale * a[4 * q + 2]) | (f32_to_bf16_bits(scale * a[4 * q + 3]) << 16);
+                *reinterpret_cast<uint2*>(stage + r * 256 + ((c ^ (r & 15)) << 4) + ((h ^ flip) << 3)) = packed;
             }
         }
+    }
+    // Only this wave reads what it wrote: LDS operations of a wave complete
+    // in order; the fence keeps the compiler from moving the reads above.
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const int c = lane & 15;
+    const int64_t col = n0 + wn * 128 + 8 * c;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        const int r = 4 * s + (lane >> 4);
+        uint4 v = *reinterpret_cast<const uint4*>(stage + r * 256 + ((c ^ (r & 15)) << 4));
+        if ((r >> 4) & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        const int64_t grow = m0 + wm * 64 + r;
+        if (grow < M && col < N) store_stream16(args.y + grow * N + col, v);
     }
 }
 
