@@ -49,7 +49,7 @@ def test_workspace_queries(lib):
     assert lib.cf_lora_workspace_bytes(0, 16) == 0
     assert lib.cf_reduce_sum_workspace_bytes(0) == 0
     assert lib.cf_reduce_sum_workspace_bytes(1) == 4
-    assert lib.cf_reduce_sum_workspace_bytes(1 << 30) == 2048 * 4
+    assert lib.cf_reduce_sum_workspace_bytes(1 << 30) == 4096 * 4
     assert lib.cf_lora_backward_workspace_bytes(8192, 4096, 4096, 16) >= 8192 * 16 * 4
     assert lib.cf_abi_version() == 1
 

@@ -102,5 +102,5 @@ def test_sum_past_2_31_elements():
     g.call("cf_reduce_sum", x.data_ptr(), g.cf("f32"), out.data_ptr(), n, ws.data_ptr(), nbytes, 0, g.stream())
     torch.cuda.synchronize()
     # fp32 partial sums of ones are exact below 2^24 per partial; the final
-    # fixed-order tree over <= 2048 partials rounds at most ~11 times.
+    # fixed-order tree over <= 4096 partials rounds at most ~12 times.
     assert abs(out.item() - n) <= n * 2.0**-20
