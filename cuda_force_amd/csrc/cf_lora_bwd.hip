@@ -26,6 +26,8 @@
 // Deterministic: every sum has a fixed order, no atomics.
 #include "cf_lora_bwd.hpp"
 
+#include <type_traits>
+
 namespace cf {
 namespace {
 
@@ -264,6 +266,30 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
     }
 }
 
+/// total += at(t) for t = t .. tiles - 1 in that order, loads issued in
+/// groups of 32, 16, 4, then 1 so a thread waits for memory a few times
+/// rather than once per eight partials.
+template <typename At>
+__device__ __forceinline__ float ordered_sum(int64_t tiles, At at) {
+    float total = 0.0f;
+    int64_t t = 0;
+    auto groups = [&](auto group) {
+        constexpr int kGroup = decltype(group)::value;
+        for (; t + kGroup <= tiles; t += kGroup) {
+            float v[kGroup];
+#pragma unroll
+            for (int k = 0; k < kGroup; ++k) v[k] = at(t + k);
+#pragma unroll
+            for (int k = 0; k < kGroup; ++k) total += v[k];
+        }
+    };
+    groups(std::integral_constant<int, 32>{});
+    groups(std::integral_constant<int, 16>{});
+    groups(std::integral_constant<int, 4>{});
+    groups(std::integral_constant<int, 1>{});
+    return total;
+}
+
 /// gt[j, m] = bf16(sum over column tiles of gpart[tile][m][j]), fixed order;
 /// thread i of the launch handles element i.
 __device__ __forceinline__ void sum_g(const float* __restrict__ gpart, uint16_t* __restrict__ gt,
@@ -271,17 +297,8 @@ __device__ __forceinline__ void sum_g(const float* __restrict__ gpart, uint16_t*
     if (i >= kRankPad * Mp) return;
     const int64_t m = i / kRankPad;
     const int64_t j = i % kRankPad;
-    // Loads of a group of tiles go out together; the adds keep tile order.
-    float total = 0.0f;
-    int64_t t = 0;
-    for (; t + 8 <= tiles; t += 8) {
-        float v[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = gpart[((t + k) * Mp + m) * kRankPad + j];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) total += v[k];
-    }
-    for (; t < tiles; ++t) total += gpart[(t * Mp + m) * kRankPad + j];
+    const float total =
+        ordered_sum(tiles, [&](int64_t t) { return gpart[(t * Mp + m) * kRankPad + j]; });
     gt[j * Mp + m] = static_cast<uint16_t>(f32_to_bf16_bits(total));
 }
 
@@ -294,17 +311,8 @@ __device__ __forceinline__ void finish(const float* __restrict__ colpart, uint16
     if (i >= rank * C) return;
     const int64_t j = i / C;
     const int64_t n = i % C;
-    // Loads of a group of tiles go out together; the adds keep tile order.
-    float total = 0.0f;
-    int64_t t = 0;
-    for (; t + 8 <= tiles; t += 8) {
-        float v[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = colpart[((t + k) * kRankPad + j) * C + n];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) total += v[k];
-    }
-    for (; t < tiles; ++t) total += colpart[(t * kRankPad + j) * C + n];
+    const float total =
+        ordered_sum(tiles, [&](int64_t t) { return colpart[(t * kRankPad + j) * C + n]; });
     const int64_t dst = kTransposed ? n * rank + j : j * C + n;
     out[dst] = static_cast<uint16_t>(f32_to_bf16_bits(scale * total));
 }
