@@ -316,6 +316,11 @@ void lora_fused_bf16_kernel(FusedArgs args) {
                 if constexpr (decltype(odd)::value) issue_x((next_kt + 2) >> 1, jb);
                 if (jb < kWLoads) issue_w(next_kt + 2, jb);
             }
+            // Left alone, the scheduler sinks each next-step w read to a few
+            // MFMAs before its use; a scheduling barrier after every second
+            // fragment group keeps the reads a group ahead. Only the adapter
+            // kernel: the plain one would need more than 256 VGPRs.
+            if (kAdapter && (jb & 1) == 1) __builtin_amdgcn_sched_barrier(0);
         }
     };
 
