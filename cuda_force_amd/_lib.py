@@ -93,6 +93,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_copy_bytes": (_I32, [_P, _P, _I64, _P]),
     "cf_stream_bytes": (_I32, [_P, _P, _I64, _I32, _P]),
     "cf_time_next_launch": (_I32, [_P, _P]),
+    "cf_time_next_launch_armed": (_I32, []),
     "cf_tensor_cores_available": (_I32, []),
     "cf_matmul_tensor_core_shape_supported": (_I32, [_I64, _I64, _I64]),
     "cf_matmul_tensor_core_workspace_bytes": (_SZ, [_I64, _I64, _I64]),

@@ -166,12 +166,14 @@ cf_status run(const void* a, const void* b, void* y, cf_dtype dtype, int64_t cou
 extern "C" {
 
 cf_status cf_silu(const void* x, void* y, cf_dtype dtype, int64_t count, void* stream) {
+    CF_ENTRY();
     if (count <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && y != nullptr, "cf_silu: null pointer");
     return cf::run<cf::Silu, false>(x, nullptr, y, dtype, count, stream, "launching silu");
 }
 
 cf_status cf_gelu(const void* x, void* y, cf_dtype dtype, int64_t count, void* stream) {
+    CF_ENTRY();
     if (count <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && y != nullptr, "cf_gelu: null pointer");
     return cf::run<cf::GeluTanh, false>(x, nullptr, y, dtype, count, stream, "launching gelu");
@@ -179,6 +181,7 @@ cf_status cf_gelu(const void* x, void* y, cf_dtype dtype, int64_t count, void* s
 
 cf_status cf_swiglu(const void* gate, const void* up, void* y, cf_dtype dtype, int64_t count,
                     void* stream) {
+    CF_ENTRY();
     if (count <= 0) return CF_OK;
     CF_REQUIRE(gate != nullptr && up != nullptr && y != nullptr, "cf_swiglu: null pointer");
     return cf::run<cf::SwiGlu, true>(gate, up, y, dtype, count, stream, "launching swiglu");

@@ -392,6 +392,21 @@ struct LaunchEvents {
 /// Hand out and disarm the calling thread's armed events.
 LaunchEvents take_launch_events();
 
+/// True when cf_time_next_launch() left events armed on the calling thread.
+bool launch_events_armed();
+
+/// Scope of one operator entry point: events armed by cf_time_next_launch()
+/// belong to the entry point's first kernel launch, and an entry point that
+/// returns without launching (empty input, invalid argument, unsupported
+/// shape) disarms them on the way out, so they never time an unrelated
+/// later launch.
+struct EntryScope {
+    EntryScope() = default;
+    EntryScope(const EntryScope&) = delete;
+    EntryScope& operator=(const EntryScope&) = delete;
+    ~EntryScope() { take_launch_events(); }
+};
+
 /// Keep a launch error that did not go through hipGetLastError for the next
 /// check_launch() on this thread.
 void note_launch_error(hipError_t error);
@@ -452,6 +467,9 @@ constexpr T ceil_div(T a, T b) {
 }
 
 }  // namespace cf
+
+/// First statement of every entry point that launches kernels.
+#define CF_ENTRY() const ::cf::EntryScope cf_entry_scope_
 
 /// Return early with CF_ERR_INVALID_ARGUMENT and a message when `cond` fails.
 #define CF_REQUIRE(cond, ...)                                                   \

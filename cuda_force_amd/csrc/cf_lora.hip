@@ -27,8 +27,6 @@
 namespace cf {
 namespace {
 
-constexpr int kMaxRank = 64;
-
 // ---------------------------------------------------------------------------
 // Generic path.
 // ---------------------------------------------------------------------------
@@ -302,10 +300,9 @@ size_t cf_lora_workspace_bytes(int64_t batch, int64_t rank) {
 cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void* b, void* y,
                          float* xa_out, cf_dtype dtype, int64_t batch, int64_t in_features,
                          int64_t out_features, int64_t rank, float scale, void* stream) {
+    CF_ENTRY();
     if (batch <= 0 || out_features <= 0) return CF_OK;
     CF_REQUIRE(in_features >= 0 && rank >= 0, "cf_lora_linear: negative dimension");
-    CF_REQUIRE(rank <= cf::kMaxRank, "cf_lora_linear: rank %lld exceeds the supported %d",
-               static_cast<long long>(rank), cf::kMaxRank);
     CF_REQUIRE(x != nullptr && w != nullptr && y != nullptr, "cf_lora_linear: null pointer");
     CF_REQUIRE(rank == 0 || (a != nullptr && b != nullptr), "cf_lora_linear: null adapter");
     CF_REQUIRE(dtype == CF_F32 || dtype == CF_BF16,
@@ -330,6 +327,7 @@ cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void
 
 cf_status cf_matmul(const void* a, const void* b, void* c, cf_dtype dtype, int64_t m, int64_t n,
                     int64_t k, void* stream) {
+    CF_ENTRY();
     if (m <= 0 || n <= 0) return CF_OK;
     CF_REQUIRE(a != nullptr && b != nullptr && c != nullptr, "cf_matmul: null pointer");
     CF_REQUIRE(dtype == CF_F32 || dtype == CF_BF16, "cf_matmul: dtype %s has no kernel",
@@ -361,11 +359,10 @@ cf_status cf_lora_backward(const void* x, const void* dy, const void* b, const f
                            void* grad_a, void* grad_b, cf_dtype dtype, int64_t batch,
                            int64_t in_features, int64_t out_features, int64_t rank, float scale,
                            void* workspace, size_t workspace_bytes, void* stream) {
+    CF_ENTRY();
     if (rank <= 0) return CF_OK;
     CF_REQUIRE(batch >= 0 && in_features >= 0 && out_features >= 0,
                "cf_lora_backward: negative dimension");
-    CF_REQUIRE(rank <= cf::kMaxRank, "cf_lora_backward: rank %lld exceeds the supported %d",
-               static_cast<long long>(rank), cf::kMaxRank);
     CF_REQUIRE(dtype == CF_F32 || dtype == CF_BF16, "cf_lora_backward: dtype %s has no kernel",
                cf::dtype_name(dtype));
     CF_REQUIRE(grad_a != nullptr && grad_b != nullptr, "cf_lora_backward: null gradient output");

@@ -31,9 +31,10 @@
 //     one extra MFMA per 16 rows; each wave covers 32 of its 64 rows, ~6%
 //     extra MFMA work, and x is read from HBM once.
 //   * Epilogue: x @ a (rounded to bf16, as the reference materialises it) is
-//     exchanged through LDS, bf16(scale * b) is read transposed from an LDS
-//     copy of b loaded at kernel start, and one v_mfma_f32_16x16x16_bf16 per
-//     16x16 block accumulates the adapter term into the base accumulators.
+//     exchanged through LDS, b is read transposed from an LDS copy loaded at
+//     kernel start, scale * b is split into bf16 high and low parts, and two
+//     v_mfma_f32_16x16x16_bf16 per 16x16 block accumulate the adapter term
+//     into the base accumulators.
 //     The tile is rounded to bf16, staged per wave in LDS and written as
 //     whole 256-byte row pieces with non-temporal 16-byte stores (or kept in
 //     fp32 and stored from registers, 16 bytes per lane, for the fp32-output
@@ -438,7 +439,12 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         }
         __syncthreads();
 
-        // acc += bf16(scale * b)^T-block @ bf16(x @ a)^T-block, K = 16.
+        // acc += scale * (b^T-block @ bf16(x @ a)^T-block), K = 16. scale * b
+        // is formed in fp32 and split into two bf16 parts, hi + lo, each
+        // multiplied by the bf16 x @ a on the MFMA units into the base
+        // accumulators: the adapter term carries about 2^-17 relative error
+        // for any scale (a single bf16(scale * b) would carry 2^-9 whenever
+        // the scale is not a power of two), and no extra registers are live.
         // b is read transposed: lane j of group g reads b row 4g + j/4,
         // columns 4(j%4) .. +3 of the block and receives column j's four
         // adapter rows 4g .. 4g + 3.
@@ -450,22 +456,29 @@ void lora_fused_bf16_kernel(FusedArgs args) {
                 __builtin_bit_cast(s16x4_t, xa_lds[(wm * 4 + ((i + 2 * wn) & 3)) * 64 + lane]);
         }
         const uint8_t* tb = lds + kOffB;
+        // Two passes (high parts, then low parts) keep one b fragment live.
 #pragma unroll
-        for (int jb = 0; jb < 8; ++jb) {
-            const int row = 4 * g + (jl >> 2);
-            const int chunk = 2 * (wn * 8 + jb) + ((jl & 3) >> 1);
-            const s16x4_t raw =
-                lds_read_tr(tb, row * (kBN * 2) + ((chunk ^ b_swizzle(row)) << 4) + (jl & 1) * 8);
-            s16x4_t bfrag;
+        for (int part = 0; part < 2; ++part) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float v = scale * bf16_bits_to_f32(static_cast<uint16_t>(raw[e]));
-                bfrag[e] = static_cast<short>(f32_to_bf16_bits(v));
-            }
+            for (int jb = 0; jb < 8; ++jb) {
+                const int row = 4 * g + (jl >> 2);
+                const int chunk = 2 * (wn * 8 + jb) + ((jl & 3) >> 1);
+                const s16x4_t raw = lds_read_tr(
+                    tb, row * (kBN * 2) + ((chunk ^ b_swizzle(row)) << 4) + (jl & 1) * 8);
+                s16x4_t bfrag;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[jb][i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bfrag, xa_frag[i], acc[jb][i],
-                                                                       0, 0, 0);
+                for (int e = 0; e < 4; ++e) {
+                    const float v = scale * bf16_bits_to_f32(static_cast<uint16_t>(raw[e]));
+                    const uint32_t hi = f32_to_bf16_bits(v);
+                    bfrag[e] = static_cast<short>(
+                        part == 0 ? hi
+                                  : f32_to_bf16_bits(v - bf16_bits_to_f32(static_cast<uint16_t>(hi))));
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc[jb][i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bfrag, xa_frag[i],
+                                                                           acc[jb][i], 0, 0, 0);
+                }
             }
         }
     }

@@ -384,6 +384,7 @@ int cf_matmul_fp8_shape_supported(int64_t m, int64_t n, int64_t k) {
 
 cf_status cf_matmul_fp8(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k, float scale,
                         void* stream) {
+    CF_ENTRY();
     if (!cf_matmul_fp8_shape_supported(m, n, k)) {
         return cf::fail(CF_ERR_UNSUPPORTED,
                         "cf_matmul_fp8: shape %lld x %lld x %lld is not tiled (k must be a positive multiple "

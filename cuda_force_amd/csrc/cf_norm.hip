@@ -506,6 +506,7 @@ extern "C" {
 
 cf_status cf_rmsnorm(const void* x, const void* w, void* y, cf_dtype dtype, int64_t rows,
                      int64_t cols, float eps, void* stream) {
+    CF_ENTRY();
     if (rows <= 0 || cols <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && w != nullptr && y != nullptr, "cf_rmsnorm: null pointer");
     return cf::run<false>(x, nullptr, w, y, nullptr, dtype, rows, cols, eps, stream);
@@ -514,6 +515,7 @@ cf_status cf_rmsnorm(const void* x, const void* w, void* y, cf_dtype dtype, int6
 cf_status cf_fused_residual_rmsnorm(const void* x, const void* residual, const void* w, void* y,
                                     void* residual_out, cf_dtype dtype, int64_t rows,
                                     int64_t cols, float eps, void* stream) {
+    CF_ENTRY();
     if (rows <= 0 || cols <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && residual != nullptr && w != nullptr && y != nullptr &&
                    residual_out != nullptr,

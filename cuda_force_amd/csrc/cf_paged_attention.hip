@@ -609,6 +609,7 @@ cf_status cf_paged_attention(const void* query, const void* k_cache, const void*
                              int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
                              int64_t max_blocks_per_sequence, float scale, void* workspace,
                              size_t workspace_bytes, void* stream) {
+    CF_ENTRY();
     if (num_sequences <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
         max_blocks_per_sequence <= 0) {
         return CF_OK;

@@ -576,6 +576,7 @@ extern "C" {
 cf_status cf_quantize_int8_group(const void* const* x, cf_dtype x_dtype, int8_t* const* q,
                                  float* const* scales, const int64_t* counts, int64_t n_tensors,
                                  void* stream) {
+    CF_ENTRY();
     if (n_tensors <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && q != nullptr && scales != nullptr && counts != nullptr,
                "cf_quantize_int8_group: null array");
@@ -595,6 +596,7 @@ cf_status cf_quantize_int8_group(const void* const* x, cf_dtype x_dtype, int8_t*
 cf_status cf_dequantize_int8_group(const int8_t* const* q, const float* const* scales,
                                    void* const* y, cf_dtype y_dtype, const int64_t* counts,
                                    int64_t n_tensors, void* stream) {
+    CF_ENTRY();
     if (n_tensors <= 0) return CF_OK;
     CF_REQUIRE(q != nullptr && scales != nullptr && y != nullptr && counts != nullptr,
                "cf_dequantize_int8_group: null array");
@@ -617,6 +619,7 @@ int64_t cf_quant_scale_count(int64_t count) {
 
 cf_status cf_quantize_int8(const void* x, cf_dtype x_dtype, int8_t* q, float* scales,
                            int64_t count, void* stream) {
+    CF_ENTRY();
     if (count <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && q != nullptr && scales != nullptr,
                "cf_quantize_int8: null pointer (x=%p q=%p scales=%p)", x,
@@ -636,6 +639,7 @@ cf_status cf_quantize_int8(const void* x, cf_dtype x_dtype, int8_t* q, float* sc
 
 cf_status cf_dequantize_int8(const int8_t* q, const float* scales, void* y, cf_dtype y_dtype,
                              int64_t count, void* stream) {
+    CF_ENTRY();
     if (count <= 0) return CF_OK;
     CF_REQUIRE(q != nullptr && scales != nullptr && y != nullptr,
                "cf_dequantize_int8: null pointer");
@@ -654,6 +658,7 @@ cf_status cf_dequantize_int8(const int8_t* q, const float* scales, void* y, cf_d
 
 cf_status cf_quantize_dequantize(const void* x, void* y, cf_dtype dtype, int64_t count,
                                  void* stream) {
+    CF_ENTRY();
     if (count <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && y != nullptr, "cf_quantize_dequantize: null pointer");
     auto s = static_cast<hipStream_t>(stream);

@@ -189,6 +189,7 @@ size_t cf_reduce_sum_workspace_bytes(int64_t count) {
 
 cf_status cf_reduce_sum(const void* x, cf_dtype x_dtype, float* out, int64_t count,
                         void* workspace, size_t workspace_bytes, int accumulate, void* stream) {
+    CF_ENTRY();
     if (count <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && out != nullptr, "cf_reduce_sum: null pointer");
     const size_t needed = cf_reduce_sum_workspace_bytes(count);
@@ -210,6 +211,7 @@ cf_status cf_reduce_sum(const void* x, cf_dtype x_dtype, float* out, int64_t cou
 
 cf_status cf_row_sum(const void* x, cf_dtype x_dtype, float* out, int64_t rows, int64_t cols,
                      void* stream) {
+    CF_ENTRY();
     if (rows <= 0 || cols <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && out != nullptr, "cf_row_sum: null pointer");
     auto s = static_cast<hipStream_t>(stream);

@@ -53,6 +53,10 @@ LaunchEvents take_launch_events() {
     return events;
 }
 
+bool launch_events_armed() {
+    return g_launch_events.start != nullptr || g_launch_events.stop != nullptr;
+}
+
 void note_launch_error(hipError_t error) { g_pending_launch_error = error; }
 
 cf_status check_launch(const char* what, hipStream_t stream) {
@@ -191,7 +195,10 @@ cf_status cf_time_next_launch(void* start_event, void* stop_event) {
     return CF_OK;
 }
 
+int cf_time_next_launch_armed(void) { return cf::launch_events_armed() ? 1 : 0; }
+
 cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int divisor, void* stream) {
+    CF_ENTRY();
     if (read_bytes <= 0) return CF_OK;
     CF_REQUIRE(src != nullptr && dst != nullptr, "cf_stream_bytes: null pointer");
     CF_REQUIRE(divisor == 1 || divisor == 2 || divisor == 4, "cf_stream_bytes: divisor %d is not 1, 2 or 4",
@@ -219,6 +226,7 @@ cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int di
 }
 
 cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream) {
+    CF_ENTRY();
     if (bytes <= 0) return CF_OK;
     CF_REQUIRE(src != nullptr && dst != nullptr, "cf_copy_bytes: null pointer");
     auto s = static_cast<hipStream_t>(stream);

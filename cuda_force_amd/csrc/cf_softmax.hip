@@ -241,6 +241,7 @@ extern "C" {
 
 cf_status cf_softmax(const void* x, cf_dtype x_dtype, void* y, cf_dtype y_dtype, int64_t rows,
                      int64_t cols, void* stream) {
+    CF_ENTRY();
     if (rows <= 0 || cols <= 0) return CF_OK;
     CF_REQUIRE(x != nullptr && y != nullptr, "cf_softmax: null pointer");
     CF_REQUIRE(x != y || x_dtype == y_dtype,

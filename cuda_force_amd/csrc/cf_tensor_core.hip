@@ -177,6 +177,7 @@ size_t cf_matmul_tensor_core_workspace_bytes(int64_t m, int64_t n, int64_t k) {
 
 cf_status cf_matmul_tensor_core(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
                                 void* workspace, size_t workspace_bytes, void* stream) {
+    CF_ENTRY();
     if (!cf_matmul_tensor_core_shape_supported(m, n, k)) {
         return cf::fail(CF_ERR_UNSUPPORTED,
                         "cf_matmul_tensor_core: shape %lld x %lld x %lld is not tiled (n must be a "

@@ -203,7 +203,9 @@ size_t cf_lora_workspace_bytes(int64_t batch, int64_t rank);
  * adapter intermediate x @ a is rounded to bf16 before the up-projection, as the
  * reference's ATen path does. When `xa_out` is non-NULL the fp32 adapter
  * intermediate x @ a ([batch, rank], before that rounding) is also written
- * there (the autograd path keeps it for the backward). rank <= 64.
+ * there (the autograd path keeps it for the backward). Any rank >= 0: bf16
+ * problems with an even rank <= 16 run the fused MFMA kernel, every other
+ * rank the unfused path (cf_lora_workspace_bytes of xa_out required).
  * Replaces launch_lora_linear (cuda/include/cudaforge/lora_linear.cuh:49-51). */
 cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void* b, void* y,
                          float* xa_out, cf_dtype dtype, int64_t batch, int64_t in_features,
@@ -351,11 +353,17 @@ cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int di
  * the call. Every kernel of the library launches through this hook; for an
  * entry point that launches several kernels (the two-stage sum, the adapter
  * backward, split-K matmuls, context-split paged attention) the first one is
- * timed. An entry point that returns without launching leaves the events
- * armed for the next launch. Both NULL disarms. It has no counterpart in the
- * reference, whose benchmarks bracket each launch with an event pair
- * (benchmarks/benchmark_kernels.cu:59-79). */
+ * timed. The events belong to the next operator entry point the thread
+ * calls: one that returns without launching (empty input, an invalid
+ * argument, an unsupported shape) disarms them, so they never time a later,
+ * unrelated launch. Runtime calls (scheduler, pools) leave them armed. Both
+ * NULL disarms. It has no counterpart in the reference, whose benchmarks
+ * bracket each launch with an event pair (benchmarks/benchmark_kernels.cu:59-79). */
 cf_status cf_time_next_launch(void* start_event, void* stop_event);
+
+/* 1 while cf_time_next_launch() has events armed on the calling thread, else
+ * 0. A diagnostic for the hook above; no counterpart in the reference. */
+int cf_time_next_launch_armed(void);
 
 /* ---- runtime: stream scheduler and caching pools ------------------------
  *

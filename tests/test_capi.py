@@ -68,11 +68,13 @@ def test_invalid_arguments_are_reported_not_thrown(lib):
     status = lib.cf_quantize_int8(null, _lib.CF_F32, null, null, 10, null)
     assert status == _lib.CF_ERR_INVALID_ARGUMENT
     assert b"null pointer" in lib.cf_last_error()
+    # Any rank is taken (large ranks run the generic path); an unfused shape
+    # without the xa workspace is an argument error raised before any launch.
     status = lib.cf_lora_linear(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
-                                ctypes.c_void_p(16), ctypes.c_void_p(16), null, _lib.CF_BF16,
-                                8, 8, 8, 65, 1.0, null)
+                                ctypes.c_void_p(16), ctypes.c_void_p(16), null, _lib.CF_F32,
+                                8, 8, 8, 128, 1.0, null)
     assert status == _lib.CF_ERR_INVALID_ARGUMENT
-    assert b"rank 65" in lib.cf_last_error()
+    assert b"xa_out" in lib.cf_last_error()
     status = lib.cf_lora_linear(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                 ctypes.c_void_p(16), ctypes.c_void_p(16), null, _lib.CF_F16,
                                 8, 8, 8, 4, 1.0, null)
@@ -124,6 +126,35 @@ def test_time_next_launch_takes_both_events_or_neither(lib):
     assert lib.cf_time_next_launch(fake, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_time_next_launch(null, fake) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_time_next_launch(null, null) == _lib.CF_OK
+
+
+def test_an_entry_point_that_launches_nothing_disarms_the_timing_events(lib):
+    """Armed events belong to the next operator call: one that returns before
+    launching (empty input, invalid argument) must not leave them for a later,
+    unrelated launch. The fake handles are never used: nothing launches."""
+    null = ctypes.c_void_p(0)
+    fake_start, fake_stop = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000)
+    assert lib.cf_time_next_launch_armed() == 0
+    calls = [
+        lambda: lib.cf_rmsnorm(null, null, null, _lib.CF_BF16, 0, 4096, 1e-6, null),         # empty
+        lambda: lib.cf_reduce_sum(null, _lib.CF_F32, null, 0, null, 0, 1, null),              # empty
+        lambda: lib.cf_quantize_int8(null, _lib.CF_F32, null, null, 10, null),                # null pointer
+        lambda: lib.cf_softmax(null, _lib.CF_F32, null, 7, 4, 4, null),                       # bad dtype
+        lambda: lib.cf_matmul_tensor_core(null, null, null, 4, 5, 4, null, 0, null),          # unsupported
+        lambda: lib.cf_lora_backward(null, null, null, null, null, null, _lib.CF_F32, 8, 8, 8, 0, 1.0,
+                                     null, 0, null),                                          # rank 0
+    ]
+    for call in calls:
+        assert lib.cf_time_next_launch(fake_start, fake_stop) == _lib.CF_OK
+        assert lib.cf_time_next_launch_armed() == 1
+        call()
+        assert lib.cf_time_next_launch_armed() == 0
+    # Runtime calls are not operator launches: they leave the events armed.
+    assert lib.cf_time_next_launch(fake_start, fake_stop) == _lib.CF_OK
+    assert lib.cf_pool_backend_name(_lib.CF_POOL_HOST) == b"host"
+    assert lib.cf_time_next_launch_armed() == 1
+    assert lib.cf_time_next_launch(null, null) == _lib.CF_OK
+    assert lib.cf_time_next_launch_armed() == 0
 
 
 def test_grouped_quantisation_host_checks(lib):

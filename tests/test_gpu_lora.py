@@ -121,6 +121,11 @@ def test_zero_b_reduces_to_the_base_layer_and_scale_is_linear():
 
 
 def test_config3_full_size():
+    """Config 3 at full size, every output element against the float64 oracle
+    (so every 256 x 256 tile, every row residue and both wave halves of each
+    tile are checked), plus float64 column sums over each 256-row band of the
+    output against the same sums of the oracle's formula (a check that a tile
+    written twice or never cannot pass)."""
     g.announce("config 3: fused LoRA bf16 8192x4096x4096 r16")
     gen = rng(3003)
     m, k, n, r = 8192, 4096, 4096, 16
@@ -132,12 +137,73 @@ def test_config3_full_size():
     B = oracle.f32_to_bf16_bits((0.02 * gen.standard_normal((n, r), dtype=np.float32)))
     w, a, b = (np.ascontiguousarray(t.T) for t in (W, A, B))
     y, xa = run_lora(x, w, a, b, "bf16", 32 / 16)
-    rows = rng(3004).choice(m, size=48, replace=False)
-    xv = g.host_values(x[rows], "bf16")
-    wv, av, bv = (g.host_values(t, "bf16") for t in (w, a, b))
-    assert_gemm_close(y[rows], oracle.lora_linear(xv, wv, av, bv, 2.0, True), "bf16", "config 3 (48 rows)")
-    np.testing.assert_allclose(xa[rows], xv.astype(np.float64) @ av, rtol=1e-3, atol=1e-3)
-    assert np.isfinite(g.host_values(y, "bf16")).all()
+    xv, wv, av, bv = (g.host_values(t, "bf16") for t in (x, w, a, b))
+    exact = oracle.lora_linear(xv, wv, av, bv, 2.0, True)
+    assert_gemm_close(y, exact, "bf16", "config 3 (all 8192 x 4096 outputs)")
+    np.testing.assert_allclose(xa, xv.astype(np.float64) @ av, rtol=1e-3, atol=1e-3)
+    # Band column sums: each output's bf16 rounding is at most 2^-8 of it, so
+    # a band's sum may move by at most 2^-8 * sum |y| (plus the fp32
+    # accumulation error, far smaller); a missing or duplicated 256-row tile
+    # moves it by about sqrt(256) times a typical |y|.
+    got = g.host_values(y, "bf16").astype(np.float64).reshape(m // 256, 256, n)
+    want = exact.reshape(m // 256, 256, n)
+    bound = 2.0**-8 * np.abs(got).sum(axis=1) * 1.01 + 1e-6 * np.abs(want).max()
+    assert (np.abs(got.sum(axis=1) - want.sum(axis=1)) <= bound).all()
+
+
+@pytest.mark.parametrize("shape,scale", [((512, 1024, 768, 16), 32 / 12), ((300, 512, 264, 12), 16 / 12)], ids=str)
+def test_fused_bf16_non_power_of_two_scale(shape, scale):
+    """alpha / rank that is not a power of two: the adapter term must carry no
+    rounding beyond the reference's bf16 x @ a. With w = 0 the output is
+    scale * bf16(x @ a) @ b alone. Taking bf16(x @ a) from the kernel's own
+    fp32 x @ a (xa_out; the oracle's float64 x @ a can round to the other bf16
+    neighbour), each stored value must be the exact value rounded once to
+    bf16: within 2^-8 of it, plus 2^-14 of sum_j |scale xa_j b_j| for the
+    arithmetic. Rounding bf16(scale * b) first leaves up to 2^-9 of that sum."""
+    m, k, n, r = shape
+    x, w, a, b = make_operands(m, k, n, r, "bf16", seed=m + n + r)
+    xv, wv, av, bv = (g.host_values(t, "bf16") for t in (x, w, a, b))
+    y, _ = run_lora(x, w, a, b, "bf16", scale)
+    assert_gemm_close(y, oracle.lora_linear(xv, wv, av, bv, scale, True), "bf16", f"scale {scale:.4f} {shape}")
+    y0, xa = run_lora(x, np.zeros_like(w), a, b, "bf16", scale)
+    xa_bf16 = oracle.round_bf16(xa[:, :r].astype(np.float64))
+    exact = scale * (xa_bf16 @ bv.astype(np.float64))
+    arithmetic = abs(scale) * (np.abs(xa_bf16) @ np.abs(bv.astype(np.float64)))
+    err = np.abs(g.host_values(y0, "bf16").astype(np.float64) - exact)
+    bad = err > 2.0**-8 * np.abs(exact) + 2.0**-14 * arithmetic
+    assert not bad.any(), f"{bad.sum()} outputs off by more than one bf16 rounding, max err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_large_rank_forward_and_backward(dtype):
+    """Rank 128 (above the fused kernel's 16): the generic path takes any rank,
+    forward and adapter backward, against the oracle."""
+    m, k, n, r = 200, 256, 136, 128
+    x, w, a, b = make_operands(m, k, n, r, dtype, seed=128)
+    y, xa = run_lora(x, w, a, b, dtype, 0.125)
+    xv, wv, av, bv = (g.host_values(t, dtype) for t in (x, w, a, b))
+    assert_gemm_close(y, oracle.lora_linear(xv, wv, av, bv, 0.125, dtype == "bf16"), dtype, f"rank 128 {dtype}")
+    gen = rng(129)
+    dy = g.storage_bits(gen.standard_normal((m, n)).astype(np.float32), dtype)
+    ga, gb = run_backward(x, dy, b, xa, dtype, 0.125)
+    exact_a, exact_b = oracle.lora_backward(xv, g.host_values(dy, dtype), bv, xa, 0.125, dtype == "bf16")
+    assert_gemm_close(ga, exact_a, dtype, f"grad_a rank 128 {dtype}")
+    assert_gemm_close(gb, exact_b, dtype, f"grad_b rank 128 {dtype}")
+
+
+def run_backward(x, dy, b, xa, dtype: str, scale: float):
+    m, k = x.shape
+    r, n = b.shape
+    xg, dyg, bg = g.to_gpu(x, dtype), g.to_gpu(dy, dtype), g.to_gpu(b, dtype)
+    xag = g.to_gpu(np.ascontiguousarray(xa, dtype=np.float32))
+    ga = g.empty((k, r), g.torch_dtype(dtype))
+    gb = g.empty((r, n), g.torch_dtype(dtype))
+    nbytes = g.lib().cf_lora_backward_workspace_bytes(m, k, n, r)
+    ws = g.empty(nbytes, torch.uint8)
+    g.call("cf_lora_backward", xg.data_ptr(), dyg.data_ptr(), bg.data_ptr(), xag.data_ptr(), ga.data_ptr(),
+           gb.data_ptr(), g.cf(dtype), m, k, n, r, scale, ws.data_ptr(), nbytes, g.stream())
+    torch.cuda.synchronize()
+    return g.to_host(ga), g.to_host(gb)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -154,20 +220,12 @@ def test_adapter_backward(dtype, shape):
     dy = g.storage_bits(gen.standard_normal((m, n)).astype(np.float32), dtype)
     b = g.storage_bits((0.02 * gen.standard_normal((r, n))).astype(np.float32), dtype)
     xa = (gen.standard_normal((m, r)) * 0.5).astype(np.float32)
-    xg, dyg, bg = g.to_gpu(x, dtype), g.to_gpu(dy, dtype), g.to_gpu(b, dtype)
-    xag = g.to_gpu(xa)
-    ga = g.empty((k, r), g.torch_dtype(dtype))
-    gb = g.empty((r, n), g.torch_dtype(dtype))
-    nbytes = g.lib().cf_lora_backward_workspace_bytes(m, k, n, r)
-    ws = g.empty(nbytes, torch.uint8)
-    g.call("cf_lora_backward", xg.data_ptr(), dyg.data_ptr(), bg.data_ptr(), xag.data_ptr(), ga.data_ptr(),
-           gb.data_ptr(), g.cf(dtype), m, k, n, r, 2.0, ws.data_ptr(), nbytes, g.stream())
-    torch.cuda.synchronize()
+    ga, gb = run_backward(x, dy, b, xa, dtype, 2.0)
     exact_a, exact_b = oracle.lora_backward(
         g.host_values(x, dtype), g.host_values(dy, dtype), g.host_values(b, dtype), xa, 2.0, dtype == "bf16"
     )
-    assert_gemm_close(g.to_host(ga), exact_a, dtype, f"grad_a {dtype} {shape}")
-    assert_gemm_close(g.to_host(gb), exact_b, dtype, f"grad_b {dtype} {shape}")
+    assert_gemm_close(ga, exact_a, dtype, f"grad_a {dtype} {shape}")
+    assert_gemm_close(gb, exact_b, dtype, f"grad_b {dtype} {shape}")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])

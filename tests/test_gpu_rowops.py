@@ -64,6 +64,25 @@ def test_rmsnorm_matches_the_oracle(dtype, shape):
     assert_close(y, exact, dtype, f"rmsnorm {dtype} {shape}")
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 128), (4, 2048), (2, 4096), (3, 8192)], ids=str)
+def test_rmsnorm_half_inputs_whose_squares_overflow_fp16(dtype, shape):
+    """Every input 300 (300^2 = 90000 > 65504, fp16's largest value), weight 1:
+    the fp32 sum of squares keeps every output finite and 1 within the
+    reference's 2e-2 relative / 1e-2 absolute (tests/cuda/test_rmsnorm.cu:99-134
+    for fp16, tests/cuda/test_reduced_precision.cu:69-103 for bf16), here at
+    the reference's 2 x 128 and at the row widths of the tiled kernels."""
+    rows, cols = shape
+    x = g.storage_bits(np.full(shape, 300.0, np.float32), dtype)
+    w = g.storage_bits(np.ones(cols, np.float32), dtype)
+    stored = run_rmsnorm(x, w, dtype, 1e-6)
+    y = g.host_values(stored, dtype).astype(np.float64)
+    assert np.isfinite(y).all()
+    assert (np.abs(y - 1.0) <= 1e-2 + 2e-2).all()
+    exact = oracle.rmsnorm(g.host_values(x, dtype), g.host_values(w, dtype), 1e-6)
+    assert_close(stored, exact, dtype, f"rmsnorm |x| = 300 {dtype} {shape}")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_rmsnorm_misaligned_rows_take_the_fallback(dtype):
     r = rng(3)
@@ -239,6 +258,22 @@ def test_softmax_golden_and_extreme_logits():
     np.testing.assert_allclose(y[0], 0.25, rtol=1e-6)
 
 
+@pytest.mark.parametrize("cols", [4, 2048])
+def test_softmax_bf16_logits_fp16_cannot_represent(cols):
+    """Logits 1e5, 9e4, -1e5, 0 in bf16 (tests/cuda/test_reduced_precision.cu:133-173):
+    every output finite, the dominant logit takes the mass (> 0.5; exactly 1
+    after rounding), and the result matches the oracle. The 2048-column row
+    pads with -inf so the wide-row kernel sees the same four logits."""
+    logits = np.full((1, cols), -np.inf, np.float32)
+    logits[0, :4] = [100000.0, 90000.0, -100000.0, 0.0]
+    x = oracle.f32_to_bf16_bits(logits)
+    assert g.host_values(x, "bf16")[0, 0] > g.host_values(x, "bf16")[0, 1]
+    y = g.host_values(run_softmax(x, "bf16", "bf16"), "bf16")
+    assert np.isfinite(y).all()
+    assert y[0, 0] > 0.5
+    assert_close(oracle.f32_to_bf16_bits(y), oracle.softmax(g.host_values(x, "bf16")), "bf16", "softmax +-1e5")
+
+
 def test_softmax_bf16_logits_to_fp32_probabilities_and_misaligned():
     x = oracle.f32_to_bf16_bits(causal(128, 512, 8))
     y = run_softmax(x, "bf16", "f32")
@@ -315,6 +350,17 @@ def test_sum_accumulates_when_asked_and_handles_bf16():
     xb = oracle.f32_to_bf16_bits(rng(12).standard_normal(50_000).astype(np.float32))
     exact = oracle.sum_exact(g.host_values(xb, "bf16"))
     assert abs(run_sum(xb, "bf16") - exact) <= max(abs(exact), 1.0) * 1e-5 * math.sqrt(50_000)
+
+
+def test_an_empty_sum_leaves_the_output_untouched():
+    """count 0 returns without launching, so *out keeps its value whether the
+    call accumulates or overwrites (tests/cuda/test_reduction.cu:73-83, where
+    the reference's launcher always accumulates)."""
+    for accumulate in (1, 0):
+        out = torch.full((1,), 7.5, device=g.DEVICE)
+        g.call("cf_reduce_sum", 0, g.cf("f32"), out.data_ptr(), 0, 0, 0, accumulate, g.stream())
+        torch.cuda.synchronize()
+        assert float(out.item()) == 7.5
 
 
 @pytest.mark.parametrize("shape", [(1, 1), (4, 17), (33, 1023), (128, 512), (3, 100_000)])
