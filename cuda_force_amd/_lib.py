@@ -78,6 +78,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_softmax": (_I32, [_P, _I32, _P, _I32, _I64, _I64, _P]),
     "cf_reduce_sum_workspace_bytes": (_SZ, [_I64]),
     "cf_reduce_sum": (_I32, [_P, _I32, _P, _I64, _P, _SZ, _I32, _P]),
+    "cf_reduce_sum_noalloc": (_I32, [_P, _I32, _P, _I64, _I32, _P]),
     "cf_row_sum": (_I32, [_P, _I32, _P, _I64, _I64, _P]),
     "cf_lora_workspace_bytes": (_SZ, [_I64, _I64]),
     "cf_lora_linear": (_I32, [_P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _F, _P]),

@@ -15,6 +15,12 @@
 //
 // G and the chunk size are functions of `count` only, so the same input gives
 // the same bits on any device and on every run.
+//
+// cf_reduce_sum_noalloc runs the same two launches with the partials in a
+// static device array instead of a caller workspace, for callers that cannot
+// allocate (HIP graph capture, serving loops that forbid hipMalloc).
+#include <mutex>
+
 #include "cf_common.hpp"
 
 namespace cf {
@@ -178,6 +184,39 @@ cf_status launch_row_sum(const void* x, float* out, int64_t rows, int64_t cols,
 }
 
 }  // namespace
+
+/// Device address of `scratch` (below) on the current device, looked up
+/// once per device with that device current and kept; never the host-side
+/// name of the array, which is no device address.
+cf_status noalloc_scratch(void** out);
+
+}  // namespace cf
+
+// Stage-1 partials of cf_reduce_sum_noalloc: every count needs at most
+// kMaxPartials of them (16 KiB). Each device holds its own copy for the life
+// of the process; all calls on one device share it.
+static __device__ __align__(256) float scratch[cf::kMaxPartials];
+
+namespace cf {
+
+cf_status noalloc_scratch(void** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mutex;
+    static void* cached[kMaxDevices] = {};
+    int device = 0;
+    CF_HIP_TRY(hipGetDevice(&device));
+    CF_REQUIRE(device >= 0 && device < kMaxDevices, "cf_reduce_sum_noalloc: device %d out of range", device);
+    std::lock_guard<std::mutex> lock(mutex);
+    if (cached[device] == nullptr) {
+        void* ptr = nullptr;
+        CF_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        CF_REQUIRE(ptr != nullptr, "cf_reduce_sum_noalloc: no device address for the scratch array");
+        cached[device] = ptr;
+    }
+    *out = cached[device];
+    return CF_OK;
+}
+
 }  // namespace cf
 
 extern "C" {
@@ -207,6 +246,35 @@ cf_status cf_reduce_sum(const void* x, cf_dtype x_dtype, float* out, int64_t cou
     }
     return cf::fail(CF_ERR_UNSUPPORTED, "cf_reduce_sum: unknown dtype %d",
                     static_cast<int>(x_dtype));
+}
+
+cf_status cf_reduce_sum_noalloc(const void* x, cf_dtype x_dtype, float* out, int64_t count,
+                                int accumulate, void* stream) {
+    CF_ENTRY();
+    if (count <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && out != nullptr, "cf_reduce_sum_noalloc: null pointer");
+    const size_t needed = cf_reduce_sum_workspace_bytes(count);
+    CF_REQUIRE(needed <= sizeof(scratch),
+               "cf_reduce_sum_noalloc: %lld elements need %zu bytes of partials, above the %zu-byte "
+               "static scratch",
+               static_cast<long long>(count), needed, sizeof(scratch));
+    if (x_dtype != CF_F32 && x_dtype != CF_BF16 && x_dtype != CF_F16) {
+        return cf::fail(CF_ERR_UNSUPPORTED, "cf_reduce_sum_noalloc: unknown dtype %d",
+                        static_cast<int>(x_dtype));
+    }
+    void* partials = nullptr;
+    const cf_status found = cf::noalloc_scratch(&partials);
+    if (found != CF_OK) return found;
+    auto s = static_cast<hipStream_t>(stream);
+    switch (x_dtype) {
+        case CF_F32:
+            return cf::launch_sum<float>(x, out, count, partials, accumulate, s);
+        case CF_BF16:
+            return cf::launch_sum<cf::bf16_t>(x, out, count, partials, accumulate, s);
+        case CF_F16:
+            return cf::launch_sum<cf::f16_t>(x, out, count, partials, accumulate, s);
+    }
+    return CF_ERR_UNSUPPORTED;
 }
 
 cf_status cf_row_sum(const void* x, cf_dtype x_dtype, float* out, int64_t rows, int64_t cols,

@@ -184,6 +184,19 @@ size_t cf_reduce_sum_workspace_bytes(int64_t count);
 cf_status cf_reduce_sum(const void* x, cf_dtype x_dtype, float* out, int64_t count,
                         void* workspace, size_t workspace_bytes, int accumulate, void* stream);
 
+/* cf_reduce_sum without a workspace and without allocating: the stage-1
+ * partial sums go to a static device array of 16 KiB (4096 floats, the most
+ * any count needs; a count whose partials would not fit is
+ * CF_ERR_INVALID_ARGUMENT), which each device holds until the process ends.
+ * Same kernels, same result bits as cf_reduce_sum. Calls no hipMalloc /
+ * hipFree. Every call on one device shares that device's array: calls that
+ * overlap on one device (two streams, or two threads without ordering) race
+ * and must be serialised by the caller. It has no counterpart in the
+ * reference; it is for callers that cannot allocate: code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc. */
+cf_status cf_reduce_sum_noalloc(const void* x, cf_dtype x_dtype, float* out, int64_t count,
+                                int accumulate, void* stream);
+
 /* Per-row sums of a row-major [rows, cols] matrix into fp32 `out[rows]`.
  * Replaces launch_row_sum (cuda/include/cudaforge/reduction.cuh:48). */
 cf_status cf_row_sum(const void* x, cf_dtype x_dtype, float* out, int64_t rows, int64_t cols,
