@@ -248,9 +248,10 @@ def bench_main_step(torch, cf, steps: int, warmup: int) -> dict:
         cf._lib.check(lib.cf_rmsnorm(x.data_ptr(), w.data_ptr(), y.data_ptr(), CF_BF16, rows, cols, 1e-6, stream))
         cf._lib.check(lib.cf_softmax(lx.data_ptr(), CF_BF16, ly.data_ptr(), CF_BF16, s_rows, s_cols, stream))
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
+    # The untimed warm-up: at least `warmup` steps and WARMUP_SECONDS of them,
+    # so the clocks have ramped before the timed steps (a step timed from an
+    # idle GPU reads several percent slow).
+    warm(torch, [lambda i=i: step(i) for i in range(nsets)], warmup)
     # Every TIMER_STRIDE-th RMSNorm launch of the timed region records its
     # own start and end timestamps on an event pair (cf_time_next_launch):
     # no extra packets enter the queue. A timed dispatch still costs its step
@@ -436,54 +437,62 @@ def bench_reduce(torch, cf, warmup: int, runs: int) -> dict:
 
 
 def bench_lora(torch, cf, warmup: int, runs: int) -> dict:
-    """config 3: fused LoRA bf16 8192x4096x4096 r16, alpha 32; adapter backward."""
+    """config 3: fused LoRA bf16 8192x4096x4096 r16, alpha 32; adapter backward.
+    Operand sets (x, W, A, B, y, dY, x@A) rotate until they exceed 1 GiB, so the
+    forward and the backward read their operands from HBM, not from the 256 MB
+    Infinity Cache; hipBLASLt's plain GEMM runs on the same sets."""
     gen = torch.Generator(device="cuda").manual_seed(4)
     m, k, n, r = 8192, 4096, 4096, 16
-    x = torch.randn(m, k, generator=gen, device="cuda").to(torch.bfloat16)
-    W = (0.02 * torch.randn(n, k, generator=gen, device="cuda")).to(torch.bfloat16)
-    A = (torch.randn(r, k, generator=gen, device="cuda") / 64).to(torch.bfloat16)
-    B = (0.02 * torch.randn(n, r, generator=gen, device="cuda")).to(torch.bfloat16)
-    w, a, b = W.t().contiguous(), A.t().contiguous(), B.t().contiguous()
-    y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-    xa = torch.empty(m, r, device="cuda")
     lib = cf._lib.load()
     flops = flops_lora(m, k, n, r)
+    set_bytes = (m * k + k * n + 2 * m * n) * 2 + (k * r + r * n) * 2 + m * r * 4
+    sets = []
+    for _ in range(sets_for(set_bytes)):
+        x = torch.randn(m, k, generator=gen, device="cuda").to(torch.bfloat16)
+        W = (0.02 * torch.randn(n, k, generator=gen, device="cuda")).to(torch.bfloat16)
+        A = (torch.randn(r, k, generator=gen, device="cuda") / 64).to(torch.bfloat16)
+        B = (0.02 * torch.randn(n, r, generator=gen, device="cuda")).to(torch.bfloat16)
+        sets.append({"x": x, "w": W.t().contiguous(), "a": A.t().contiguous(), "b": B.t().contiguous(),
+                     "y": torch.empty(m, n, dtype=torch.bfloat16, device="cuda"),
+                     "dy": torch.randn(m, n, generator=gen, device="cuda").to(torch.bfloat16),
+                     "xa": torch.empty(m, r, device="cuda")})
+        del W, A, B
 
-    def fused():
-        cf._lib.check(lib.cf_lora_linear(x.data_ptr(), w.data_ptr(), a.data_ptr(), b.data_ptr(), y.data_ptr(),
-                                         None, cf._lib.CF_BF16, m, k, n, r, 2.0,
-                                         torch.cuda.current_stream().cuda_stream))
+    def fused(s, xa_out=None):
+        return lambda: cf._lib.check(lib.cf_lora_linear(
+            s["x"].data_ptr(), s["w"].data_ptr(), s["a"].data_ptr(), s["b"].data_ptr(), s["y"].data_ptr(),
+            xa_out, cf._lib.CF_BF16, m, k, n, r, 2.0, torch.cuda.current_stream().cuda_stream))
 
-    f = summary(time_launches(torch, [fused], warmup, runs))
-    with_kernel_time(torch, cf, f, [fused], flops=flops, peak=PEAK_BF16_TFLOPS)
-    out = {"lora_bf16_8192x4096x4096_r16": {**f, "flops": flops, "TFLOP/s": flops / (f["median_ms"] * 1e-3) / 1e12,
+    launches = [fused(s) for s in sets]
+    f = summary(time_launches(torch, launches, warmup, runs))
+    with_kernel_time(torch, cf, f, launches, flops=flops, peak=PEAK_BF16_TFLOPS)
+    out = {"lora_bf16_8192x4096x4096_r16": {**f, "flops": flops, "buffer_sets": len(sets),
+                                             "TFLOP/s": flops / (f["median_ms"] * 1e-3) / 1e12,
                                              "frac_mfma": flops / (f["median_ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}}
 
-    def library_gemm():
-        torch.matmul(x, w, out=y)
-
-    lg = summary(time_launches(torch, [library_gemm], warmup, runs))
+    gemms = [lambda s=s: torch.matmul(s["x"], s["w"], out=s["y"]) for s in sets]
+    lg = summary(time_launches(torch, gemms, warmup, runs))
     base = 2 * m * k * n
     out["hipblaslt_gemm_bf16_8192x4096x4096_context"] = {
         **lg, "TFLOP/s": base / (lg["median_ms"] * 1e-3) / 1e12}
 
-    dy = torch.randn(m, n, generator=gen, device="cuda").to(torch.bfloat16)
+    for s in sets:  # the forward's x @ A, which the backward reads
+        fused(s, s["xa"].data_ptr())()
     ga = torch.empty(k, r, dtype=torch.bfloat16, device="cuda")
     gb = torch.empty(r, n, dtype=torch.bfloat16, device="cuda")
-    cf._lib.check(lib.cf_lora_linear(x.data_ptr(), w.data_ptr(), a.data_ptr(), b.data_ptr(), y.data_ptr(),
-                                     xa.data_ptr(), cf._lib.CF_BF16, m, k, n, r, 2.0,
-                                     torch.cuda.current_stream().cuda_stream))
     nbytes = lib.cf_lora_backward_workspace_bytes(m, k, n, r)
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
 
-    def backward():
-        cf._lib.check(lib.cf_lora_backward(x.data_ptr(), dy.data_ptr(), b.data_ptr(), xa.data_ptr(), ga.data_ptr(),
-                                           gb.data_ptr(), cf._lib.CF_BF16, m, k, n, r, 2.0, ws.data_ptr(), nbytes,
-                                           torch.cuda.current_stream().cuda_stream))
+    def backward(s):
+        return lambda: cf._lib.check(lib.cf_lora_backward(
+            s["x"].data_ptr(), s["dy"].data_ptr(), s["b"].data_ptr(), s["xa"].data_ptr(), ga.data_ptr(),
+            gb.data_ptr(), cf._lib.CF_BF16, m, k, n, r, 2.0, ws.data_ptr(), nbytes,
+            torch.cuda.current_stream().cuda_stream))
 
-    bw = summary(time_launches(torch, [backward], warmup, runs))
+    bw = summary(time_launches(torch, [backward(s) for s in sets], warmup, runs))
     bw_bytes = m * k * 2 + m * n * 2 + m * r * 4 + r * n * 2 + k * r * 2 + r * n * 2
-    out["lora_backward_bf16_8192x4096x4096_r16"] = {**bw, "bytes": bw_bytes, "GB/s": gbs(bw_bytes, bw["median_ms"]),
+    out["lora_backward_bf16_8192x4096x4096_r16"] = {**bw, "bytes": bw_bytes, "buffer_sets": len(sets),
+                                                    "GB/s": gbs(bw_bytes, bw["median_ms"]),
                                                     "frac_hbm": gbs(bw_bytes, bw["median_ms"]) / PEAK_HBM_GBS}
     return out
 
@@ -744,7 +753,8 @@ def cpu_baseline(seconds: float) -> dict | None:
         "cores": results["rmsnorm"]["threads"],
         "kind": "reference",
         "sample": ("reference CPU operators (cpp/src/bindings.cpp rmsnorm_cpu + softmax_cpu via ATen) on "
-                   "the configs[1] step itself: RMSNorm bf16 [16384, 4096] + softmax bf16 [1024, 2048]; "
+                   "the configs[1] step itself: RMSNorm bf16 [16384, 4096] + softmax bf16 [1024, 2048] on "
+                   "causal-masked N(0, 4) logits; "
                    f"median of the calls made in ~{seconds:.0f} s per op (at least 5)"),
         "rmsnorm_median_s": results["rmsnorm"]["median_s"],
         "softmax_median_s": results["softmax"]["median_s"],

@@ -129,7 +129,12 @@ def time_reference(op: str, shape: list[int], dtype: str, seconds: float, thread
         w = (1 + 0.02 * torch.randn(shape[-1], generator=gen)).to(tdtype)
         fn = lambda: torch.ops.cudaforge.rmsnorm(x, w, 1e-6)  # noqa: E731
     elif op == "softmax":
-        x = (2.0 * torch.randn(*shape, generator=gen)).to(tdtype)
+        # Config 2's logits: N(0, 4) with the causal -inf mask of row index
+        # mod cols, as the GPU step times them.
+        rows, cols = shape[0], shape[-1]
+        x = 2.0 * torch.randn(rows, cols, generator=gen)
+        masked = torch.arange(cols)[None, :] > (torch.arange(rows) % cols)[:, None]
+        x = x.masked_fill(masked, float("-inf")).to(tdtype)
         fn = lambda: torch.ops.cudaforge.softmax(x)  # noqa: E731
     elif op == "lora_linear":
         m, k, n, r = shape
