@@ -355,6 +355,25 @@ def bench_rowops(torch, cf, warmup: int, runs: int) -> dict:
         out[label] = {**r, "bytes": sb, "GB/s": gbs(sb, r["median_ms"]),
                       "frac_hbm": gbs(sb, r["median_ms"]) / PEAK_HBM_GBS}
         del sets, launches
+    # Config 4's attention softmax as the block now runs it: softmax(scores /
+    # sqrt(128) + causal) on [8 x 32 x 512, 512] bf16 scores in one pass
+    # (cf_softmax_scaled). Algorithmic bytes: the visible scores read once
+    # (row r of each head block keeps r + 1 columns) plus every output written.
+    s_rows, s_cols = 131072, 512
+    visible = sum((r % s_cols) + 1 for r in range(s_cols)) * (s_rows // s_cols)
+    sb = (visible + s_rows * s_cols) * 2
+    sets = []
+    for _ in range(sets_for(2 * s_rows * s_cols * 2)):
+        x = torch.randn(s_rows, s_cols, generator=gen, device="cuda").to(torch.bfloat16)
+        sets.append((x, torch.empty_like(x)))
+    launches = [lambda s=s: cf._lib.check(lib.cf_softmax_scaled(
+        s[0].data_ptr(), cf._lib.CF_BF16, s[1].data_ptr(), cf._lib.CF_BF16, s_rows, s_cols,
+        1 / 128 ** 0.5, s_cols, torch.cuda.current_stream().cuda_stream)) for s in sets]
+    r = summary(time_launches(torch, launches, warmup, runs))
+    with_kernel_time(torch, cf, r, launches, nbytes=sb)
+    out["softmax_scaled_causal_bf16_131072x512"] = {**r, "bytes": sb, "GB/s": gbs(sb, r["median_ms"]),
+                                                     "frac_hbm": gbs(sb, r["median_ms"]) / PEAK_HBM_GBS}
+    del sets, launches
     # The row's neighbours in the same family: fused residual add +
     # RMSNorm at config 2's shape, and the activations over a Llama-7B MLP
     # activation ([16384, 11008]).

@@ -27,6 +27,7 @@ from cuda_force_amd.ops import (
     silu,
     softmax,
     softmax_as,
+    softmax_scaled,
     sum_reduce,
     swiglu,
 )
@@ -53,6 +54,7 @@ __all__ = [
     "silu",
     "softmax",
     "softmax_as",
+    "softmax_scaled",
     "sum_reduce",
     "swiglu",
 ]

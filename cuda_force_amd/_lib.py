@@ -76,6 +76,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_rmsnorm": (_I32, [_P, _P, _P, _I32, _I64, _I64, _F, _P]),
     "cf_fused_residual_rmsnorm": (_I32, [_P, _P, _P, _P, _P, _I32, _I64, _I64, _F, _P]),
     "cf_softmax": (_I32, [_P, _I32, _P, _I32, _I64, _I64, _P]),
+    "cf_softmax_scaled": (_I32, [_P, _I32, _P, _I32, _I64, _I64, _F, _I64, _P]),
     "cf_reduce_sum_workspace_bytes": (_SZ, [_I64]),
     "cf_reduce_sum": (_I32, [_P, _I32, _P, _I64, _P, _SZ, _I32, _P]),
     "cf_reduce_sum_noalloc": (_I32, [_P, _I32, _P, _I64, _I32, _P]),

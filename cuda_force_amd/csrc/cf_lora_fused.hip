@@ -142,6 +142,160 @@ struct XFrags {
     bf16x8_t a;
 };
 
+/// Epilogue of a 256 x 256 tile, shared by both K-loop schedules: the
+/// adapter up-projection (x @ a exchanged through LDS, then
+/// scale * b @ bf16(x @ a) on the MFMA units into the base accumulators),
+/// then the stores. acc[jb][i] of wave `wave` holds output rows
+/// wm*64 + 16 ((i + 2 wn) & 3) + lane%16, columns wn*128 + 16 jb + 4 (lane/16) .. +3;
+/// xacc[t] holds (x @ a) for row block 2 wn + t of the wave's 64 rows. Every
+/// wave must have finished reading operands from LDS (the first barrier
+/// below, or the one before the staged stores, orders the reuse of the
+/// operand area).
+template <bool kAdapter, bool kOutF32>
+__device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds, f32x4_t (&acc)[8][4],
+                                            const f32x4_t (&xacc)[2], int wave, int lane, int tn,
+                                            int64_t m0, int64_t n0) {
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    const int g = lane >> 4;
+    const int jl = lane & 15;
+    const int64_t M = args.M;
+    const int64_t N = args.N;
+    const int64_t rank = args.rank;
+    if (kAdapter) {
+        // x @ a: lane holds (x @ a)[row wm*64 + 16 (2 wn + t) + lane%16][4 g .. 4 g + 3].
+        uint2* xa_lds = reinterpret_cast<uint2*>(lds + kOffXa);
+        const bool write_xa = args.xa_out != nullptr && tn == 0;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int rb = wm * 4 + wn * 2 + t;
+            uint2 packed;
+            packed.x = f32_to_bf16_bits(xacc[t][0]) | (f32_to_bf16_bits(xacc[t][1]) << 16);
+            packed.y = f32_to_bf16_bits(xacc[t][2]) | (f32_to_bf16_bits(xacc[t][3]) << 16);
+            xa_lds[rb * 64 + lane] = packed;
+            const int64_t row = m0 + rb * 16 + jl;
+            if (write_xa && row < M) {
+                float* dst = args.xa_out + row * rank;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (4 * g + e < rank) dst[4 * g + e] = xacc[t][e];
+                }
+            }
+        }
+        __syncthreads();
+
+        // acc += scale * (b^T-block @ bf16(x @ a)^T-block), K = 16. scale * b
+        // is formed in fp32 and split into two bf16 parts, hi + lo, each
+        // multiplied by the bf16 x @ a on the MFMA units into the base
+        // accumulators: the adapter term carries about 2^-17 relative error
+        // for any scale (a single bf16(scale * b) would carry 2^-9 whenever
+        // the scale is not a power of two), and no extra registers are live.
+        // b is read transposed: lane j of group g reads b row 4g + j/4,
+        // columns 4(j%4) .. +3 of the block and receives column j's four
+        // adapter rows 4g .. 4g + 3.
+        const float scale = args.scale;
+        s16x4_t xa_frag[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xa_frag[i] =
+                __builtin_bit_cast(s16x4_t, xa_lds[(wm * 4 + ((i + 2 * wn) & 3)) * 64 + lane]);
+        }
+        const uint8_t* tb = lds + kOffB;
+        // Two passes (high parts, then low parts) keep one b fragment live.
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+#pragma unroll
+            for (int jb = 0; jb < 8; ++jb) {
+                const int row = 4 * g + (jl >> 2);
+                const int chunk = 2 * (wn * 8 + jb) + ((jl & 3) >> 1);
+                const s16x4_t raw = lds_read_tr(
+                    tb, row * (kBN * 2) + ((chunk ^ b_swizzle(row)) << 4) + (jl & 1) * 8);
+                s16x4_t bfrag;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v = scale * bf16_bits_to_f32(static_cast<uint16_t>(raw[e]));
+                    const uint32_t hi = f32_to_bf16_bits(v);
+                    bfrag[e] = static_cast<short>(
+                        part == 0 ? hi
+                                  : f32_to_bf16_bits(v - bf16_bits_to_f32(static_cast<uint16_t>(hi))));
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc[jb][i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bfrag, xa_frag[i],
+                                                                           acc[jb][i], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // Store: acc[jb][i] lane holds y[row wm*64 + 16 rb(i) + lane%16]
+    // [columns wn*128 + 16 jb + 4 g .. +3]; N is a multiple of 8, so a
+    // four- or eight-column group is entirely inside or outside the matrix.
+    if constexpr (!kOutF32) {
+        // bf16 output goes through LDS, so that each store instruction
+        // writes whole rows (16 lanes x 16 bytes = 256 contiguous bytes of a
+        // row, 4 rows per instruction) instead of 32-byte pieces of 16 rows.
+        // Each wave stages its own 64x128 sub-tile (16 KiB, rows of 256
+        // bytes) in the operand area, which every wave has left: the
+        // barrier after the x @ a exchange, or the one below, orders that.
+        // Chunk c (16 bytes) of row r sits at chunk c ^ (r & 15): the 8-byte
+        // writes of a half-wave (16 rows, one chunk each) and the 16-byte
+        // reads (whole rows) both spread over all banks.
+        if constexpr (!kAdapter) __syncthreads();
+        uint8_t* stage = lds + wave * (64 * 256);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 16 * ((i + 2 * wn) & 3) + jl;
+#pragma unroll
+            for (int jb = 0; jb < 8; ++jb) {
+                const int chunk = 2 * jb + (g >> 1);
+                uint2 packed;
+                packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
+                packed.y = f32_to_bf16_bits(acc[jb][i][2]) | (f32_to_bf16_bits(acc[jb][i][3]) << 16);
+                *reinterpret_cast<uint2*>(stage + row * 256 + ((chunk ^ (row & 15)) << 4) +
+                                          (g & 1) * 8) = packed;
+            }
+        }
+        // Only this wave reads what it wrote: LDS operations of a wave
+        // complete in order; the fence keeps the compiler from moving the
+        // reads above the writes.
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        const int c = lane & 15;
+        const int64_t col = n0 + wn * 128 + 8 * c;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int row = 4 * s + (lane >> 4);
+            const uint4 v =
+                *reinterpret_cast<const uint4*>(stage + row * 256 + ((c ^ (row & 15)) << 4));
+            const int64_t grow = m0 + wm * 64 + row;
+            if (grow < M && col < N) store_stream16(args.y + grow * N + col, v);
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t row = m0 + wm * 64 + 16 * ((i + 2 * wn) & 3) + jl;
+        if (row >= M) continue;
+        uint16_t* yrow = args.y + row * N;
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+            const int64_t col = n0 + wn * 128 + 16 * jb + 4 * g;
+            if (kOutF32 && col < N) {
+                // Split K: slice blockIdx.y of the K range writes its own
+                // partial product.
+                *reinterpret_cast<f32x4_t*>(args.y32 + static_cast<int64_t>(blockIdx.y) * M * N +
+                                            row * N + col) = acc[jb][i];
+            } else if (col < N) {
+                uint2 packed;
+                packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
+                packed.y = f32_to_bf16_bits(acc[jb][i][2]) | (f32_to_bf16_bits(acc[jb][i][3]) << 16);
+                *reinterpret_cast<uint2*>(yrow + col) = packed;
+            }
+        }
+    }
+}
+
 template <bool kAdapter, bool kOutF32>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lora_fused_bf16_kernel(FusedArgs args) {
@@ -416,139 +570,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         run(std::false_type{});
     }
 
-    // ---- epilogue ----
-    if (kAdapter) {
-        // x @ a: lane holds (x @ a)[row wm*64 + 16 (2 wn + t) + lane%16][4 g .. 4 g + 3].
-        uint2* xa_lds = reinterpret_cast<uint2*>(lds + kOffXa);
-        const bool write_xa = args.xa_out != nullptr && tn == 0;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int rb = wm * 4 + wn * 2 + t;
-            uint2 packed;
-            packed.x = f32_to_bf16_bits(xacc[t][0]) | (f32_to_bf16_bits(xacc[t][1]) << 16);
-            packed.y = f32_to_bf16_bits(xacc[t][2]) | (f32_to_bf16_bits(xacc[t][3]) << 16);
-            xa_lds[rb * 64 + lane] = packed;
-            const int64_t row = m0 + rb * 16 + jl;
-            if (write_xa && row < M) {
-                float* dst = args.xa_out + row * rank;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (4 * g + e < rank) dst[4 * g + e] = xacc[t][e];
-                }
-            }
-        }
-        __syncthreads();
-
-        // acc += scale * (b^T-block @ bf16(x @ a)^T-block), K = 16. scale * b
-        // is formed in fp32 and split into two bf16 parts, hi + lo, each
-        // multiplied by the bf16 x @ a on the MFMA units into the base
-        // accumulators: the adapter term carries about 2^-17 relative error
-        // for any scale (a single bf16(scale * b) would carry 2^-9 whenever
-        // the scale is not a power of two), and no extra registers are live.
-        // b is read transposed: lane j of group g reads b row 4g + j/4,
-        // columns 4(j%4) .. +3 of the block and receives column j's four
-        // adapter rows 4g .. 4g + 3.
-        const float scale = args.scale;
-        s16x4_t xa_frag[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            xa_frag[i] =
-                __builtin_bit_cast(s16x4_t, xa_lds[(wm * 4 + ((i + 2 * wn) & 3)) * 64 + lane]);
-        }
-        const uint8_t* tb = lds + kOffB;
-        // Two passes (high parts, then low parts) keep one b fragment live.
-#pragma unroll
-        for (int part = 0; part < 2; ++part) {
-#pragma unroll
-            for (int jb = 0; jb < 8; ++jb) {
-                const int row = 4 * g + (jl >> 2);
-                const int chunk = 2 * (wn * 8 + jb) + ((jl & 3) >> 1);
-                const s16x4_t raw = lds_read_tr(
-                    tb, row * (kBN * 2) + ((chunk ^ b_swizzle(row)) << 4) + (jl & 1) * 8);
-                s16x4_t bfrag;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float v = scale * bf16_bits_to_f32(static_cast<uint16_t>(raw[e]));
-                    const uint32_t hi = f32_to_bf16_bits(v);
-                    bfrag[e] = static_cast<short>(
-                        part == 0 ? hi
-                                  : f32_to_bf16_bits(v - bf16_bits_to_f32(static_cast<uint16_t>(hi))));
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    acc[jb][i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bfrag, xa_frag[i],
-                                                                           acc[jb][i], 0, 0, 0);
-                }
-            }
-        }
-    }
-
-    // Store: acc[jb][i] lane holds y[row wm*64 + 16 rb(i) + lane%16]
-    // [columns wn*128 + 16 jb + 4 g .. +3]; N is a multiple of 8, so a
-    // four- or eight-column group is entirely inside or outside the matrix.
-    if constexpr (!kOutF32) {
-        // bf16 output goes through LDS, so that each store instruction
-        // writes whole rows (16 lanes x 16 bytes = 256 contiguous bytes of a
-        // row, 4 rows per instruction) instead of 32-byte pieces of 16 rows.
-        // Each wave stages its own 64x128 sub-tile (16 KiB, rows of 256
-        // bytes) in the operand area, which every wave has left: the
-        // barrier after the x @ a exchange, or the one below, orders that.
-        // Chunk c (16 bytes) of row r sits at chunk c ^ (r & 15): the 8-byte
-        // writes of a half-wave (16 rows, one chunk each) and the 16-byte
-        // reads (whole rows) both spread over all banks.
-        if constexpr (!kAdapter) __syncthreads();
-        uint8_t* stage = lds + wave * (64 * 256);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 16 * ((i + 2 * wn) & 3) + jl;
-#pragma unroll
-            for (int jb = 0; jb < 8; ++jb) {
-                const int chunk = 2 * jb + (g >> 1);
-                uint2 packed;
-                packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
-                packed.y = f32_to_bf16_bits(acc[jb][i][2]) | (f32_to_bf16_bits(acc[jb][i][3]) << 16);
-                *reinterpret_cast<uint2*>(stage + row * 256 + ((chunk ^ (row & 15)) << 4) +
-                                          (g & 1) * 8) = packed;
-            }
-        }
-        // Only this wave reads what it wrote: LDS operations of a wave
-        // complete in order; the fence keeps the compiler from moving the
-        // reads above the writes.
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        const int c = lane & 15;
-        const int64_t col = n0 + wn * 128 + 8 * c;
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const int row = 4 * s + (lane >> 4);
-            const uint4 v =
-                *reinterpret_cast<const uint4*>(stage + row * 256 + ((c ^ (row & 15)) << 4));
-            const int64_t grow = m0 + wm * 64 + row;
-            if (grow < M && col < N) store_stream16(args.y + grow * N + col, v);
-        }
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int64_t row = m0 + wm * 64 + 16 * ((i + 2 * wn) & 3) + jl;
-        if (row >= M) continue;
-        uint16_t* yrow = args.y + row * N;
-#pragma unroll
-        for (int jb = 0; jb < 8; ++jb) {
-            const int64_t col = n0 + wn * 128 + 16 * jb + 4 * g;
-            if (kOutF32 && col < N) {
-                // Split K: slice blockIdx.y of the K range writes its own
-                // partial product.
-                *reinterpret_cast<f32x4_t*>(args.y32 + static_cast<int64_t>(blockIdx.y) * M * N +
-                                            row * N + col) = acc[jb][i];
-            } else if (col < N) {
-                uint2 packed;
-                packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
-                packed.y = f32_to_bf16_bits(acc[jb][i][2]) | (f32_to_bf16_bits(acc[jb][i][3]) << 16);
-                *reinterpret_cast<uint2*>(yrow + col) = packed;
-            }
-        }
-    }
+    finish_tile<kAdapter, kOutF32>(args, lds, acc, xacc, wave, lane, tn, m0, n0);
 }
 
 }  // namespace

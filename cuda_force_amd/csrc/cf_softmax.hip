@@ -20,6 +20,14 @@
 //
 // Fallback: long rows, unaligned pointers or ragged widths use a workgroup per
 // row with three passes over the row (max, sum, normalise).
+//
+// cf_softmax_scaled is the same kernel on scale * x with an optional causal
+// mask (column c of row r hidden when c > r mod period): the attention-score
+// softmax of a causal block, softmax(scores / sqrt(d) + causal), in one pass
+// instead of a scale-and-mask pass followed by a softmax. A 16-byte vector
+// of a row that lies wholly past the row's last visible column is not read
+// at all (buffer load with an out-of-range offset: zeros, no memory access),
+// so a causal score matrix is read about half, and written whole.
 #include "cf_common.hpp"
 
 namespace cf {
@@ -46,25 +54,58 @@ __device__ __forceinline__ void store_vec(Tout* p, const float* v) {
     }
 }
 
+/// Scale and causal mask of cf_softmax_scaled (kMasked kernels only):
+/// logits are scale * x, and column c of row r is -inf when period > 0 and
+/// c > r mod period.
+struct Masking {
+    float scale;
+    int64_t period;
+};
+
+/// Last visible column of `row` (cols - 1 when there is no mask).
+__device__ __forceinline__ int64_t last_visible(const Masking& m, int64_t row, int64_t cols) {
+    return m.period > 0 ? row % m.period : cols - 1;
+}
+
+/// The same for the wave kernel, whose x spans fewer than 2^31 bytes (so
+/// row, period and cols fit in 32 bits): a 32-bit remainder.
+__device__ __forceinline__ int last_visible32(const Masking& m, int64_t row, int64_t cols) {
+    return m.period > 0 ? static_cast<int>(static_cast<uint32_t>(row) % static_cast<uint32_t>(m.period))
+                        : static_cast<int>(cols) - 1;
+}
+
+/// 16-byte streaming load through a buffer resource: an offset past the
+/// resource's range returns zeros without touching memory.
+__device__ __forceinline__ uint4 buffer_load_stream16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, 0, 2 /* nt */);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 /// One wave per kRows consecutive rows, one-shot grid; all of the wave's
 /// loads are issued before the first reduction. No load depends on a
 /// condition (which would make the compiler wait for each one before the
 /// next): rows past the end are loaded from the last row and not stored,
 /// and with kFullCols every lane's vectors are inside the row; otherwise
 /// the missing columns are replaced by -inf after the load.
-template <typename Tin, typename Tout, int kVecs, int kRows, bool kFullCols>
+template <typename Tin, typename Tout, int kVecs, int kRows, bool kFullCols, bool kMasked>
 __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const Tin* x, Tout* y,
                                                                          int64_t rows,
-                                                                         int64_t cols) {
+                                                                         int64_t cols,
+                                                                         Masking mask) {
     constexpr int kPer = Storage<Tin>::kPerVec;
     const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
     const int64_t vec_cols = cols / kPer;
+    // Wave-uniform (readfirstlane tells the compiler): the row index and
+    // the mask's remainder are computed once per wave.
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
-                         static_cast<int64_t>(threadIdx.x) / kWaveSize;
+                         __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWaveSize);
     const int64_t row0 = wave * kRows;
     if (row0 >= rows) return;  // wave-uniform
     const float neg_inf = -__builtin_inff();
 
+    // kMasked: x spans fewer than 2^31 bytes (checked on the host).
+    const __amdgpu_buffer_rsrc_t xbuf =
+        make_buffer(x, kMasked ? static_cast<uint32_t>(rows * cols * sizeof(Tin)) : 0u);
     uint4 raw[kRows][kVecs];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
@@ -73,7 +114,14 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
         for (int j = 0; j < kVecs; ++j) {
             const int64_t idx = static_cast<int64_t>(j) * kWaveSize + lane;
             const int64_t ic = kFullCols || idx < vec_cols ? idx : vec_cols - 1;
-            raw[r][j] = load_stream16(x + row * cols + ic * kPer);
+            if constexpr (kMasked) {
+                const bool read = static_cast<int>(ic) * kPer <= last_visible32(mask, row, cols);
+                raw[r][j] = buffer_load_stream16(
+                    xbuf, read ? static_cast<uint32_t>((row * cols + ic * kPer) * sizeof(Tin))
+                               : 0x80000000u);
+            } else {
+                raw[r][j] = load_stream16(x + row * cols + ic * kPer);
+            }
         }
     }
     // Keep all of the wave's loads ahead of the first reduction.
@@ -84,11 +132,19 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
         const int64_t row = row0 + r;
         if (row >= rows) continue;  // wave-uniform
         float v[kVecs][kPer];
+        const int visible = kMasked ? last_visible32(mask, row, cols) : 0;
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             const int64_t idx = static_cast<int64_t>(j) * kWaveSize + lane;
             if (kFullCols || idx < vec_cols) {
                 unpack16<Tin>(raw[r][j], v[j]);
+                if constexpr (kMasked) {
+                    const int first = static_cast<int>(idx) * kPer;
+#pragma unroll
+                    for (int i = 0; i < kPer; ++i) {
+                        v[j][i] = first + i <= visible ? mask.scale * v[j][i] : neg_inf;
+                    }
+                }
             } else {
 #pragma unroll
                 for (int i = 0; i < kPer; ++i) v[j][i] = neg_inf;
@@ -128,36 +184,44 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
 }
 
 /// Any shape: one workgroup per row, three passes.
-template <typename Tin, typename Tout>
+template <typename Tin, typename Tout, bool kMasked>
 __global__ __launch_bounds__(kDefaultBlockSize) void softmax_block_kernel(const Tin* x, Tout* y,
                                                                           int64_t rows,
-                                                                          int64_t cols) {
+                                                                          int64_t cols,
+                                                                          Masking mask) {
     __shared__ float slot[kWavesPerBlock];
     const float neg_inf = -__builtin_inff();
     for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
         const Tin* xr = x + row * cols;
+        // Columns past `visible` are -inf (never read); the rest are scaled.
+        const int64_t visible = kMasked ? last_visible(mask, row, cols) : cols - 1;
+        auto logit = [&](int64_t c) {
+            return kMasked ? (c <= visible ? mask.scale * Storage<Tin>::load(xr + c) : neg_inf)
+                           : Storage<Tin>::load(xr + c);
+        };
         float local_max = neg_inf;
         for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-            local_max = fmaxf(local_max, Storage<Tin>::load(xr + c));
+            local_max = fmaxf(local_max, logit(c));
         }
         const float row_max = block_reduce_f32<kWavesPerBlock, MaxF32>(local_max, slot);
         float local_sum = 0.0f;
         for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-            local_sum += __expf(Storage<Tin>::load(xr + c) - row_max);
+            local_sum += __expf(logit(c) - row_max);
         }
         const float inv_sum = 1.0f / block_reduce_f32<kWavesPerBlock, AddF32>(local_sum, slot);
         // When x and y alias, every thread must finish reading before any
         // writes: the reductions above end in a barrier, and this pass reads
         // and writes the same element in the same thread.
         for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-            const float e = __expf(Storage<Tin>::load(xr + c) - row_max);
+            const float e = __expf(logit(c) - row_max);
             Storage<Tout>::store(y + row * cols + c, e * inv_sum);
         }
     }
 }
 
-template <typename Tin, typename Tout, int kVecs>
-void launch_wave(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t stream) {
+template <typename Tin, typename Tout, int kVecs, bool kMasked>
+void launch_wave(const void* x, void* y, int64_t rows, int64_t cols, const Masking& mask,
+                 hipStream_t stream) {
     // Rows per wave: two for rows of one 16-byte vector per lane, else one.
     // More loads in flight per lane are slower, not faster: on [131072, 512]
     // bf16 eight rows per wave (eight 16-byte loads per lane before the
@@ -175,63 +239,80 @@ void launch_wave(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t
     const unsigned g = static_cast<unsigned>(grid);
     if (grid_rows == 1) {
         if (full) {
-            launch(softmax_wave_kernel<Tin, Tout, kVecs, 1, true>, dim3(g), dim3(kDefaultBlockSize),
-                   0, stream, xin, out, rows, cols);
+            launch(softmax_wave_kernel<Tin, Tout, kVecs, 1, true, kMasked>, dim3(g), dim3(kDefaultBlockSize),
+                   0, stream, xin, out, rows, cols, mask);
         } else {
-            launch(softmax_wave_kernel<Tin, Tout, kVecs, 1, false>, dim3(g),
-                   dim3(kDefaultBlockSize), 0, stream, xin, out, rows, cols);
+            launch(softmax_wave_kernel<Tin, Tout, kVecs, 1, false, kMasked>, dim3(g),
+                   dim3(kDefaultBlockSize), 0, stream, xin, out, rows, cols, mask);
         }
         return;
     }
     if (full) {
-        launch(softmax_wave_kernel<Tin, Tout, kVecs, kRows, true>, dim3(g), dim3(kDefaultBlockSize),
-               0, stream, xin, out, rows, cols);
+        launch(softmax_wave_kernel<Tin, Tout, kVecs, kRows, true, kMasked>, dim3(g), dim3(kDefaultBlockSize),
+               0, stream, xin, out, rows, cols, mask);
     } else {
-        launch(softmax_wave_kernel<Tin, Tout, kVecs, kRows, false>, dim3(g),
-               dim3(kDefaultBlockSize), 0, stream, xin, out, rows, cols);
+        launch(softmax_wave_kernel<Tin, Tout, kVecs, kRows, false, kMasked>, dim3(g),
+               dim3(kDefaultBlockSize), 0, stream, xin, out, rows, cols, mask);
     }
 }
 
-template <typename Tin, typename Tout>
-cf_status dispatch(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t stream) {
+template <typename Tin, typename Tout, bool kMasked>
+cf_status dispatch(const void* x, void* y, int64_t rows, int64_t cols, const Masking& mask,
+                   hipStream_t stream) {
     constexpr int kPer = Storage<Tin>::kPerVec;
-    const bool vec = cols % kPer == 0 && host_aligned(x, 16) && host_aligned(y, 16);
+    // The masked wave kernel addresses x through a buffer resource with
+    // 32-bit offsets and 0x80000000 as its "skip" offset.
+    const bool offsets_fit = !kMasked || rows * cols * static_cast<int64_t>(sizeof(Tin)) < (1LL << 31);
+    const bool vec = cols % kPer == 0 && host_aligned(x, 16) && host_aligned(y, 16) && offsets_fit;
     const int64_t vectors_per_lane = ceil_div<int64_t>(cols / kPer, kWaveSize);
     if (vec && vectors_per_lane <= 16) {
         if (vectors_per_lane <= 1) {
-            launch_wave<Tin, Tout, 1>(x, y, rows, cols, stream);
+            launch_wave<Tin, Tout, 1, kMasked>(x, y, rows, cols, mask, stream);
         } else if (vectors_per_lane <= 2) {
-            launch_wave<Tin, Tout, 2>(x, y, rows, cols, stream);
+            launch_wave<Tin, Tout, 2, kMasked>(x, y, rows, cols, mask, stream);
         } else if (vectors_per_lane <= 4) {
-            launch_wave<Tin, Tout, 4>(x, y, rows, cols, stream);
+            launch_wave<Tin, Tout, 4, kMasked>(x, y, rows, cols, mask, stream);
         } else if (vectors_per_lane <= 8) {
-            launch_wave<Tin, Tout, 8>(x, y, rows, cols, stream);
+            launch_wave<Tin, Tout, 8, kMasked>(x, y, rows, cols, mask, stream);
         } else {
-            launch_wave<Tin, Tout, 16>(x, y, rows, cols, stream);
+            launch_wave<Tin, Tout, 16, kMasked>(x, y, rows, cols, mask, stream);
         }
     } else {
         const int64_t max_blocks = static_cast<int64_t>(cu_count()) * 8;
         const int64_t grid = rows < max_blocks ? rows : max_blocks;
-        launch(softmax_block_kernel<Tin, Tout>, dim3(static_cast<unsigned>(grid)),
+        launch(softmax_block_kernel<Tin, Tout, kMasked>, dim3(static_cast<unsigned>(grid)),
                dim3(kDefaultBlockSize), 0, stream, static_cast<const Tin*>(x),
-               static_cast<Tout*>(y), rows, cols);
+               static_cast<Tout*>(y), rows, cols, mask);
     }
     return check_launch("launching softmax", stream);
 }
 
-template <typename Tin>
+template <typename Tin, bool kMasked>
 cf_status dispatch_out(const void* x, void* y, cf_dtype y_dtype, int64_t rows, int64_t cols,
-                       hipStream_t stream) {
+                       const Masking& mask, hipStream_t stream) {
     switch (y_dtype) {
         case CF_F32:
-            return dispatch<Tin, float>(x, y, rows, cols, stream);
+            return dispatch<Tin, float, kMasked>(x, y, rows, cols, mask, stream);
         case CF_BF16:
-            return dispatch<Tin, bf16_t>(x, y, rows, cols, stream);
+            return dispatch<Tin, bf16_t, kMasked>(x, y, rows, cols, mask, stream);
         case CF_F16:
-            return dispatch<Tin, f16_t>(x, y, rows, cols, stream);
+            return dispatch<Tin, f16_t, kMasked>(x, y, rows, cols, mask, stream);
     }
-    return fail(CF_ERR_UNSUPPORTED, "cf_softmax: unknown output dtype %d",
-                static_cast<int>(y_dtype));
+    return fail(CF_ERR_UNSUPPORTED, "softmax: unknown output dtype %d", static_cast<int>(y_dtype));
+}
+
+template <bool kMasked>
+cf_status dispatch_in(const void* x, cf_dtype x_dtype, void* y, cf_dtype y_dtype, int64_t rows,
+                      int64_t cols, const Masking& mask, hipStream_t stream) {
+    switch (x_dtype) {
+        case CF_F32:
+            return dispatch_out<float, kMasked>(x, y, y_dtype, rows, cols, mask, stream);
+        case CF_BF16:
+            return dispatch_out<bf16_t, kMasked>(x, y, y_dtype, rows, cols, mask, stream);
+        case CF_F16:
+            return dispatch_out<f16_t, kMasked>(x, y, y_dtype, rows, cols, mask, stream);
+    }
+    return fail(CF_ERR_UNSUPPORTED, "softmax: unknown input dtype %d", static_cast<int>(x_dtype));
 }
 
 }  // namespace
@@ -246,17 +327,22 @@ cf_status cf_softmax(const void* x, cf_dtype x_dtype, void* y, cf_dtype y_dtype,
     CF_REQUIRE(x != nullptr && y != nullptr, "cf_softmax: null pointer");
     CF_REQUIRE(x != y || x_dtype == y_dtype,
                "cf_softmax: input and output may alias only when their dtypes match");
-    auto s = static_cast<hipStream_t>(stream);
-    switch (x_dtype) {
-        case CF_F32:
-            return cf::dispatch_out<float>(x, y, y_dtype, rows, cols, s);
-        case CF_BF16:
-            return cf::dispatch_out<cf::bf16_t>(x, y, y_dtype, rows, cols, s);
-        case CF_F16:
-            return cf::dispatch_out<cf::f16_t>(x, y, y_dtype, rows, cols, s);
-    }
-    return cf::fail(CF_ERR_UNSUPPORTED, "cf_softmax: unknown input dtype %d",
-                    static_cast<int>(x_dtype));
+    return cf::dispatch_in<false>(x, x_dtype, y, y_dtype, rows, cols, cf::Masking{1.0f, 0},
+                                  static_cast<hipStream_t>(stream));
+}
+
+cf_status cf_softmax_scaled(const void* x, cf_dtype x_dtype, void* y, cf_dtype y_dtype,
+                            int64_t rows, int64_t cols, float scale, int64_t causal_period,
+                            void* stream) {
+    CF_ENTRY();
+    if (rows <= 0 || cols <= 0) return CF_OK;
+    CF_REQUIRE(x != nullptr && y != nullptr, "cf_softmax_scaled: null pointer");
+    CF_REQUIRE(x != y || x_dtype == y_dtype,
+               "cf_softmax_scaled: input and output may alias only when their dtypes match");
+    CF_REQUIRE(causal_period >= 0, "cf_softmax_scaled: negative causal period %lld",
+               static_cast<long long>(causal_period));
+    return cf::dispatch_in<true>(x, x_dtype, y, y_dtype, rows, cols,
+                                 cf::Masking{scale, causal_period}, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

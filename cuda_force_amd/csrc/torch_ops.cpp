@@ -13,12 +13,14 @@
 //     reference's accept float32 only (bindings.cpp:45-48); lora_linear takes
 //     float32 and bfloat16;
 //   * a few extra operators the Python layer uses: dequantize_int8_to (half
-//     outputs), quantize_dequantize, softmax_as (output dtype), row_sum, and
+//     outputs), quantize_dequantize, softmax_as (output dtype),
+//     softmax_scaled (scaled, causally masked attention scores), row_sum, and
 //     lora_linear_fwd / lora_linear_bwd for the adapter autograd path.
 #include <c10/hip/HIPStream.h>
 #include <torch/csrc/autograd/autograd_not_implemented_fallback.h>
 #include <torch/extension.h>
 
+#include <limits>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -113,6 +115,19 @@ torch::Tensor softmax_as_hip(const torch::Tensor& input, torch::ScalarType out_d
 
 torch::Tensor softmax_hip(const torch::Tensor& input) {
     return softmax_as_hip(input, input.scalar_type());
+}
+
+torch::Tensor softmax_scaled_hip(const torch::Tensor& input, double scale, int64_t causal_period,
+                                 torch::ScalarType out_dtype) {
+    check_2d(input, "input");
+    check_contiguous(input, "input");
+    TORCH_CHECK(causal_period >= 0, "causal_period must be >= 0, got ", causal_period);
+    const at::DeviceGuard guard(input.device());
+    torch::Tensor output = torch::empty(input.sizes(), input.options().dtype(out_dtype));
+    check_status(cf_softmax_scaled(input.data_ptr(), to_cf(input, "input"), output.data_ptr(),
+                                   to_cf(out_dtype), input.size(0), input.size(1),
+                                   static_cast<float>(scale), causal_period, stream_for(input)));
+    return output;
 }
 
 std::tuple<torch::Tensor, torch::Tensor> lora_linear_fwd_hip(const torch::Tensor& x,
@@ -352,6 +367,21 @@ torch::Tensor softmax_as_cpu(const torch::Tensor& input, torch::ScalarType out_d
     return torch::softmax(input.to(torch::kFloat32), /*dim=*/-1).to(out_dtype);
 }
 
+torch::Tensor softmax_scaled_cpu(const torch::Tensor& input, double scale, int64_t causal_period,
+                                 torch::ScalarType out_dtype) {
+    check_2d(input, "input");
+    TORCH_CHECK(causal_period >= 0, "causal_period must be >= 0, got ", causal_period);
+    torch::Tensor logits = input.to(torch::kFloat32) * scale;
+    if (causal_period > 0) {
+        const auto options = torch::TensorOptions().dtype(torch::kLong).device(input.device());
+        const torch::Tensor cols = torch::arange(input.size(1), options).unsqueeze(0);
+        const torch::Tensor rows =
+            torch::remainder(torch::arange(input.size(0), options), causal_period).unsqueeze(1);
+        logits = logits.masked_fill(cols > rows, -std::numeric_limits<float>::infinity());
+    }
+    return torch::softmax(logits, /*dim=*/-1).to(out_dtype);
+}
+
 torch::Tensor lora_linear_cpu(const torch::Tensor& x, const torch::Tensor& w,
                               const torch::Tensor& a, const torch::Tensor& b, double scale) {
     return torch::matmul(x, w) + scale * torch::matmul(torch::matmul(x, a), b);
@@ -473,6 +503,7 @@ TORCH_LIBRARY(cudaforge, m) {
     m.def("dequantize_int8_to(Tensor quantised, Tensor scales, ScalarType dtype) -> Tensor");
     m.def("quantize_dequantize(Tensor input) -> Tensor");
     m.def("softmax_as(Tensor input, ScalarType dtype) -> Tensor");
+    m.def("softmax_scaled(Tensor input, float scale, int causal_period, ScalarType dtype) -> Tensor");
     m.def("row_sum(Tensor input) -> Tensor");
     m.def(
         "lora_linear_fwd(Tensor x, Tensor w, Tensor a, Tensor b, float scale) "
@@ -489,8 +520,8 @@ TORCH_LIBRARY(cudaforge, m) {
 TORCH_LIBRARY_IMPL(cudaforge, Autograd, m) {
     for (const char* name :
          {"rmsnorm", "softmax", "lora_linear", "sum", "silu", "gelu", "swiglu", "quantize_int8",
-          "dequantize_int8", "dequantize_int8_to", "quantize_dequantize", "softmax_as", "row_sum",
-          "lora_linear_fwd", "lora_linear_bwd"}) {
+          "dequantize_int8", "dequantize_int8_to", "quantize_dequantize", "softmax_as",
+          "softmax_scaled", "row_sum", "lora_linear_fwd", "lora_linear_bwd"}) {
         m.impl(name, torch::autograd::autogradNotImplementedFallback());
     }
 }
@@ -510,6 +541,7 @@ TORCH_LIBRARY_IMPL(cudaforge, CPU, m) {
     m.impl("dequantize_int8_to", &dequantize_int8_to_cpu);
     m.impl("quantize_dequantize", &quantize_dequantize_cpu);
     m.impl("softmax_as", &softmax_as_cpu);
+    m.impl("softmax_scaled", &softmax_scaled_cpu);
     m.impl("row_sum", &row_sum_cpu);
     m.impl("lora_linear_fwd", &lora_linear_fwd_cpu);
     m.impl("lora_linear_bwd", &lora_linear_bwd_cpu);
@@ -530,6 +562,7 @@ TORCH_LIBRARY_IMPL(cudaforge, CUDA, m) {
     m.impl("dequantize_int8_to", &dequantize_int8_to_hip);
     m.impl("quantize_dequantize", &quantize_dequantize_hip);
     m.impl("softmax_as", &softmax_as_hip);
+    m.impl("softmax_scaled", &softmax_scaled_hip);
     m.impl("row_sum", &row_sum_hip);
     m.impl("lora_linear_fwd", &lora_linear_fwd_hip);
     m.impl("lora_linear_bwd", &lora_linear_bwd_hip);

@@ -260,6 +260,45 @@ def softmax_as(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return torch.softmax(x.float(), dim=-1).to(dtype)
 
 
+def _softmax_scaled_reference(x: torch.Tensor, scale: float, causal_period: int) -> torch.Tensor:
+    rows = x.reshape(-1, x.shape[-1]).float() * scale
+    if causal_period > 0:
+        cols = torch.arange(rows.shape[1], device=x.device)[None, :]
+        limit = (torch.arange(rows.shape[0], device=x.device) % causal_period)[:, None]
+        rows = rows.masked_fill(cols > limit, float("-inf"))
+    return torch.softmax(rows, dim=-1).view(x.shape)
+
+
+def softmax_scaled(
+    x: torch.Tensor, scale: float, causal_period: int = 0, dtype: torch.dtype | None = None
+) -> torch.Tensor:
+    """Softmax over the last dim of ``scale * x`` with an optional causal mask.
+
+    Row ``r`` of the flattened ``[-1, cols]`` view keeps columns
+    ``0 .. r % causal_period`` and gives the rest probability 0 (no mask when
+    ``causal_period`` is 0). For attention scores ``[batch, heads, seq, seq]``,
+    ``softmax_scaled(q @ k^T, 1 / sqrt(d), seq)`` is the causal softmax that
+    examples/transformer_block.py:57-59 composes from ``scores / sqrt(d) +
+    causal`` and ``softmax``, in one pass that does not read the masked
+    scores. Result in ``dtype`` (default: the input's); fp32 arithmetic. Not
+    in the reference's API."""
+    dtype = x.dtype if dtype is None else dtype
+    if causal_period < 0:
+        raise ValueError(f"causal_period must be >= 0, got {causal_period}")
+    if x.numel() == 0:
+        return x.to(dtype).clone()
+    x = x.contiguous()
+    if (
+        _dispatch_available("softmax_scaled", x)
+        and x.dtype in KERNEL_DTYPES
+        and dtype in KERNEL_DTYPES
+    ):
+        rows = x.reshape(-1, x.shape[-1])
+        return torch.ops.cudaforge.softmax_scaled(rows, float(scale), int(causal_period), dtype).view(x.shape)
+    _refuse_gpu_fallback("softmax_scaled", x)
+    return _softmax_scaled_reference(x, scale, causal_period).to(dtype)
+
+
 def lora_linear(
     x: torch.Tensor,
     weight: torch.Tensor,

@@ -8,8 +8,9 @@ composition for the MI355X build, at the configuration the benchmark names:
 every projection is a LoRA-adapted linear (rank 16, alpha 32) through the fused
 bf16 MFMA kernel, so one block runs
 
-    fused_residual_rmsnorm -> lora_linear Q, K, V -> scores = Q K^T / sqrt(d)
-    + causal mask -> softmax -> P V -> lora_linear O -> fused_residual_rmsnorm
+    fused_residual_rmsnorm -> lora_linear Q, K, V -> scores = Q K^T ->
+    softmax(scores / sqrt(d) + causal mask) in one kernel -> P V ->
+    lora_linear O -> fused_residual_rmsnorm
     -> lora_linear gate, up -> swiglu -> lora_linear down
 
 The two batched attention products go through torch.matmul (hipBLASLt), as in
@@ -107,11 +108,12 @@ class LlamaBlock:
         # out [batch, heads, head_dim, seq] by one copy, so no transposed view
         # reaches the bf16 batched GEMM.
         kt = k.view(batch, seq, c.heads, c.head_dim).permute(0, 2, 3, 1).contiguous()
-        causal = torch.triu(torch.full((seq, seq), float("-inf"), device=normed.device), 1)
-        # causal + scores / sqrt(d) in one pass over the score matrix.
-        scores = torch.add(causal.to(q.dtype), torch.matmul(qh, kt), alpha=1.0 / math.sqrt(c.head_dim))
+        scores = torch.matmul(qh, kt)
         mark("scores_matmul")
-        weights = ops.softmax(scores.view(-1, seq)).view_as(scores)
+        # softmax(scores / sqrt(d) + causal) in one pass: row r of each
+        # head's [seq, seq] block keeps columns 0 .. r; the masked scores
+        # are never read.
+        weights = ops.softmax_scaled(scores.view(-1, seq), 1.0 / math.sqrt(c.head_dim), seq).view_as(scores)
         mark("softmax")
         attended = torch.matmul(weights, vh).transpose(1, 2).reshape(batch * seq, c.hidden)
         mark("pv_matmul")

@@ -169,6 +169,17 @@ cf_status cf_fused_residual_rmsnorm(const void* x, const void* residual, const v
 cf_status cf_softmax(const void* x, cf_dtype x_dtype, void* y, cf_dtype y_dtype, int64_t rows,
                      int64_t cols, void* stream);
 
+/* Row softmax of scale * x with an optional causal mask: column c of row r is
+ * -inf (probability 0) when causal_period > 0 and c > r mod causal_period;
+ * causal_period 0 masks nothing. fp32 arithmetic as cf_softmax; masked
+ * 16-byte vectors of x are not read. This is the attention-score softmax of
+ * examples/transformer_block.py:57-59 (softmax(scores / sqrt(d) + causal))
+ * in one pass: the reference composes it from a scale-and-mask pass and
+ * launch_softmax (cuda/include/cudaforge/softmax.cuh:43-65). */
+cf_status cf_softmax_scaled(const void* x, cf_dtype x_dtype, void* y, cf_dtype y_dtype,
+                            int64_t rows, int64_t cols, float scale, int64_t causal_period,
+                            void* stream);
+
 /* ---- reductions --------------------------------------------------------- */
 
 /* Bytes of workspace cf_reduce_sum needs for `count` elements (the stage-1

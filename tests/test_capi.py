@@ -60,6 +60,10 @@ def test_empty_inputs_return_ok_without_touching_the_device(lib):
     assert lib.cf_dequantize_int8(null, null, null, _lib.CF_F32, -1, null) == _lib.CF_OK
     assert lib.cf_rmsnorm(null, null, null, _lib.CF_BF16, 0, 4096, 1e-6, null) == _lib.CF_OK
     assert lib.cf_softmax(null, _lib.CF_F32, null, _lib.CF_F32, 5, 0, null) == _lib.CF_OK
+    assert lib.cf_softmax_scaled(null, _lib.CF_BF16, null, _lib.CF_BF16, 0, 512, 0.5, 512, null) == _lib.CF_OK
+    fake = ctypes.c_void_p(0x1000)  # rejected before any launch
+    assert lib.cf_softmax_scaled(fake, _lib.CF_BF16, fake, _lib.CF_BF16, 4, 4, 0.5, -1, null) == \
+        _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_lora_linear(null, null, null, null, null, null, _lib.CF_BF16, 0, 8, 8, 2, 1.0, null) == _lib.CF_OK
 
 

@@ -293,6 +293,69 @@ def test_config2_softmax_full_size():
     np.testing.assert_allclose(g.host_values(y, "bf16").astype(np.float64).sum(axis=1), 1.0, atol=2e-2)
 
 
+def run_softmax_scaled(x: np.ndarray, in_dtype: str, out_dtype: str, scale: float, period: int,
+                       offset: int = 0, in_place: bool = False) -> np.ndarray:
+    rows, cols = x.shape
+    flat = np.concatenate([np.zeros(offset, x.dtype), x.reshape(-1)])
+    xg = g.to_gpu(flat, in_dtype)
+    yg = xg if in_place else g.empty(flat.size, g.torch_dtype(out_dtype))
+    g.call("cf_softmax_scaled", xg.data_ptr() + offset * xg.element_size(), g.cf(in_dtype),
+           yg.data_ptr() + offset * yg.element_size(), g.cf(out_dtype), rows, cols, scale, period, g.stream())
+    torch.cuda.synchronize()
+    return g.to_host(yg)[offset:].reshape(rows, cols)
+
+
+def masked_logits(values: np.ndarray, scale: float, period: int) -> np.ndarray:
+    """scale * x in float64 with the causal -inf mask of cf_softmax_scaled."""
+    z = scale * values.astype(np.float64)
+    if period > 0:
+        col = np.arange(z.shape[1])[None, :]
+        z = np.where(col > (np.arange(z.shape[0]) % period)[:, None], -np.inf, z)
+    return z
+
+
+@pytest.mark.parametrize(
+    "dtype,shape,period",
+    [("bf16", (1024, 2048), 2048), ("bf16", (4099, 512), 512), ("f32", (4097, 256), 256), ("f16", (640, 1024), 512),
+     ("bf16", (2048, 512), 0), ("f32", (3, 1025), 7), ("bf16", (5, 40000), 3), ("f32", (96, 4096), 96)],
+    ids=str,
+)
+def test_softmax_scaled_causal_matches_the_oracle(dtype, shape, period):
+    """softmax(scale * x) with column c of row r masked when c > r mod period
+    (period 0: no mask), against the float64 oracle on the same stored
+    logits; masked outputs are exactly 0 and whatever the masked inputs hold
+    (NaN here) never reaches a result."""
+    rows, cols = shape
+    g.announce(f"softmax_scaled {dtype} {shape} period {period}")
+    scale = 1 / math.sqrt(128)
+    x = g.storage_bits((rng(rows + cols + period).standard_normal(shape) * 8).astype(np.float32), dtype)
+    xv = g.host_values(x, dtype)
+    z = masked_logits(xv, scale, period)
+    poisoned = x.copy()
+    nan_bits = {"bf16": 0x7FC0, "f16": 0x7E00}
+    if dtype == "f32":
+        poisoned[np.isinf(z)] = np.nan
+    else:
+        poisoned[np.isinf(z)] = nan_bits[dtype]
+    y = run_softmax_scaled(poisoned, dtype, dtype, scale, period)
+    exact = oracle.softmax(z)
+    assert_close(y, exact, dtype, f"softmax_scaled {dtype} {shape} period {period}")
+    assert (g.host_values(y, dtype)[np.isinf(z)] == 0).all()
+    # fp32 probabilities from 16-bit logits, and the same kernel in place.
+    if dtype != "f32":
+        assert_close(run_softmax_scaled(x, dtype, "f32", scale, period), exact, "f32", "fp32 out")
+    assert_close(run_softmax_scaled(x, dtype, dtype, scale, period, in_place=True), exact, dtype, "in place")
+
+
+def test_softmax_scaled_misaligned_and_scale_only():
+    x = (rng(21).standard_normal((37, 512)) * 3).astype(np.float32)
+    exact = oracle.softmax(masked_logits(x, 0.25, 512))
+    assert_close(run_softmax_scaled(x, "f32", "f32", 0.25, 512, offset=1), exact, "f32", "misaligned causal")
+    # period 0 and scale 1: exactly cf_softmax's result.
+    xb = oracle.f32_to_bf16_bits(x)
+    np.testing.assert_array_equal(run_softmax_scaled(xb, "bf16", "bf16", 1.0, 0), run_softmax(xb, "bf16", "bf16"))
+
+
 @pytest.mark.parametrize("dtype,shape", [("bf16", (4099, 512)), ("f32", (4097, 256)), ("bf16", (2049, 384))],
                          ids=str)
 def test_softmax_two_rows_per_wave(dtype, shape):

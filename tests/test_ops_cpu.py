@@ -64,6 +64,24 @@ def test_softmax_stability_and_shift_invariance():
     assert cf.softmax_as(y.bfloat16(), torch.float32).dtype == torch.float32
 
 
+def test_softmax_scaled_is_the_causal_attention_softmax():
+    """softmax_scaled(s, scale, seq) on [batch * heads * seq, seq] scores equals
+    softmax(scores * scale + causal) as examples/transformer_block.py:57-59
+    composes it (per head block: row i keeps columns 0..i)."""
+    batch_heads, seq = 3, 16
+    scores = torch.randn(batch_heads, seq, seq) * 4
+    causal = torch.triu(torch.full((seq, seq), float("-inf")), 1)
+    expected = torch.softmax(scores * 0.125 + causal, dim=-1)
+    got = cf.softmax_scaled(scores.reshape(-1, seq), 0.125, seq).view(batch_heads, seq, seq)
+    torch.testing.assert_close(got, expected, rtol=1e-6, atol=1e-7)
+    assert (got[:, 0, 1:] == 0).all() and torch.equal(got[:, 0, 0], torch.ones(batch_heads))
+    # No mask: a scaled softmax; output dtype selectable; bad period refused.
+    torch.testing.assert_close(cf.softmax_scaled(scores, 2.0), torch.softmax(2.0 * scores, dim=-1))
+    assert cf.softmax_scaled(scores.bfloat16(), 1.0, seq, torch.float32).dtype == torch.float32
+    with pytest.raises(ValueError, match="causal_period"):
+        cf.softmax_scaled(scores, 1.0, -1)
+
+
 @pytest.mark.parametrize(("batch", "k", "n", "r"), [(1, 8, 4, 2), (4, 64, 32, 8), (7, 129, 65, 3), (16, 256, 256, 16)])
 def test_lora_linear_matches_the_definition(batch, k, n, r):
     x, w = torch.randn(batch, k), torch.randn(k, n)
