@@ -147,7 +147,10 @@ cf_status cf_quantize_dequantize(const void* x, void* y, cf_dtype dtype, int64_t
  * matrix; fp32 arithmetic for every storage dtype; eps inside the sqrt.
  * `x`, `w`, `y` share `dtype`. Replaces launch_rmsnorm / launch_rmsnorm_half /
  * launch_rmsnorm_bf16 (cuda/include/cudaforge/rmsnorm.cuh:35-62); semantics of
- * _rmsnorm_reference (python/cudaforge/ops.py:164-171). */
+ * _rmsnorm_reference (python/cudaforge/ops.py:164-171). launch_rmsnorm's
+ * `RMSNormKernel variant` (Naive, Vectorised: rmsnorm.cuh:9-19) chose between
+ * two implementations of this same function; the kernel here is chosen from
+ * the shape and alignment, so a caller drops the argument. */
 cf_status cf_rmsnorm(const void* x, const void* w, void* y, cf_dtype dtype, int64_t rows,
                      int64_t cols, float eps, void* stream);
 
@@ -165,7 +168,10 @@ cf_status cf_fused_residual_rmsnorm(const void* x, const void* residual, const v
  * `y_dtype` may differ from `x_dtype` (e.g. bf16 logits -> fp32 probabilities).
  * `x` and `y` may alias when the dtypes match. Replaces launch_softmax /
  * launch_softmax_half / launch_softmax_bf16 (cuda/include/cudaforge/softmax.cuh:43-65);
- * semantics of torch.softmax(x, -1) (python/cudaforge/ops.py:174-175). */
+ * semantics of torch.softmax(x, -1) (python/cudaforge/ops.py:174-175).
+ * launch_softmax's `SoftmaxKernel variant` (Naive, SharedMemory, Online:
+ * softmax.cuh:9-24) chose between implementations of this same function; the
+ * kernel here is chosen from the shape, so a caller drops the argument. */
 cf_status cf_softmax(const void* x, cf_dtype x_dtype, void* y, cf_dtype y_dtype, int64_t rows,
                      int64_t cols, void* stream);
 
@@ -191,7 +197,13 @@ size_t cf_reduce_sum_workspace_bytes(int64_t count);
  * With accumulate != 0 the sum is added to `*out` (the reference launcher's
  * contract: cuda/include/cudaforge/reduction.cuh:36-42); with 0 it overwrites.
  * Deterministic: a fixed two-stage tree whose shape depends only on `count`.
- * Replaces launch_reduce_sum (cuda/include/cudaforge/reduction.cuh:43-44). */
+ * Replaces launch_reduce_sum (cuda/include/cudaforge/reduction.cuh:43-44): its
+ * contract (add into a zeroed *out) is accumulate = 1. Its `ReductionKernel
+ * variant` (Naive, SharedMemory, WarpOptimised: reduction.cuh:14-34) chose
+ * between implementations of the same sum, and reduction_grid_size
+ * (reduction.cuh:55, the launch grid those variants used) has no counterpart:
+ * the grid here is a function of `count` alone, at most 4096 stage-1
+ * workgroups, i.e. cf_reduce_sum_workspace_bytes(count) / 4. */
 cf_status cf_reduce_sum(const void* x, cf_dtype x_dtype, float* out, int64_t count,
                         void* workspace, size_t workspace_bytes, int accumulate, void* stream);
 
@@ -230,7 +242,10 @@ size_t cf_lora_workspace_bytes(int64_t batch, int64_t rank);
  * there (the autograd path keeps it for the backward). Any rank >= 0: bf16
  * problems with an even rank <= 16 run the fused MFMA kernel, every other
  * rank the unfused path (cf_lora_workspace_bytes of xa_out required).
- * Replaces launch_lora_linear (cuda/include/cudaforge/lora_linear.cuh:49-51). */
+ * Replaces launch_lora_linear (cuda/include/cudaforge/lora_linear.cuh:49-51):
+ * its `workspace` (batch x rank floats for the unfused variant) is `xa_out`,
+ * and its `LoRAKernel variant` (Unfused, Fused: lora_linear.cuh:9-20) has no
+ * counterpart - the path is chosen from dtype, shape and alignment. */
 cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void* b, void* y,
                          float* xa_out, cf_dtype dtype, int64_t batch, int64_t in_features,
                          int64_t out_features, int64_t rank, float scale, void* stream);
