@@ -2,7 +2,7 @@
 """Benchmark of the custom-op hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--configs 1,2,3,4,5,paged,tensorcore,fp8]
+                    [--configs 1,ceiling,2,reduce,3,4,5,paged,tensorcore,fp8]
 
 Prints ONE JSON line (the driver's contract). The workload behind `value` is
 BASELINE.json's configs[1] - the memory-bound pair RMSNorm bf16 [16384, 4096]
@@ -34,7 +34,9 @@ for entry points that launch one kernel also the median of 25 dispatches
 timed by their own start/end timestamps, launched back to back
 (`kernel_median_ms`, the kernel-trace figure; `kernel_frac_*` is computed from
 it): config 1
-quantise/dequantise, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
+quantise/dequantise, `ceiling` the same two kernels and the streaming ceilings
+of their traffic (read-only 64 MiB, write-only 16 MiB, both, a copy) launched
+back to back over 2.6 GB of rotating buffers, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
 hipBLASLt's plain GEMM through torch for context) and its adapter backward,
 `reduce` the two-stage sum (16M and 256M fp32) and per-row sums,
 config 4 the Llama block forward (tokens/s end to end, per-operator event
@@ -312,6 +314,20 @@ def bench_quant(torch, cf, warmup: int, runs: int) -> dict:
 
     ceiling = summary(time_launches(torch, [stream(s) for s in sets], warmup, runs))
     with_kernel_time(torch, cf, ceiling, [stream(s) for s in sets], nbytes=n * 5)
+    # Its two halves alone, same load and store patterns: read 64 MiB (one
+    # word per 16 KiB written), and write 16 MiB (nothing read).
+    def read_only(s):
+        return lambda: cf._lib.check(lib.cf_stream_bytes(
+            s[0].data_ptr(), s[3].data_ptr(), n * 4, 0, torch.cuda.current_stream().cuda_stream))
+
+    def write_only(s):
+        return lambda: cf._lib.check(lib.cf_stream_bytes(
+            None, s[1].data_ptr(), n, -1, torch.cuda.current_stream().cuda_stream))
+
+    reads = summary(time_launches(torch, [read_only(s) for s in sets], warmup, runs))
+    with_kernel_time(torch, cf, reads, [read_only(s) for s in sets], nbytes=n * 4)
+    writes = summary(time_launches(torch, [write_only(s) for s in sets], warmup, runs))
+    with_kernel_time(torch, cf, writes, [write_only(s) for s in sets], nbytes=n)
     d = summary(time_launches(torch, [dequant(s) for s in sets], warmup, runs))
     with_kernel_time(torch, cf, d, [dequant(s) for s in sets], nbytes=bytes_dequant(n, 4))
     return {
@@ -323,7 +339,77 @@ def bench_quant(torch, cf, warmup: int, runs: int) -> dict:
         "stream_ceiling_read64MiB_write16MiB_context": {
             **ceiling, "bytes": n * 5, "GB/s": gbs(n * 5, ceiling["median_ms"]),
             "frac_hbm": gbs(n * 5, ceiling["median_ms"]) / PEAK_HBM_GBS},
+        "stream_read_only_64MiB_context": {
+            **reads, "bytes": n * 4, "GB/s": gbs(n * 4, reads["median_ms"]),
+            "frac_hbm": gbs(n * 4, reads["median_ms"]) / PEAK_HBM_GBS},
+        "stream_write_only_16MiB_context": {
+            **writes, "bytes": n, "GB/s": gbs(n, writes["median_ms"]),
+            "frac_hbm": gbs(n, writes["median_ms"]) / PEAK_HBM_GBS},
     }
+
+
+def bench_ceiling(torch, cf, warmup: int, runs: int) -> dict:
+    """Config 1's kernels next to the streaming ceilings of their traffic, all
+    under the same conditions: 32 rotating buffer sets (2.6 GB, so no launch
+    finds its input in the 256 MB Infinity Cache), one untimed pass over them,
+    then two passes launched back to back straight through ctypes (a Python
+    launch loop with per-call overhead near these ~15 us kernels' duration
+    lets the queue run dry between them) and timed by one HIP event pair.
+    Kernels: quantise and dequantise fp32 [4096, 4096]; reading the 64 MiB
+    input alone; writing 16 MiB alone; reading 64 MiB and writing 16 MiB
+    with the quantiser's pattern (cf_stream_bytes divisors 0, -1 and 4); and a
+    64 MiB copy; and config 5's 2 : 1 read/write mix at the size of one
+    grouped launch. `median_ms` is the median over 3 rounds of the per-launch
+    time."""
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    n = 4096 * 4096
+    lib = cf._lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    nsets = 32
+    xs = [with_outliers(torch, gen, torch.randn(n, generator=gen, device="cuda"), 0.01, 20.0)
+          for _ in range(nsets)]
+    qs = [torch.empty(n, dtype=torch.int8, device="cuda") for _ in range(nsets)]
+    ss = [torch.empty((n + 63) // 64, device="cuda") for _ in range(nsets)]
+    ys = [torch.empty(n, device="cuda") for _ in range(nsets)]
+    xp, qp, sp, yp = ([t.data_ptr() for t in ts] for ts in (xs, qs, ss, ys))
+    f32 = cf._lib.CF_F32
+    kinds = {
+        "quantize_f32_4096x4096": (bytes_quant(n, 4), lambda i: lib.cf_quantize_int8(xp[i], f32, qp[i], sp[i], n, st)),
+        "dequantize_f32_4096x4096": (bytes_dequant(n, 4),
+                                     lambda i: lib.cf_dequantize_int8(qp[i], sp[i], yp[i], f32, n, st)),
+        "read_only_64MiB": (n * 4, lambda i: lib.cf_stream_bytes(xp[i], sp[i], n * 4, 0, st)),
+        "write_only_16MiB": (n, lambda i: lib.cf_stream_bytes(None, qp[i], n, -1, st)),
+        "read_64MiB_write_16MiB": (n * 5, lambda i: lib.cf_stream_bytes(xp[i], qp[i], n * 4, 4, st)),
+        "copy_64MiB": (n * 8, lambda i: lib.cf_copy_bytes(xp[i], yp[i], n * 4, st)),
+    }
+    # Config 5's bulk bf16 quantiser moves 2 bytes in per byte out in launches
+    # of up to 48 tensors (~2.3 GB each): its traffic mix at that scale, one
+    # launch reading 1.5 GiB and writing 0.75 GiB (divisor 2).
+    big = 3 << 29
+    big_in = torch.empty(big, dtype=torch.uint8, device="cuda")
+    big_out = torch.empty(big // 2, dtype=torch.uint8, device="cuda")
+    kinds["read_1536MiB_write_768MiB"] = (
+        big + big // 2, lambda i: lib.cf_stream_bytes(big_in.data_ptr(), big_out.data_ptr(), big, 2, st))
+    samples: dict[str, list[float]] = {}
+    for _ in range(3):
+        for label, (_, call) in kinds.items():
+            for i in range(nsets):  # untimed pass, statuses checked
+                cf._lib.check(call(i))
+            start = torch.cuda.Event(enable_timing=True)
+            stop = torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(2):
+                for i in range(nsets):
+                    call(i)
+            stop.record()
+            torch.cuda.synchronize()
+            samples.setdefault(label, []).append(start.elapsed_time(stop) / (2 * nsets))
+    out = {}
+    for label, (nbytes, _) in kinds.items():
+        r = summary(samples[label])
+        out[f"ceiling_{label}"] = {**r, "bytes": nbytes, "GB/s": gbs(nbytes, r["median_ms"]),
+                                   "frac_hbm": gbs(nbytes, r["median_ms"]) / PEAK_HBM_GBS}
+    return out
 
 
 def bench_rowops(torch, cf, warmup: int, runs: int) -> dict:
@@ -799,8 +885,9 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--quick", action="store_true", help="skip the breakdown (main step only)")
-    parser.add_argument("--configs", default="1,2,reduce,3,4,5,paged,tensorcore,fp8",
-                        help="breakdown configs to run (comma-separated: 1-5, paged, tensorcore)")
+    parser.add_argument("--configs", default="1,ceiling,2,reduce,3,4,5,paged,tensorcore,fp8",
+                        help="breakdown configs to run (comma-separated: 1-5, ceiling, reduce, paged, "
+                             "tensorcore, fp8)")
     parser.add_argument("--detail", default="", help="also write the full result JSON here")
     args = parser.parse_args(argv)
 
@@ -833,6 +920,7 @@ def main(argv: list[str] | None = None) -> int:
         wanted = {c.strip() if not c.strip().isdigit() else f"config{c.strip()}"
                   for c in args.configs.split(",") if c.strip()}
         for name, fn in (("config1", lambda: bench_quant(torch, cf, args.warmup, args.runs)),
+                         ("ceiling", lambda: bench_ceiling(torch, cf, args.warmup, args.runs)),
                          ("config2", lambda: bench_rowops(torch, cf, args.warmup, args.runs)),
                          ("reduce", lambda: bench_reduce(torch, cf, args.warmup, args.runs)),
                          ("config3", lambda: bench_lora(torch, cf, args.warmup, args.runs)),

@@ -141,6 +141,19 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint4* __restrict__ s
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) v[u] = load_stream16(src + base + u * 256);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kDivisor == 0) {
+        // Read only: one 4-byte word per workgroup (1/4096 of the bytes
+        // read) - thread 0's xor of its vectors - so the loads are not dead.
+        // A plain store: L2 merges the words into whole lines, where 4096
+        // scattered non-temporal 4-byte writes slowed a 64 MiB read by a
+        // fifth.
+        uint32_t folded = 0;
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) folded ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(folded)));
+        if (threadIdx.x == 0) reinterpret_cast<uint32_t*>(dst)[blockIdx.x] = total;
+        return;
+    }
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
         const int64_t i = base + u * 256;
@@ -151,6 +164,18 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint4* __restrict__ s
         } else {
             store_stream4(dst + 4 * i, v[u].x ^ v[u].y ^ v[u].z ^ v[u].w);
         }
+    }
+}
+
+/// Write only: each lane stores four 16-byte vectors of its index (one
+/// 1 KiB piece per wave instruction, the copy's store pattern); nothing is
+/// read.
+__global__ __launch_bounds__(256) void write_stream_kernel(uint4* __restrict__ dst) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * kCopyUnroll + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+        const uint32_t i = static_cast<uint32_t>(base + u * 256);
+        store_stream16(dst + base + u * 256, make_uint4(i, ~i, i ^ 0x5bd1e995u, i + 1u));
     }
 }
 
@@ -200,13 +225,13 @@ int cf_time_next_launch_armed(void) { return cf::launch_events_armed() ? 1 : 0; 
 cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int divisor, void* stream) {
     CF_ENTRY();
     if (read_bytes <= 0) return CF_OK;
-    CF_REQUIRE(src != nullptr && dst != nullptr, "cf_stream_bytes: null pointer");
-    CF_REQUIRE(divisor == 1 || divisor == 2 || divisor == 4, "cf_stream_bytes: divisor %d is not 1, 2 or 4",
-               divisor);
+    CF_REQUIRE(dst != nullptr && (src != nullptr || divisor == -1), "cf_stream_bytes: null pointer");
+    CF_REQUIRE(divisor == 1 || divisor == 2 || divisor == 4 || divisor == 0 || divisor == -1,
+               "cf_stream_bytes: divisor %d is not 1, 2, 4, 0 or -1", divisor);
     constexpr int64_t kChunk = 256 * cf::kCopyUnroll * 16;
     CF_REQUIRE(read_bytes % kChunk == 0, "cf_stream_bytes: %lld bytes are not a multiple of %lld",
                static_cast<long long>(read_bytes), static_cast<long long>(kChunk));
-    CF_REQUIRE(cf::host_aligned(src, 16) && cf::host_aligned(dst, 16),
+    CF_REQUIRE((divisor == -1 || cf::host_aligned(src, 16)) && cf::host_aligned(dst, 16),
                "cf_stream_bytes: src and dst must be 16-byte aligned");
     const int64_t grid = read_bytes / kChunk;
     CF_REQUIRE(grid < (1LL << 31), "cf_stream_bytes: %lld bytes exceed the launch limit",
@@ -215,7 +240,11 @@ cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int di
     const dim3 g(static_cast<unsigned>(grid));
     const auto* in = static_cast<const uint4*>(src);
     auto* out = static_cast<uint8_t*>(dst);
-    if (divisor == 1) {
+    if (divisor == -1) {
+        cf::launch(cf::write_stream_kernel, g, dim3(256), 0, s, static_cast<uint4*>(dst));
+    } else if (divisor == 0) {
+        cf::launch(cf::stream_kernel<0>, g, dim3(256), 0, s, in, out);
+    } else if (divisor == 1) {
         cf::launch(cf::stream_kernel<1>, g, dim3(256), 0, s, in, out);
     } else if (divisor == 2) {
         cf::launch(cf::stream_kernel<2>, g, dim3(256), 0, s, in, out);

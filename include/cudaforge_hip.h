@@ -378,10 +378,13 @@ cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream)
 /* Reads `read_bytes` from `src` and writes read_bytes / `divisor` bytes
  * derived from them to `dst` (divisor 1, 2 or 4), with the fp32 quantiser's
  * access pattern (four 16-byte loads per lane, then the stores; one-shot
- * grid). read_bytes must be a multiple of 16 KiB and both pointers 16-byte
- * aligned. It has no counterpart in the reference: it measures the streaming
- * ceiling of a traffic mix (divisor 4 is the fp32 quantiser's 4 : 1) next to
- * the kernels that move it. */
+ * grid). Divisor 0 only reads (dst receives one 4-byte word per 16 KiB
+ * read); divisor -1 only writes read_bytes bytes to dst with the same store
+ * pattern (src unused, may be NULL). read_bytes must be a multiple of 16 KiB
+ * and the pointers used 16-byte aligned. It has no counterpart in the
+ * reference: it measures the streaming ceiling of a traffic mix (divisor 4
+ * is the fp32 quantiser's 4 : 1) and of its read and write halves next to
+ * the kernels that move them. */
 cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int divisor, void* stream);
 
 /* Arms the calling thread's next kernel launch made by this library: that

@@ -186,5 +186,7 @@ def test_stream_bytes_host_checks(lib):
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: rejected before any launch
     assert lib.cf_stream_bytes(null, null, 0, 4, null) == _lib.CF_OK
     assert lib.cf_stream_bytes(fake, fake, 16384, 3, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_stream_bytes(null, null, 16384, -1, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_stream_bytes(null, fake, 16384, 0, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_stream_bytes(fake, fake, 1000, 4, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_stream_bytes(null, fake, 16384, 4, null) == _lib.CF_ERR_INVALID_ARGUMENT

@@ -78,3 +78,25 @@ def test_stream_bytes_writes_what_it_read(divisor):
     else:
         want = v[:, 0] ^ v[:, 1] ^ v[:, 2] ^ v[:, 3]
     assert torch.equal(dst, want)
+
+
+def test_stream_bytes_read_only_and_write_only_modes():
+    """Divisor 0 reads only (workgroup b stores thread 0's xor of its four
+    vectors, the ones at 16-byte index 1024 b + 256 u); divisor -1 writes only
+    (vector i = (i, ~i, i ^ 0x5bd1e995, i + 1))."""
+    print("case: cf_stream_bytes read-only / write-only", flush=True)
+    src = torch.randint(0, 1 << 31, (1 << 14,), dtype=torch.int32, device="cuda")  # 64 KiB = 4 workgroups
+    dst = torch.zeros(4, dtype=torch.int32, device="cuda")
+    call("cf_stream_bytes", src.data_ptr(), dst.data_ptr(), src.numel() * 4, 0, stream())
+    out = torch.zeros(1 << 14, dtype=torch.int32, device="cuda")
+    call("cf_stream_bytes", None, out.data_ptr(), out.numel() * 4, -1, stream())
+    torch.cuda.synchronize()
+    vectors = src.view(-1, 4)
+    for b in range(4):
+        picked = vectors[[1024 * b + 256 * u for u in range(4)]]
+        want = picked[:, 0] ^ picked[:, 1] ^ picked[:, 2] ^ picked[:, 3]
+        assert int(dst[b]) == int(want[0] ^ want[1] ^ want[2] ^ want[3])
+    i = torch.arange(1 << 12, dtype=torch.int64, device="cuda")
+    expect = torch.stack([i, ~i & 0xFFFFFFFF, i ^ 0x5BD1E995, i + 1], dim=1) & 0xFFFFFFFF
+    got = out.view(-1, 4).to(torch.int64) & 0xFFFFFFFF
+    assert torch.equal(got, expect)
