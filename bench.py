@@ -2,7 +2,7 @@
 """Benchmark of the custom-op hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--configs 1,ceiling,2,reduce,3,4,5,paged,tensorcore,fp8]
+                    [--configs 1,ceiling,reference,2,reduce,3,4,5,paged,tensorcore,fp8]
 
 Prints ONE JSON line (the driver's contract). The workload behind `value` is
 BASELINE.json's configs[1] - the memory-bound pair RMSNorm bf16 [16384, 4096]
@@ -36,7 +36,9 @@ timed by their own start/end timestamps, launched back to back
 it): config 1
 quantise/dequantise, `ceiling` the same two kernels and the streaming ceilings
 of their traffic (read-only 64 MiB, write-only 16 MiB, both, a copy) launched
-back to back over 2.6 GB of rotating buffers, config 2 per kernel, config 3 fused LoRA TFLOP/s (with
+back to back over 2.6 GB of rotating buffers, `reference` every kernel the
+reference publishes a figure for at its own benchmark shape (fp32, with the
+reference's RTX 3090 figure beside it), config 2 per kernel, config 3 fused LoRA TFLOP/s (with
 hipBLASLt's plain GEMM through torch for context) and its adapter backward,
 `reduce` the two-stage sum (16M and 256M fp32) and per-row sums,
 config 4 the Llama block forward (tokens/s end to end, per-operator event
@@ -409,6 +411,107 @@ def bench_ceiling(torch, cf, warmup: int, runs: int) -> dict:
         r = summary(samples[label])
         out[f"ceiling_{label}"] = {**r, "bytes": nbytes, "GB/s": gbs(nbytes, r["median_ms"]),
                                    "frac_hbm": gbs(nbytes, r["median_ms"]) / PEAK_HBM_GBS}
+    return out
+
+
+# The reference's published kernel table (README.md:400-451; RTX 3090, fp32,
+# median of 100 event-timed launches): shape -> median ms, as context beside
+# this build's figures at the same shapes.
+REFERENCE_3090_MS = {
+    "sum_f32_64K": 0.0082, "sum_f32_1M": 0.0102, "sum_f32_16M": 0.0922,
+    "softmax_f32_128x8192": 0.0154, "rmsnorm_f32_4096x1024": 0.0440, "rmsnorm_f32_2048x4096": 0.0829,
+    "silu_f32_16M": 0.1567, "swiglu_f32_16M": 0.2294, "fused_residual_rmsnorm_f32_2048x4096": 0.1597,
+    "quantize_f32_16M": 0.1915, "dequantize_f32_16M": 0.1126,
+    "lora_f32_32x1024x1024_r8": 0.0850, "lora_f32_64x2048x2048_r16": 0.3640,
+    "lora_f32_128x4096x4096_r16": 2.0562,
+}
+
+
+def bench_reference_shapes(torch, cf, warmup: int, runs: int) -> dict:
+    """Every kernel the reference publishes a figure for, at its benchmark shape
+    (fp32; README.md:400-451). Memory-bound kernels report the median of 25
+    dispatches timed by their own timestamps (`kernel_median_ms`; the sum's
+    two launches by an event pair per batch instead) over >= 1 GiB of rotating
+    buffers; the LoRA linear reports TFLOP/s of event-timed batches.
+    `reference_3090_ms` is the reference's own figure (other hardware)."""
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    lib = cf._lib.load()
+    f32 = cf._lib.CF_F32
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    out = {}
+
+    def record(label, entry):
+        entry["reference_3090_ms"] = REFERENCE_3090_MS[label]
+        out[label] = entry
+
+    def streamed(label, nbytes, make, call):
+        sets = [make() for _ in range(sets_for(nbytes))]
+        launches = [lambda s=s: cf._lib.check(call(s)) for s in sets]
+        r = summary(time_launches(torch, launches, warmup, runs))
+        with_kernel_time(torch, cf, r, launches, nbytes=nbytes)
+        record(label, {**r, "bytes": nbytes, "GB/s": r["kernel_GB/s"], "frac_hbm": r["kernel_frac_hbm"]})
+
+    for n, label in ((1 << 16, "sum_f32_64K"), (1 << 20, "sum_f32_1M"), (1 << 24, "sum_f32_16M")):
+        ws = torch.empty(max(lib.cf_reduce_sum_workspace_bytes(n), 16), dtype=torch.uint8, device="cuda")
+        res = torch.empty(1, device="cuda")
+        sets = [torch.randn(n, generator=gen, device="cuda") for _ in range(sets_for(4 * n))]
+        launches = [lambda x=x, n=n, ws=ws: cf._lib.check(lib.cf_reduce_sum(
+            x.data_ptr(), f32, res.data_ptr(), n, ws.data_ptr(), ws.numel(), 0, st())) for x in sets]
+        r = summary(time_launches(torch, launches, warmup, runs))
+        record(label, {**r, "bytes": 4 * n, "launches": 2, "GB/s": gbs(4 * n, r["median_ms"]),
+                       "frac_hbm": gbs(4 * n, r["median_ms"]) / PEAK_HBM_GBS})
+    rows, cols = 128, 8192
+    streamed("softmax_f32_128x8192", 2 * rows * cols * 4,
+             lambda: (torch.randn(rows, cols, generator=gen, device="cuda"), torch.empty(rows, cols, device="cuda")),
+             lambda s: lib.cf_softmax(s[0].data_ptr(), f32, s[1].data_ptr(), f32, rows, cols, st()))
+    for rows, cols in ((4096, 1024), (2048, 4096)):
+        w = torch.randn(cols, generator=gen, device="cuda")
+        streamed(f"rmsnorm_f32_{rows}x{cols}", bytes_rmsnorm(rows, cols, 4),
+                 lambda rows=rows, cols=cols: (torch.randn(rows, cols, generator=gen, device="cuda"),
+                                               torch.empty(rows, cols, device="cuda")),
+                 lambda s, rows=rows, cols=cols, w=w: lib.cf_rmsnorm(
+                     s[0].data_ptr(), w.data_ptr(), s[1].data_ptr(), f32, rows, cols, 1e-6, st()))
+    n = 1 << 24
+    streamed("silu_f32_16M", 2 * n * 4,
+             lambda: (torch.randn(n, generator=gen, device="cuda"), torch.empty(n, device="cuda")),
+             lambda s: lib.cf_silu(s[0].data_ptr(), s[1].data_ptr(), f32, n, st()))
+    streamed("swiglu_f32_16M", 3 * n * 4,
+             lambda: tuple(torch.randn(n, generator=gen, device="cuda") for _ in range(3)),
+             lambda s: lib.cf_swiglu(s[0].data_ptr(), s[1].data_ptr(), s[2].data_ptr(), f32, n, st()))
+    rows, cols = 2048, 4096
+    w = torch.randn(cols, generator=gen, device="cuda")
+    streamed("fused_residual_rmsnorm_f32_2048x4096", 4 * rows * cols * 4,
+             lambda: tuple(torch.randn(rows, cols, generator=gen, device="cuda") for _ in range(4)),
+             lambda s: lib.cf_fused_residual_rmsnorm(s[0].data_ptr(), s[1].data_ptr(), w.data_ptr(), s[2].data_ptr(),
+                                                     s[3].data_ptr(), f32, rows, cols, 1e-6, st()))
+    streamed("quantize_f32_16M", bytes_quant(n, 4),
+             lambda: (torch.randn(n, generator=gen, device="cuda"), torch.empty(n, dtype=torch.int8, device="cuda"),
+                      torch.empty(n // 64, device="cuda")),
+             lambda s: lib.cf_quantize_int8(s[0].data_ptr(), f32, s[1].data_ptr(), s[2].data_ptr(), n, st()))
+    streamed("dequantize_f32_16M", bytes_dequant(n, 4),
+             lambda: (torch.randint(-127, 128, (n,), generator=gen, device="cuda", dtype=torch.int8),
+                      torch.rand(n // 64, generator=gen, device="cuda"), torch.empty(n, device="cuda")),
+             lambda s: lib.cf_dequantize_int8(s[0].data_ptr(), s[1].data_ptr(), s[2].data_ptr(), f32, n, st()))
+    for m, k, nn, r in ((32, 1024, 1024, 8), (64, 2048, 2048, 16), (128, 4096, 4096, 16)):
+        label = f"lora_f32_{m}x{k}x{nn}_r{r}"
+        flops = flops_lora(m, k, nn, r)
+        set_bytes = 4 * (m * k + k * nn + k * r + r * nn + m * nn)
+        sets = []
+        for _ in range(sets_for(set_bytes)):
+            sets.append((torch.randn(m, k, generator=gen, device="cuda"),
+                         0.02 * torch.randn(k, nn, generator=gen, device="cuda"),
+                         torch.randn(k, r, generator=gen, device="cuda") / 64,
+                         0.02 * torch.randn(r, nn, generator=gen, device="cuda"),
+                         torch.empty(m, nn, device="cuda"), torch.empty(m, r, device="cuda")))
+        ws_bytes = lib.cf_lora_linear_ws_bytes(f32, m, k, nn, r)
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
+        launches = [lambda s=s, m=m, k=k, nn=nn, r=r, ws_bytes=ws_bytes, ws=ws: cf._lib.check(lib.cf_lora_linear_ws(
+            s[0].data_ptr(), s[1].data_ptr(), s[2].data_ptr(), s[3].data_ptr(), s[4].data_ptr(), s[5].data_ptr(),
+            f32, m, k, nn, r, 2.0, ws.data_ptr() if ws_bytes else None, ws_bytes, st())) for s in sets]
+        res = summary(time_launches(torch, launches, warmup, max(runs // 4, 8)))
+        tflops = flops / (res["median_ms"] * 1e-3) / 1e12
+        record(label, {**res, "flops": flops, "TFLOP/s": tflops})
+        del sets
     return out
 
 
@@ -885,9 +988,9 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--quick", action="store_true", help="skip the breakdown (main step only)")
-    parser.add_argument("--configs", default="1,ceiling,2,reduce,3,4,5,paged,tensorcore,fp8",
-                        help="breakdown configs to run (comma-separated: 1-5, ceiling, reduce, paged, "
-                             "tensorcore, fp8)")
+    parser.add_argument("--configs", default="1,ceiling,reference,2,reduce,3,4,5,paged,tensorcore,fp8",
+                        help="breakdown configs to run (comma-separated: 1-5, ceiling, reference, "
+                             "reduce, paged, tensorcore, fp8)")
     parser.add_argument("--detail", default="", help="also write the full result JSON here")
     args = parser.parse_args(argv)
 
@@ -921,6 +1024,7 @@ def main(argv: list[str] | None = None) -> int:
                   for c in args.configs.split(",") if c.strip()}
         for name, fn in (("config1", lambda: bench_quant(torch, cf, args.warmup, args.runs)),
                          ("ceiling", lambda: bench_ceiling(torch, cf, args.warmup, args.runs)),
+                         ("reference", lambda: bench_reference_shapes(torch, cf, args.warmup, args.runs)),
                          ("config2", lambda: bench_rowops(torch, cf, args.warmup, args.runs)),
                          ("reduce", lambda: bench_reduce(torch, cf, args.warmup, args.runs)),
                          ("config3", lambda: bench_lora(torch, cf, args.warmup, args.runs)),

@@ -83,6 +83,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_row_sum": (_I32, [_P, _I32, _P, _I64, _I64, _P]),
     "cf_lora_workspace_bytes": (_SZ, [_I64, _I64]),
     "cf_lora_linear": (_I32, [_P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _F, _P]),
+    "cf_lora_linear_ws_bytes": (_SZ, [_I32, _I64, _I64, _I64, _I64]),
+    "cf_lora_linear_ws": (
+        _I32,
+        [_P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _F, _P, _SZ, _P],
+    ),
     "cf_matmul": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _P]),
     "cf_lora_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "cf_lora_backward": (

@@ -8,9 +8,14 @@
 // Fast path (bf16, K % 64 == 0, N % 8 == 0, r <= 16, 16-byte aligned): the
 // fused MFMA kernel in cf_lora_fused.hip, one launch.
 //
-// Generic path (fp32, or shapes the fast path does not take): x @ a into a
-// fp32 [M, r] workspace (one wave per row), then a 64x64-tiled fp32 FMA GEMM
-// whose epilogue adds scale * (xa @ b).
+// fp32 (r <= 16, K and N multiples of 4, 16-byte aligned): the MFMA kernel of
+// cf_lora_f32.hip, operands split into bf16 high and low parts on the way
+// into LDS, one launch (plus a fixed-order sum when a workspace lets it split
+// the reduction).
+//
+// Generic path (shapes neither fast path takes): x @ a into a fp32 [M, r]
+// workspace (one wave per row), then a 64x64-tiled fp32 FMA GEMM whose
+// epilogue adds scale * (xa @ b).
 //
 // Backward (adapter only, op layout):
 //   G      = dy @ b^T            [M, r]
@@ -22,6 +27,7 @@
 // the chunks in a fixed order (deterministic).
 #include "cf_common.hpp"
 #include "cf_lora_bwd.hpp"
+#include "cf_lora_f32.hpp"
 #include "cf_lora_fused.hpp"
 
 namespace cf {
@@ -314,6 +320,13 @@ cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void
         return cf::launch_lora_fused(x, w, a, b, y, xa_out, batch, out_features, in_features, rank,
                                 scale, s);
     }
+    if (dtype == CF_F32 &&
+        cf::lora_f32_eligible(x, w, a, b, y, batch, out_features, in_features, rank)) {
+        return cf::launch_lora_f32(static_cast<const float*>(x), static_cast<const float*>(w),
+                                   static_cast<const float*>(a), static_cast<const float*>(b),
+                                   static_cast<float*>(y), xa_out, batch, out_features, in_features,
+                                   rank, scale, 1, nullptr, s);
+    }
     CF_REQUIRE(rank == 0 || xa_out != nullptr,
                "cf_lora_linear: this shape takes the unfused path, which needs xa_out "
                "(cf_lora_workspace_bytes(batch, rank) bytes) as its workspace");
@@ -323,6 +336,42 @@ cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void
     }
     return cf::launch_generic<cf::bf16_t>(x, w, a, b, y, xa_out, batch, out_features, in_features,
                                           rank, scale, s);
+}
+
+size_t cf_lora_linear_ws_bytes(cf_dtype dtype, int64_t batch, int64_t in_features,
+                               int64_t out_features, int64_t rank) {
+    if (dtype != CF_F32 || batch <= 0 || in_features <= 0 || out_features <= 0 || rank < 0 ||
+        rank > 16 || in_features % 4 != 0 || out_features % 4 != 0) {
+        return 0;
+    }
+    const int splits = cf::lora_f32_splits(batch, out_features, in_features);
+    return cf::lora_f32_workspace_bytes(batch, out_features, rank, splits);
+}
+
+cf_status cf_lora_linear_ws(const void* x, const void* w, const void* a, const void* b, void* y,
+                            float* xa_out, cf_dtype dtype, int64_t batch, int64_t in_features,
+                            int64_t out_features, int64_t rank, float scale, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+    CF_ENTRY();
+    if (batch <= 0 || out_features <= 0) return CF_OK;
+    CF_REQUIRE(in_features >= 0 && rank >= 0, "cf_lora_linear_ws: negative dimension");
+    const size_t needed = cf_lora_linear_ws_bytes(dtype, batch, in_features, out_features, rank);
+    if (needed > 0 &&
+        cf::lora_f32_eligible(x, w, a, b, y, batch, out_features, in_features, rank)) {
+        CF_REQUIRE(x != nullptr && w != nullptr && y != nullptr && (rank == 0 || (a != nullptr && b != nullptr)),
+                   "cf_lora_linear_ws: null pointer");
+        CF_REQUIRE(workspace != nullptr && workspace_bytes >= needed,
+                   "cf_lora_linear_ws: workspace of %zu bytes given, %zu needed", workspace_bytes,
+                   needed);
+        CF_REQUIRE(cf::host_aligned(workspace, 16), "cf_lora_linear_ws: workspace must be 16-byte aligned");
+        return cf::launch_lora_f32(static_cast<const float*>(x), static_cast<const float*>(w),
+                                   static_cast<const float*>(a), static_cast<const float*>(b),
+                                   static_cast<float*>(y), xa_out, batch, out_features, in_features,
+                                   rank, scale, cf::lora_f32_splits(batch, out_features, in_features),
+                                   workspace, static_cast<hipStream_t>(stream));
+    }
+    return cf_lora_linear(x, w, a, b, y, xa_out, dtype, batch, in_features, out_features, rank,
+                          scale, stream);
 }
 
 cf_status cf_matmul(const void* a, const void* b, void* c, cf_dtype dtype, int64_t m, int64_t n,
@@ -335,6 +384,11 @@ cf_status cf_matmul(const void* a, const void* b, void* c, cf_dtype dtype, int64
     auto s = static_cast<hipStream_t>(stream);
     if (dtype == CF_BF16 && cf::lora_fused_eligible(a, b, nullptr, nullptr, m, n, k, 0)) {
         return cf::launch_lora_fused(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);
+    }
+    if (dtype == CF_F32 && cf::lora_f32_eligible(a, b, nullptr, nullptr, c, m, n, k, 0)) {
+        return cf::launch_lora_f32(static_cast<const float*>(a), static_cast<const float*>(b), nullptr,
+                                   nullptr, static_cast<float*>(c), nullptr, m, n, k, 0, 0.0f, 1,
+                                   nullptr, s);
     }
     if (dtype == CF_F32) {
         return cf::launch_generic<float>(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);

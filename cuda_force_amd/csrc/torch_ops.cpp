@@ -162,10 +162,17 @@ std::tuple<torch::Tensor, torch::Tensor> lora_linear_fwd_hip(const torch::Tensor
     const at::DeviceGuard guard(x.device());
     torch::Tensor output = torch::empty({batch, out_features}, x.options());
     torch::Tensor xa = torch::empty({batch, rank}, x.options().dtype(torch::kFloat32));
-    check_status(cf_lora_linear(x.data_ptr(), w.data_ptr(), a.data_ptr(), b.data_ptr(),
-                                output.data_ptr(), xa.data_ptr<float>(), to_cf(x, "x"), batch,
-                                in_features, out_features, rank, static_cast<float>(scale),
-                                stream_for(x)));
+    // Small fp32 problems split their reduction through a workspace from
+    // torch's caching allocator (no synchronising hipMalloc).
+    const size_t ws_bytes =
+        cf_lora_linear_ws_bytes(to_cf(x, "x"), batch, in_features, out_features, rank);
+    torch::Tensor workspace =
+        torch::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, x.options().dtype(torch::kUInt8));
+    check_status(cf_lora_linear_ws(x.data_ptr(), w.data_ptr(), a.data_ptr(), b.data_ptr(),
+                                   output.data_ptr(), xa.data_ptr<float>(), to_cf(x, "x"), batch,
+                                   in_features, out_features, rank, static_cast<float>(scale),
+                                   ws_bytes > 0 ? workspace.data_ptr() : nullptr, ws_bytes,
+                                   stream_for(x)));
     return {output, xa};
 }
 

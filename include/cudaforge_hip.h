@@ -240,8 +240,10 @@ size_t cf_lora_workspace_bytes(int64_t batch, int64_t rank);
  * reference's ATen path does. When `xa_out` is non-NULL the fp32 adapter
  * intermediate x @ a ([batch, rank], before that rounding) is also written
  * there (the autograd path keeps it for the backward). Any rank >= 0: bf16
- * problems with an even rank <= 16 run the fused MFMA kernel, every other
- * rank the unfused path (cf_lora_workspace_bytes of xa_out required).
+ * problems with an even rank <= 16 run the fused MFMA kernel, fp32 problems
+ * with rank <= 16 and in_features, out_features multiples of 4 the fp32 MFMA
+ * kernel of cf_lora_linear_ws (one slice), every other case the unfused path
+ * (cf_lora_workspace_bytes of xa_out required).
  * Replaces launch_lora_linear (cuda/include/cudaforge/lora_linear.cuh:49-51):
  * its `workspace` (batch x rank floats for the unfused variant) is `xa_out`,
  * and its `LoRAKernel variant` (Unfused, Fused: lora_linear.cuh:9-20) has no
@@ -249,6 +251,29 @@ size_t cf_lora_workspace_bytes(int64_t batch, int64_t rank);
 cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void* b, void* y,
                          float* xa_out, cf_dtype dtype, int64_t batch, int64_t in_features,
                          int64_t out_features, int64_t rank, float scale, void* stream);
+
+/* Workspace bytes cf_lora_linear_ws can use to split the reduction of a small
+ * fp32 problem across workgroups (0 when it would not split: bf16, large
+ * outputs, shapes the fp32 MFMA kernel does not take). It has no counterpart
+ * in the reference, whose launcher's workspace is the batch x rank
+ * intermediate (cuda/include/cudaforge/lora_linear.cuh:62). */
+size_t cf_lora_linear_ws_bytes(cf_dtype dtype, int64_t batch, int64_t in_features,
+                               int64_t out_features, int64_t rank);
+
+/* cf_lora_linear with a workspace of cf_lora_linear_ws_bytes(...) bytes
+ * (16-byte aligned; NULL when that is 0). fp32 problems with rank <= 16 and
+ * in_features, out_features multiples of 4 run on the MFMA units with each
+ * operand split into bf16 high and low parts (three products per term, about
+ * 2^-16 relative error per product; fp32 accumulation), and a small problem
+ * splits its reduction range across workgroups, partial results summed in a
+ * fixed order (deterministic). cf_lora_linear runs the same kernel without
+ * the split. Replaces launch_lora_linear
+ * (cuda/include/cudaforge/lora_linear.cuh:49-51) for callers that can give
+ * it a workspace. */
+cf_status cf_lora_linear_ws(const void* x, const void* w, const void* a, const void* b, void* y,
+                            float* xa_out, cf_dtype dtype, int64_t batch, int64_t in_features,
+                            int64_t out_features, int64_t rank, float scale, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /* c[m, n] = a[m, k] @ b[k, n], row-major, one dtype (fp32 or bf16), fp32
  * accumulation. Replaces launch_matmul (cuda/include/cudaforge/lora_linear.cuh:57-58). */

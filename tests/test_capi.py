@@ -88,6 +88,22 @@ def test_invalid_arguments_are_reported_not_thrown(lib):
                                null, 0, 0, null)
     assert status == _lib.CF_ERR_INVALID_ARGUMENT
     assert b"workspace" in lib.cf_last_error()
+    # The fp32 LoRA workspace: 0 for bf16 and for shapes the fp32 MFMA kernel
+    # does not take; one smaller than asked for is rejected before any launch.
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 32, 1024, 1024, 8) == 0
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_F32, 32, 1022, 1024, 8) == 0
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_F32, 32, 1024, 1024, 17) == 0
+    nbytes = lib.cf_lora_linear_ws_bytes(_lib.CF_F32, 32, 1024, 1024, 8)
+    assert nbytes >= 2 * 32 * 1024 * 4
+    p = ctypes.c_void_p(4096)
+    status = lib.cf_lora_linear_ws(p, p, p, p, p, null, _lib.CF_F32, 32, 1024, 1024, 8, 0.5, p,
+                                   nbytes - 256, null)
+    assert status == _lib.CF_ERR_INVALID_ARGUMENT
+    assert b"workspace" in lib.cf_last_error()
+    status = lib.cf_lora_linear_ws(p, p, p, p, p, null, _lib.CF_F16, 32, 1024, 1024, 8, 0.5, null, 0,
+                                   null)
+    assert status == _lib.CF_ERR_INVALID_ARGUMENT
+    assert b"float16" in lib.cf_last_error()
 
 
 def test_sticky_error_classification(lib):

@@ -62,6 +62,59 @@ def test_fp32_reference_shapes(shape):
     assert_gemm_close(y, oracle.lora_linear(x, w, a, b, 0.25, False), "f32", f"fp32 {shape}")
 
 
+def run_lora_ws(x, w, a, b, scale: float):
+    """fp32 through cf_lora_linear_ws with the workspace it asks for."""
+    m, k = x.shape
+    n = w.shape[1]
+    r = a.shape[1]
+    xg, wg, ag, bg = (g.to_gpu(t, "f32") for t in (x, w, a, b))
+    yg = g.empty((m, n), torch.float32)
+    xa = g.empty((m, max(r, 1)), torch.float32)
+    nbytes = g.lib().cf_lora_linear_ws_bytes(g.cf("f32"), m, k, n, r)
+    ws = g.empty(max(nbytes, 16), torch.uint8)
+    g.call("cf_lora_linear_ws", xg.data_ptr(), wg.data_ptr(), ag.data_ptr(), bg.data_ptr(), yg.data_ptr(),
+           xa.data_ptr(), g.cf("f32"), m, k, n, r, scale, ws.data_ptr() if nbytes else None, nbytes, g.stream())
+    torch.cuda.synchronize()
+    return g.to_host(yg), g.to_host(xa), nbytes
+
+
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (32, 1024, 1024, 8),     # the reference's benchmark shapes (README.md:449-451)
+        (64, 2048, 2048, 16),
+        (128, 4096, 4096, 16),
+        (100, 260, 132, 5),      # ragged M, N, K (multiples of 4), odd rank
+        (1000, 512, 520, 12),    # many row tiles
+        (3, 4, 8, 1),            # one partial K-step
+        (70, 36, 68, 16),        # two K-steps, the second partial
+        (40, 8192, 64, 16),      # one tile, long reduction: many slices
+        (48, 512, 256, 0),       # no adapter
+    ],
+)
+def test_fp32_mfma_path(shape):
+    """fp32 problems with rank <= 16 and K, N multiples of 4 take the MFMA
+    kernel (bf16 high/low split): one slice through cf_lora_linear, a split
+    reduction through cf_lora_linear_ws; both within the fp32 tolerance of the
+    float64 oracle, x @ a too, and the split sum bit-identical between runs."""
+    m, k, n, r = shape
+    g.announce(f"fp32 MFMA LoRA {shape}")
+    gen = rng(7 * m + k + n + r)
+    x, w, a, b = (gen.standard_normal(s).astype(np.float32) for s in ((m, k), (k, n), (k, r), (r, n)))
+    exact = oracle.lora_linear(x, w, a, b, 0.25, False)
+    exact_xa = x.astype(np.float64) @ a.astype(np.float64)
+    y1, xa1 = run_lora(x, w, a, b, "f32", 0.25)
+    assert_gemm_close(y1, exact, "f32", f"one slice {shape}")
+    y2, xa2, nbytes = run_lora_ws(x, w, a, b, 0.25)
+    assert_gemm_close(y2, exact, "f32", f"split reduction ({nbytes} B workspace) {shape}")
+    if r > 0:
+        assert_gemm_close(xa1[:, :r], exact_xa, "f32", f"x @ a one slice {shape}")
+        assert_gemm_close(xa2[:, :r], exact_xa, "f32", f"x @ a split {shape}")
+    y3, xa3, _ = run_lora_ws(x, w, a, b, 0.25)
+    assert np.array_equal(y2.view(np.uint32), y3.view(np.uint32)), f"split sum not deterministic {shape}"
+    assert np.array_equal(xa2.view(np.uint32), xa3.view(np.uint32)), f"split x @ a not deterministic {shape}"
+
+
 def test_fp32_golden_cases():
     for case, d in load_golden("lora.npz").items():
         if not case.startswith("f32"):
