@@ -30,8 +30,8 @@ each op for about --cpu-seconds of CPU work, on this host's cores.
 median over 5 batches of back-to-back launches timed by HIP events, after at
 least 0.3 s of warm-up, with cache-cold rotation (`median_ms`: launch-to-launch
 time, which for kernels of a few microseconds is the host's launch rate), and
-for entry points that launch one kernel also the median of 25 dispatches
-timed by their own start/end timestamps, launched back to back
+the median of 25 calls timed by their kernels' own start/end timestamps
+(from the first kernel's start to the last one's end), launched back to back
 (`kernel_median_ms`, the kernel-trace figure; `kernel_frac_*` is computed from
 it): config 1
 quantise/dequantise, `ceiling` the same two kernels and the streaming ceilings
@@ -66,6 +66,8 @@ sys.path.insert(0, str(ROOT))
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA
 PEAK_FP8_TFLOPS = 5000.0       # dense fp8 MFMA
+PEAK_FP32_TFLOPS = 157.3       # fp32 (the fp32 LoRA rows' reference point; they run as 3 bf16 MFMA products)
+SUM_SINGLE_LAUNCH_BYTES = 256 * 1024  # cf_reduce_sum: one launch up to this input size
 KERNEL_SAMPLES = 25            # breakdown: dispatches timed by their own timestamps
 TIMER_STRIDE = 8               # main step: every 8th RMSNorm dispatch is timed
 METRIC = "INT8 quant/RMSNorm/softmax GB/s (% HBM peak); fused LoRA-linear TFLOP/s"
@@ -153,7 +155,8 @@ def kernel_times(torch, cf, launches, count: int = KERNEL_SAMPLES) -> list[float
     less the median can read 10-30% long on some runs (the Python launch loop
     then falls behind the GPU and some dispatches start from an idle queue);
     the kernel-trace averages in profiles/ are the reference figures there.
-    Only for entry points that launch one kernel."""
+    An entry point of several kernels is timed from its first kernel's start
+    to its last kernel's end."""
     timers = [cf._lib.DispatchTimer() for _ in range(count)]
     torch.cuda.synchronize()
     for i, timer in enumerate(timers):
@@ -429,11 +432,13 @@ REFERENCE_3090_MS = {
 
 def bench_reference_shapes(torch, cf, warmup: int, runs: int) -> dict:
     """Every kernel the reference publishes a figure for, at its benchmark shape
-    (fp32; README.md:400-451). Memory-bound kernels report the median of 25
-    dispatches timed by their own timestamps (`kernel_median_ms`; the sum's
-    two launches by an event pair per batch instead) over >= 1 GiB of rotating
-    buffers; the LoRA linear reports TFLOP/s of event-timed batches.
-    `reference_3090_ms` is the reference's own figure (other hardware)."""
+    (fp32; README.md:400-451). Every row reports the median of 25 calls timed
+    by their kernels' own timestamps (`kernel_median_ms`, first kernel's start
+    to last kernel's end) beside the launch-loop median (`median_ms`, which
+    for calls of a few microseconds is the Python launch rate), over >= 1 GiB
+    of rotating buffers; rates (GB/s, TFLOP/s) are from `kernel_median_ms`.
+    `reference_3090_ms` is the reference's own figure (other hardware), an
+    event pair around each launch (benchmarks/benchmark_kernels.cu:59-79)."""
     gen = torch.Generator(device="cuda").manual_seed(12)
     lib = cf._lib.load()
     f32 = cf._lib.CF_F32
@@ -458,8 +463,9 @@ def bench_reference_shapes(torch, cf, warmup: int, runs: int) -> dict:
         launches = [lambda x=x, n=n, ws=ws: cf._lib.check(lib.cf_reduce_sum(
             x.data_ptr(), f32, res.data_ptr(), n, ws.data_ptr(), ws.numel(), 0, st())) for x in sets]
         r = summary(time_launches(torch, launches, warmup, runs))
-        record(label, {**r, "bytes": 4 * n, "launches": 2, "GB/s": gbs(4 * n, r["median_ms"]),
-                       "frac_hbm": gbs(4 * n, r["median_ms"]) / PEAK_HBM_GBS})
+        with_kernel_time(torch, cf, r, launches, nbytes=4 * n)
+        record(label, {**r, "bytes": 4 * n, "launches": 1 if 4 * n <= SUM_SINGLE_LAUNCH_BYTES else 2,
+                       "GB/s": r["kernel_GB/s"], "frac_hbm": r["kernel_frac_hbm"]})
     rows, cols = 128, 8192
     streamed("softmax_f32_128x8192", 2 * rows * cols * 4,
              lambda: (torch.randn(rows, cols, generator=gen, device="cuda"), torch.empty(rows, cols, device="cuda")),
@@ -509,8 +515,8 @@ def bench_reference_shapes(torch, cf, warmup: int, runs: int) -> dict:
             s[0].data_ptr(), s[1].data_ptr(), s[2].data_ptr(), s[3].data_ptr(), s[4].data_ptr(), s[5].data_ptr(),
             f32, m, k, nn, r, 2.0, ws.data_ptr() if ws_bytes else None, ws_bytes, st())) for s in sets]
         res = summary(time_launches(torch, launches, warmup, max(runs // 4, 8)))
-        tflops = flops / (res["median_ms"] * 1e-3) / 1e12
-        record(label, {**res, "flops": flops, "TFLOP/s": tflops})
+        with_kernel_time(torch, cf, res, launches, flops=flops, peak=PEAK_FP32_TFLOPS)
+        record(label, {**res, "flops": flops, "launches": 2 if ws_bytes else 1, "TFLOP/s": res["kernel_TFLOP/s"]})
         del sets
     return out
 
@@ -626,6 +632,7 @@ def bench_reduce(torch, cf, warmup: int, runs: int) -> dict:
             x.data_ptr(), cf._lib.CF_F32, res.data_ptr(), n, ws.data_ptr(), ws_bytes, 0,
             torch.cuda.current_stream().cuda_stream)) for x in sets]
         r = summary(time_launches(torch, launches, warmup, runs))
+        with_kernel_time(torch, cf, r, launches, nbytes=nbytes)
         out[label] = {**r, "bytes": nbytes, "launches": 2, "GB/s": gbs(nbytes, r["median_ms"]),
                       "frac_hbm": gbs(nbytes, r["median_ms"]) / PEAK_HBM_GBS}
         del sets

@@ -392,6 +392,12 @@ struct LaunchEvents {
 /// Hand out and disarm the calling thread's armed events.
 LaunchEvents take_launch_events();
 
+/// Events for the kernel about to launch: the start event once (the entry
+/// point's first kernel records its start), the stop event to every launch
+/// until the entry point returns (the last kernel's completion stays
+/// recorded), so an entry point of several kernels is timed whole.
+LaunchEvents next_launch_events();
+
 /// True when cf_time_next_launch() left events armed on the calling thread.
 bool launch_events_armed();
 
@@ -412,14 +418,16 @@ struct EntryScope {
 void note_launch_error(hipError_t error);
 
 /// Launch `kernel` on `stream`. When cf_time_next_launch() armed events on
-/// this thread, the dispatch itself records its start and completion on them
-/// (hipExtLaunchKernel), so their elapsed time is the kernel's own execution
-/// time, without the queue packets an event pair around the launch adds.
+/// this thread, the dispatch itself records them (hipExtLaunchKernel): the
+/// entry point's first kernel its start, each kernel its completion, so their
+/// elapsed time is the entry point's GPU time from its first kernel's start to
+/// its last kernel's end, without the queue packets an event pair around the
+/// call adds.
 template <typename... KArgs, typename... Args>
 inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes,
                    hipStream_t stream, Args&&... args) {
     static_assert(sizeof...(KArgs) == sizeof...(Args), "argument count of the kernel");
-    const LaunchEvents events = take_launch_events();
+    const LaunchEvents events = next_launch_events();
     if (events.start == nullptr && events.stop == nullptr) {
         kernel<<<grid, block, lds_bytes, stream>>>(std::forward<Args>(args)...);
         return;

@@ -13,6 +13,10 @@
 //            iteration cost 1.3 us at 16M elements), reduces it in a fixed
 //            order and writes (or adds into) *out.
 //
+// Inputs of at most 256 KiB skip the tree: one workgroup of 1024 threads sums
+// them (the same per-lane loop, sixteen loads in flight) and writes *out, one
+// launch instead of two.
+//
 // G and the chunk size are functions of `count` only, so the same input gives
 // the same bits on any device and on every run.
 //
@@ -28,7 +32,11 @@ namespace {
 
 constexpr int kWavesPerBlock = kDefaultBlockSize / kWaveSize;
 constexpr int64_t kMaxPartials = 4096;  // 2048 and 8192 measured 2% and 0.5% slower at 256M
-constexpr int64_t kMinChunk = 8192;
+// One round of stage-1 loads (256 threads x 4 vectors x 16 bytes) per chunk
+// at least, so mid-size inputs spread over more workgroups, each one round
+// trip deep.
+constexpr int kStage1Unroll = 4;
+constexpr int64_t kMinChunk = 4096;
 constexpr int kPartialsPerThread = 8;
 constexpr int kStage2Threads = 512;
 static_assert(kMaxPartials == kStage2Threads * kPartialsPerThread,
@@ -40,29 +48,28 @@ int64_t partial_count(int64_t count) {
     return wanted < kMaxPartials ? (wanted < 1 ? 1 : wanted) : kMaxPartials;
 }
 
-template <typename T, bool kVec>
-__global__ __launch_bounds__(kDefaultBlockSize) void sum_stage1_kernel(const T* __restrict__ x,
-                                                                       float* __restrict__ partial,
-                                                                       int64_t count,
-                                                                       int64_t chunk) {
-    __shared__ float slot[kWavesPerBlock];
+/// Sum of x[begin, end) over one workgroup of kThreads threads: 16-byte
+/// loads, kUnroll in flight and four independent accumulators per lane, a
+/// DPP wave reduction and an LDS exchange across the waves (every thread
+/// receives the total). kVec: x 16-byte aligned, begin a multiple of
+/// kPer * kThreads elements.
+template <typename T, bool kVec, int kThreads, int kUnroll>
+__device__ __forceinline__ float range_sum(const T* __restrict__ x, int64_t begin, int64_t end, float* slot) {
     constexpr int kPer = Storage<T>::kPerVec;
-    const int64_t begin = static_cast<int64_t>(blockIdx.x) * chunk;
-    const int64_t end = begin + chunk < count ? begin + chunk : count;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (kVec) {
-        // chunk is a multiple of kPer * blockDim, so every vector is aligned
-        // and lies entirely before `end` unless it straddles `count`.
-        const int64_t step = static_cast<int64_t>(blockDim.x) * kPer;
+        // Every vector is aligned and lies entirely before `end` unless it
+        // straddles it (the scalar tail).
+        constexpr int64_t step = static_cast<int64_t>(kThreads) * kPer;
         int64_t e = begin + static_cast<int64_t>(threadIdx.x) * kPer;
-        // Four loads in flight per lane: issued together, then accumulated
+        // kUnroll loads in flight per lane: issued together, then accumulated
         // (one load per iteration left each lane waiting on its latency).
-        for (; e + 3 * step + kPer <= end; e += 4 * step) {
-            uint4 raw[4];
+        for (; e + (kUnroll - 1) * step + kPer <= end; e += kUnroll * step) {
+            uint4 raw[kUnroll];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) raw[u] = *reinterpret_cast<const uint4*>(x + e + u * step);
+            for (int u = 0; u < kUnroll; ++u) raw[u] = *reinterpret_cast<const uint4*>(x + e + u * step);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < kUnroll; ++u) {
                 float v[kPer];
                 unpack16<T>(raw[u], v);
 #pragma unroll
@@ -79,13 +86,41 @@ __global__ __launch_bounds__(kDefaultBlockSize) void sum_stage1_kernel(const T* 
             if (e + i < end) acc[0] += Storage<T>::load(x + e + i);
         }
     } else {
-        for (int64_t e = begin + threadIdx.x; e < end; e += blockDim.x) {
+        for (int64_t e = begin + threadIdx.x; e < end; e += kThreads) {
             acc[0] += Storage<T>::load(x + e);
         }
     }
-    const float total =
-        block_reduce_f32<kWavesPerBlock, AddF32>((acc[0] + acc[1]) + (acc[2] + acc[3]), slot);
+    return block_reduce_f32<kThreads / kWaveSize, AddF32>((acc[0] + acc[1]) + (acc[2] + acc[3]), slot);
+}
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(kDefaultBlockSize) void sum_stage1_kernel(const T* __restrict__ x,
+                                                                       float* __restrict__ partial,
+                                                                       int64_t count,
+                                                                       int64_t chunk) {
+    __shared__ float slot[kWavesPerBlock];
+    // chunk is a multiple of kPer * blockDim, so every chunk starts aligned.
+    const int64_t begin = static_cast<int64_t>(blockIdx.x) * chunk;
+    const int64_t end = begin + chunk < count ? begin + chunk : count;
+    const float total = range_sum<T, kVec, kDefaultBlockSize, kStage1Unroll>(x, begin, end, slot);
     if (threadIdx.x == 0) partial[blockIdx.x] = total;
+}
+
+/// Inputs of at most kSingleLaunchBytes: one workgroup sums all of x and
+/// writes (or adds into) *out - one launch instead of two. 16 loads in
+/// flight per lane cover the largest such input in one round trip.
+constexpr int kSingleThreads = 1024;
+constexpr int kSingleUnroll = 16;
+constexpr int64_t kSingleLaunchBytes = 256 * 1024;
+static_assert(kSingleLaunchBytes == int64_t{kSingleThreads} * kSingleUnroll * 16,
+              "one round of loads covers a single-launch input");
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(kSingleThreads) void sum_single_kernel(const T* __restrict__ x, int64_t count,
+                                                                    float* __restrict__ out, int accumulate) {
+    __shared__ float slot[kSingleThreads / kWaveSize];
+    const float total = range_sum<T, kVec, kSingleThreads, kSingleUnroll>(x, 0, count, slot);
+    if (threadIdx.x == 0) *out = accumulate ? *out + total : total;
 }
 
 __global__ __launch_bounds__(kStage2Threads) void sum_stage2_kernel(
@@ -148,6 +183,16 @@ template <typename T>
 cf_status launch_sum(const void* x, float* out, int64_t count, void* workspace,
                      int accumulate, hipStream_t stream) {
     constexpr int kPer = Storage<T>::kPerVec;
+    if (count * static_cast<int64_t>(sizeof(T)) <= kSingleLaunchBytes) {
+        if (host_aligned(x, 16)) {
+            launch(sum_single_kernel<T, true>, dim3(1), dim3(kSingleThreads), 0, stream, static_cast<const T*>(x),
+                   count, out, accumulate);
+        } else {
+            launch(sum_single_kernel<T, false>, dim3(1), dim3(kSingleThreads), 0, stream, static_cast<const T*>(x),
+                   count, out, accumulate);
+        }
+        return check_launch("launching reduce_sum", stream);
+    }
     const int64_t partials = partial_count(count);
     // Chunk rounded up to whole workgroup strides so every vector stays aligned.
     const int64_t stride = static_cast<int64_t>(kDefaultBlockSize) * kPer;

@@ -53,6 +53,12 @@ LaunchEvents take_launch_events() {
     return events;
 }
 
+LaunchEvents next_launch_events() {
+    const LaunchEvents events = g_launch_events;
+    g_launch_events.start = nullptr;
+    return events;
+}
+
 bool launch_events_armed() {
     return g_launch_events.start != nullptr || g_launch_events.stop != nullptr;
 }

@@ -18,8 +18,13 @@
 // storage types (bf16 logits -> fp32 probabilities) and may alias when equal:
 // a wave reads its whole row before it writes any of it.
 //
-// Fallback: long rows, unaligned pointers or ragged widths use a workgroup per
-// row with three passes over the row (max, sum, normalise).
+// Rows too long for one wave's registers (more than 1024 16-byte vectors: fp32
+// rows past 4096 columns, 16-bit rows past 8192) take a workgroup of 1024
+// threads per row, the row again in registers (up to 8 vectors per thread),
+// with the two reductions across the workgroup through LDS.
+//
+// Fallback: longer rows, unaligned pointers or ragged widths use a workgroup
+// per row with three passes over the row (max, sum, normalise).
 //
 // cf_softmax_scaled is the same kernel on scale * x with an optional causal
 // mask (column c of row r hidden when c > r mod period): the attention-score
@@ -183,6 +188,99 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
     }
 }
 
+/// One workgroup of kRowThreads threads per row (grid-stride over rows), the
+/// row in registers: thread t holds vectors t, t + kRowThreads, ... of it.
+/// Every thread reads its vectors before the first reduction's barrier, so
+/// x and y may alias.
+constexpr int kRowThreads = 1024;
+
+template <typename Tin, typename Tout, int kVecs, bool kFullCols, bool kMasked>
+__global__ __launch_bounds__(kRowThreads) void softmax_row_kernel(const Tin* x, Tout* y, int64_t rows,
+                                                                  int64_t cols, Masking mask) {
+    constexpr int kPer = Storage<Tin>::kPerVec;
+    __shared__ float slot[kRowThreads / kWaveSize];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int64_t vec_cols = cols / kPer;
+    const float neg_inf = -__builtin_inff();
+    // kMasked: x spans fewer than 2^31 bytes (checked on the host).
+    const __amdgpu_buffer_rsrc_t xbuf =
+        make_buffer(x, kMasked ? static_cast<uint32_t>(rows * cols * sizeof(Tin)) : 0u);
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const int visible = kMasked ? last_visible32(mask, row, cols) : 0;
+        uint4 raw[kVecs];
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t idx = static_cast<int64_t>(j) * kRowThreads + tid;
+            const int64_t ic = kFullCols || idx < vec_cols ? idx : vec_cols - 1;
+            if constexpr (kMasked) {
+                const bool read = static_cast<int>(ic) * kPer <= visible;
+                raw[j] = buffer_load_stream16(
+                    xbuf, read ? static_cast<uint32_t>((row * cols + ic * kPer) * sizeof(Tin)) : 0x80000000u);
+            } else {
+                raw[j] = load_stream16(x + row * cols + ic * kPer);
+            }
+        }
+        float v[kVecs][kPer];
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t idx = static_cast<int64_t>(j) * kRowThreads + tid;
+            if (kFullCols || idx < vec_cols) {
+                unpack16<Tin>(raw[j], v[j]);
+                if constexpr (kMasked) {
+                    const int first = static_cast<int>(idx) * kPer;
+#pragma unroll
+                    for (int i = 0; i < kPer; ++i) v[j][i] = first + i <= visible ? mask.scale * v[j][i] : neg_inf;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) v[j][i] = neg_inf;
+            }
+        }
+        float local_max = neg_inf;
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) local_max = fmaxf(local_max, v[j][i]);
+        }
+        const float row_max = block_reduce_f32<kRowThreads / kWaveSize, MaxF32>(local_max, slot);
+        float partial[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                v[j][i] = __expf(v[j][i] - row_max);
+                partial[i & 1] += v[j][i];
+            }
+        }
+        const float inv_sum =
+            1.0f / block_reduce_f32<kRowThreads / kWaveSize, AddF32>(partial[0] + partial[1], slot);
+#pragma unroll
+        for (int j = 0; j < kVecs; ++j) {
+            const int64_t idx = static_cast<int64_t>(j) * kRowThreads + tid;
+            if (kFullCols || idx < vec_cols) {
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) v[j][i] = v[j][i] * inv_sum;
+                store_vec<Tout, kPer>(y + row * cols + idx * kPer, v[j]);
+            }
+        }
+    }
+}
+
+template <typename Tin, typename Tout, int kVecs, bool kMasked>
+void launch_row(const void* x, void* y, int64_t rows, int64_t cols, const Masking& mask, hipStream_t stream) {
+    const bool full = cols / Storage<Tin>::kPerVec == static_cast<int64_t>(kVecs) * kRowThreads;
+    const unsigned grid = static_cast<unsigned>(rows < (1 << 20) ? rows : (1 << 20));
+    const auto* xin = static_cast<const Tin*>(x);
+    auto* out = static_cast<Tout*>(y);
+    if (full) {
+        launch(softmax_row_kernel<Tin, Tout, kVecs, true, kMasked>, dim3(grid), dim3(kRowThreads), 0, stream, xin,
+               out, rows, cols, mask);
+    } else {
+        launch(softmax_row_kernel<Tin, Tout, kVecs, false, kMasked>, dim3(grid), dim3(kRowThreads), 0, stream, xin,
+               out, rows, cols, mask);
+    }
+}
+
 /// Any shape: one workgroup per row, three passes.
 template <typename Tin, typename Tout, bool kMasked>
 __global__ __launch_bounds__(kDefaultBlockSize) void softmax_block_kernel(const Tin* x, Tout* y,
@@ -276,6 +374,15 @@ cf_status dispatch(const void* x, void* y, int64_t rows, int64_t cols, const Mas
             launch_wave<Tin, Tout, 8, kMasked>(x, y, rows, cols, mask, stream);
         } else {
             launch_wave<Tin, Tout, 16, kMasked>(x, y, rows, cols, mask, stream);
+        }
+    } else if (vec && vectors_per_lane <= 8 * kRowThreads / kWaveSize) {
+        const int64_t per_thread = ceil_div<int64_t>(cols / kPer, kRowThreads);
+        if (per_thread <= 2) {
+            launch_row<Tin, Tout, 2, kMasked>(x, y, rows, cols, mask, stream);
+        } else if (per_thread <= 4) {
+            launch_row<Tin, Tout, 4, kMasked>(x, y, rows, cols, mask, stream);
+        } else {
+            launch_row<Tin, Tout, 8, kMasked>(x, y, rows, cols, mask, stream);
         }
     } else {
         const int64_t max_blocks = static_cast<int64_t>(cu_count()) * 8;

@@ -412,18 +412,19 @@ cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream)
  * the kernels that move them. */
 cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int divisor, void* stream);
 
-/* Arms the calling thread's next kernel launch made by this library: that
- * dispatch records its own start and completion timestamps on `start_event`
- * and `stop_event` (hipEvent_t, created by the caller with timing enabled), so
- * hipEventElapsedTime(start, stop) is the kernel's execution time as a kernel
+/* Arms the calling thread's next operator call into this library: its
+ * kernel dispatches record their own timestamps on `start_event` and
+ * `stop_event` (hipEvent_t, created by the caller with timing enabled), so
+ * hipEventElapsedTime(start, stop) is the kernel execution time as a kernel
  * trace reports it, without the queue packets of an event pair recorded around
  * the call. Every kernel of the library launches through this hook; for an
  * entry point that launches several kernels (the two-stage sum, the adapter
- * backward, split-K matmuls, context-split paged attention) the first one is
- * timed. The events belong to the next operator entry point the thread
- * calls: one that returns without launching (empty input, an invalid
- * argument, an unsupported shape) disarms them, so they never time a later,
- * unrelated launch. Runtime calls (scheduler, pools) leave them armed. Both
+ * backward, split-K matmuls and LoRA, context-split paged attention) the
+ * interval runs from the first kernel's start to the last one's completion,
+ * the gaps between them included. The events belong to the next operator
+ * entry point the thread calls: one that returns without launching (empty
+ * input, an invalid argument, an unsupported shape) disarms them, so they
+ * never time a later, unrelated launch. Runtime calls (scheduler, pools) leave them armed. Both
  * NULL disarms. It has no counterpart in the reference, whose benchmarks
  * bracket each launch with an event pair (benchmarks/benchmark_kernels.cu:59-79). */
 cf_status cf_time_next_launch(void* start_event, void* stop_event);

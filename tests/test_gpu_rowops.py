@@ -369,6 +369,38 @@ def test_softmax_two_rows_per_wave(dtype, shape):
     assert_close(y[picked], oracle.softmax(g.host_values(x[picked], dtype)), dtype, f"softmax {dtype} {shape}")
 
 
+@pytest.mark.parametrize(
+    "in_dtype,out_dtype,shape",
+    [
+        ("f32", "f32", (128, 8192)),     # the reference's benchmark shape (README.md:420-431): 2 vectors per thread
+        ("f32", "f32", (7, 4100)),       # 1025 vectors: just past one wave's registers, ragged
+        ("f32", "f32", (3, 12000)),      # 4 vectors per thread, ragged
+        ("f32", "f32", (2, 32772)),      # 8193 vectors: past the workgroup kernel, three-pass fallback
+        ("bf16", "bf16", (5, 65536)),    # 8 vectors per thread, full
+        ("bf16", "f32", (6, 16384)),     # bf16 logits to fp32 probabilities
+        ("f16", "f16", (4, 20000)),      # ragged 16-bit row
+    ],
+    ids=str,
+)
+def test_softmax_long_rows(in_dtype, out_dtype, shape):
+    """Rows longer than one wave's registers take a 1024-thread workgroup per
+    row with the row in registers (up to 8 16-byte vectors per thread); past
+    that, the three-pass kernel. Both against the float64 oracle, the
+    workgroup kernel in place and causally masked too."""
+    rows, cols = shape
+    g.announce(f"softmax long rows {in_dtype}->{out_dtype} {shape}")
+    x = g.storage_bits((rng(rows * 7 + cols).standard_normal(shape) * 4).astype(np.float32), in_dtype)
+    xv = g.host_values(x, in_dtype)
+    assert_close(run_softmax(x, in_dtype, out_dtype), oracle.softmax(xv), out_dtype, f"softmax {shape}")
+    if in_dtype == out_dtype:
+        assert_close(run_softmax_scaled(x, in_dtype, in_dtype, 1.0, 0, in_place=True), oracle.softmax(xv), in_dtype,
+                     f"in place {shape}")
+    period = max(rows // 2, 1) if rows > 4 else cols
+    z = masked_logits(xv, 0.125, period)
+    assert_close(run_softmax_scaled(x, in_dtype, out_dtype, 0.125, period), oracle.softmax(z), out_dtype,
+                 f"causal period {period} {shape}")
+
+
 def test_softmax_in_place():
     x = rng(10).standard_normal((16, 1024)).astype(np.float32)
     xg = g.to_gpu(x)
@@ -413,6 +445,30 @@ def test_sum_accumulates_when_asked_and_handles_bf16():
     xb = oracle.f32_to_bf16_bits(rng(12).standard_normal(50_000).astype(np.float32))
     exact = oracle.sum_exact(g.host_values(xb, "bf16"))
     assert abs(run_sum(xb, "bf16") - exact) <= max(abs(exact), 1.0) * 1e-5 * math.sqrt(50_000)
+
+
+@pytest.mark.parametrize("dtype,n", [("f32", 65536), ("f32", 65537), ("bf16", 131072), ("bf16", 131073),
+                                     ("f16", 131071)], ids=str)
+def test_sum_around_the_single_launch_boundary(dtype, n):
+    """Inputs of at most 256 KiB are summed by one workgroup in one launch,
+    larger ones by the two-stage tree: both within the sqrt(n) bound of the
+    exact sum, deterministic, accumulating when asked, and misaligned input
+    (scalar loads) too."""
+    g.announce(f"sum {dtype} n={n}")
+    x = g.storage_bits(rng(n).standard_normal(n).astype(np.float32), dtype)
+    exact = oracle.sum_exact(g.host_values(x, dtype))
+    got = run_sum(x, dtype)
+    assert abs(got - exact) <= max(abs(exact), 1.0) * 1e-5 * math.sqrt(n)
+    assert run_sum(x, dtype) == got
+    assert abs(run_sum(x, dtype, accumulate_onto=100.0) - (exact + 100.0)) <= max(abs(exact), 1.0) * 1e-5 * math.sqrt(n)
+    padded = np.concatenate([x[:1], x])
+    xg = g.to_gpu(padded, dtype)
+    out = torch.zeros(1, device=g.DEVICE)
+    ws = g.empty(max(1, g.lib().cf_reduce_sum_workspace_bytes(n)), torch.uint8)
+    g.call("cf_reduce_sum", xg.data_ptr() + xg.element_size(), g.cf(dtype), out.data_ptr(), n, ws.data_ptr(),
+           ws.numel(), 0, g.stream())
+    torch.cuda.synchronize()
+    assert abs(float(out.item()) - exact) <= max(abs(exact), 1.0) * 1e-5 * math.sqrt(n)
 
 
 def test_an_empty_sum_leaves_the_output_untouched():

@@ -1,7 +1,8 @@
 """Dispatch timing (cf_time_next_launch): a timed launch computes the same
 result as an untimed one, its elapsed time is the kernel's own (positive, and
-no longer than an event pair recorded around the same launch), and only the
-next launch on the thread is timed."""
+no longer than an event pair recorded around the same launch), an entry point
+of two kernels is timed from the first one's start to the second one's end,
+and only the next operator call on the thread is timed."""
 
 from __future__ import annotations
 
@@ -42,6 +43,39 @@ def test_timed_launch_matches_untimed_and_is_the_kernel_time():
     timer.close()
     assert torch.equal(plain.view(torch.int16), timed.view(torch.int16))
     assert 0.0 < kernel_ms <= around_ms * 1.02 + 1e-3, (kernel_ms, around_ms)
+
+
+def test_an_entry_point_of_two_kernels_is_timed_whole():
+    """The two-stage sum launches two kernels: the armed interval runs from the
+    first one's start to the second one's end, inside an event pair around the
+    call, and the result is the untimed one's."""
+    print("case: dispatch timer on the two-stage sum of 16M fp32", flush=True)
+    n = 1 << 24
+    x = torch.randn(n, generator=torch.Generator(device="cuda").manual_seed(3), device="cuda")
+    nbytes = _lib.load().cf_reduce_sum_workspace_bytes(n)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    outs = [torch.empty(1, device="cuda") for _ in range(2)]
+
+    def run(out):
+        call("cf_reduce_sum", x.data_ptr(), _lib.CF_F32, out.data_ptr(), n, ws.data_ptr(), nbytes, 0, stream())
+
+    for _ in range(3):
+        run(outs[0])
+    torch.cuda.synchronize()
+    timer = _lib.DispatchTimer()
+    pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    pair[0].record()
+    timer.arm()
+    run(outs[1])
+    pair[1].record()
+    torch.cuda.synchronize()
+    kernel_ms = timer.elapsed_ms()
+    around_ms = pair[0].elapsed_time(pair[1])
+    timer.close()
+    assert torch.equal(outs[0], outs[1])
+    # 64 MiB at no more than 8 TB/s: at least 8 us of stage 1 alone.
+    assert 0.008 <= kernel_ms <= around_ms * 1.02 + 1e-3, (kernel_ms, around_ms)
+    assert _lib.load().cf_time_next_launch_armed() == 0
 
 
 def test_only_the_next_launch_is_timed():
