@@ -10,15 +10,18 @@
 //
 // The work is two reductions over M of HBM-sized operands, so the design
 // reads dy once and x once (the HBM floor) and keeps everything else small:
-//   1. One pass over dy in 256 x 256 tiles (Mp = M rounded up to 256): each
-//      64-row chunk goes HBM -> registers -> LDS; G partial rows = chunk @
+//   1. One pass over dy in 512-row x 256-column tiles (Mp = M rounded up to
+//      512), two 64-row chunks in flight per workgroup: each chunk goes
+//      HBM -> registers -> LDS; G partial rows = chunk @
 //      b^T (16x16x32 MFMA, row fragments by ds_read_b128, b fragments held in
 //      registers) and grad_b partials += bf16(xa)^T-chunk @ chunk (16x16x32
 //      MFMA; the chunk's fp32 xa arrives with one 16-byte load per thread
 //      and is rounded and transposed into LDS, the m-contiguous operand is
 //      read by ds_read_b64_tr_b16). Partials
 //      go to fp32 workspaces, one slice per 256-column tile (G) and per
-//      256-row tile (grad_b).
+//      512-row tile (grad_b). 512-row tiles halve the grad_b/grad_a partials
+//      of 256-row ones (37.8 against 39.5 us at 8192 x 4096 x 4096 r16,
+//      operands cache-cold); three or four chunks in flight were slower.
 //   2. One launch sums both in a fixed order: grad_b (times scale, cast) and
 //      G -> GT (bf16 [16, Mp]).
 //   3. The same column-reduction pass over x with GT: grad_a partials.
@@ -37,9 +40,10 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
-constexpr int kTileRows = 256;   // rows (M) per workgroup
+constexpr int kTileRows = 512;   // rows (M) per workgroup
 constexpr int kTileCols = 256;   // columns per workgroup
 constexpr int kChunkRows = 64;   // rows staged in LDS at a time
+constexpr int kInFlight = 2;     // chunks loaded ahead per workgroup
 constexpr int kThreads = 256;
 constexpr int kRankPad = 16;     // adapter rank padded to one MFMA dimension
 constexpr int kRowBytes = kTileCols * 2;
@@ -89,7 +93,7 @@ struct ColumnArgs {
     int64_t rank;
 };
 
-/// One 256-row x 256-column tile of v: colpart[tile row][j][n] =
+/// One kTileRows x 256-column tile of v: colpart[tile row][j][n] =
 /// sum_m pt[j, m] * v[m, n] over the tile's rows; with kRowDot also
 /// gpart[tile column][m][j] = sum_n v[m, n] * b[j, n] over its columns.
 template <bool kRowDot>
@@ -118,11 +122,20 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
     const int piece_chunk = tid & 31;
     const int64_t piece_col = n0 + 8 * piece_chunk;
     const bool col_ok = piece_col < C;
-    uint4 staged[kPiecesPerThread];
+    // kInFlight chunks in flight: slot s of each staging array holds chunk c
+    // with c % kInFlight == s (the chunk loop below is unrolled, so slots are
+    // registers).
+    uint4 staged[kInFlight][kPiecesPerThread];
     // dy pass: thread t also loads bytes 16 t .. +15 of the chunk's xa rows
     // (64 x rank fp32, contiguous), i.e. flat elements 4 t .. 4 t + 3:
     // element q is xa[row0 + xa_row[q]][xa_col[q]].
-    uint4 staged_xa = make_uint4(0u, 0u, 0u, 0u);
+    uint4 staged_xa[kInFlight];
+#pragma unroll
+    for (int s = 0; s < kInFlight; ++s) staged_xa[s] = make_uint4(0u, 0u, 0u, 0u);
+    // x pass: the chunk's pt fragments, pt[j = lane % 16][row0 + 32 ms +
+    // 8 (lane / 16) .. +7], loaded with the chunk so that waiting for them
+    // never waits for a later chunk's loads.
+    bf16x8_t staged_pt[kInFlight][2];
     int xa_row[4];
     int xa_col[4];
     if constexpr (kRowDot) {
@@ -138,13 +151,15 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
     }
     const __amdgpu_buffer_rsrc_t xabuf = make_buffer(
         args.xa, static_cast<uint32_t>(kRowDot ? args.M * args.rank * 4 : 0));
-    auto load_chunk = [&](int64_t row0) {
+    const __amdgpu_buffer_rsrc_t ptbuf =
+        make_buffer(args.pt, static_cast<uint32_t>(kRowDot ? 0 : kRankPad * args.Mp * 2));
+    auto load_chunk = [&](int slot, int64_t row0) {
 #pragma unroll
         for (int i = 0; i < kPiecesPerThread; ++i) {
             const int64_t row = row0 + 8 * i + (tid >> 5);
             const uint32_t off =
                 col_ok ? static_cast<uint32_t>((row * C + piece_col) * 2) : kOutOfRange;
-            staged[i] = buffer_load16(vbuf, off, 0);
+            staged[slot][i] = buffer_load16(vbuf, off, 0);
         }
         if constexpr (kRowDot) {
             // Past the chunk's kChunkRows x rank elements (rank < 16), or past
@@ -152,18 +167,25 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
             const uint32_t off = 4 * tid < kChunkRows * args.rank
                                      ? static_cast<uint32_t>((row0 * args.rank + 4 * tid) * 4)
                                      : kOutOfRange;
-            staged_xa = buffer_load16(xabuf, off, 0);
+            staged_xa[slot] = buffer_load16(xabuf, off, 0);
+        } else {
+#pragma unroll
+            for (int ms = 0; ms < 2; ++ms) {
+                const uint32_t off = static_cast<uint32_t>((jl * args.Mp + row0 + 32 * ms + 8 * g) * 2);
+                staged_pt[slot][ms] = as_bf16x8(buffer_load16(ptbuf, off, 0));
+            }
         }
     };
-    auto store_chunk = [&]() {
+    auto store_chunk = [&](int slot) {
 #pragma unroll
         for (int i = 0; i < kPiecesPerThread; ++i) {
             const int row = 8 * i + (tid >> 5);
-            *reinterpret_cast<uint4*>(tile + tile_offset(row, piece_chunk)) = staged[i];
+            *reinterpret_cast<uint4*>(tile + tile_offset(row, piece_chunk)) = staged[slot][i];
         }
         if constexpr (kRowDot) {
             if (4 * tid < kChunkRows * args.rank) {
-                const uint32_t v[4] = {staged_xa.x, staged_xa.y, staged_xa.z, staged_xa.w};
+                const uint32_t v[4] = {staged_xa[slot].x, staged_xa[slot].y, staged_xa[slot].z,
+                                       staged_xa[slot].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     xat[xa_col[q]][xa_row[q]] = static_cast<uint16_t>(f32_to_bf16_bits(__uint_as_float(v[q])));
@@ -194,33 +216,32 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
     f32x4_t acc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const __amdgpu_buffer_rsrc_t ptbuf =
-        make_buffer(kRowDot ? static_cast<const void*>(args.xa) : static_cast<const void*>(args.pt),
-                    static_cast<uint32_t>(kRowDot ? args.M * args.rank * 4 : kRankPad * args.Mp * 2));
 
-    load_chunk(m0);
-    for (int chunk = 0; chunk < kTileRows / kChunkRows; ++chunk) {
+    constexpr int kChunks = kTileRows / kChunkRows;
+#pragma unroll
+    for (int c = 0; c < kInFlight && c < kChunks; ++c) load_chunk(c, m0 + c * kChunkRows);
+#pragma unroll
+    for (int chunk = 0; chunk < kChunks; ++chunk) {
+        const int slot = chunk % kInFlight;
         const int64_t row0 = m0 + static_cast<int64_t>(chunk) * kChunkRows;
         __syncthreads();  // previous chunk's readers are done
-        store_chunk();
+        store_chunk(slot);
         __syncthreads();
-        if (chunk + 1 < kTileRows / kChunkRows) load_chunk(row0 + kChunkRows);
 
-        // pt fragments: pt[j = lane % 16][row0 + 32 ms + 8 (lane / 16) .. +7].
-        // The dy pass reads them from the transposed bf16 copy of the chunk's
-        // xa in LDS (rounded as the transposed copy of the x pass is); rows
-        // past M and columns past the rank are zero.
+        // pt fragments. The dy pass reads them from the transposed bf16 copy
+        // of the chunk's xa in LDS (rounded as the transposed copy of the x
+        // pass is); rows past M and columns past the rank are zero.
         bf16x8_t ptfrag[2];
 #pragma unroll
         for (int ms = 0; ms < 2; ++ms) {
             if constexpr (kRowDot) {
                 ptfrag[ms] = *reinterpret_cast<const bf16x8_t*>(&xat[jl][32 * ms + 8 * g]);
             } else {
-                const uint32_t off =
-                    static_cast<uint32_t>((jl * args.Mp + row0 + 32 * ms + 8 * g) * 2);
-                ptfrag[ms] = as_bf16x8(buffer_load16(ptbuf, off, 0));
+                ptfrag[ms] = staged_pt[slot][ms];
             }
         }
+        if (chunk + kInFlight < kChunks) load_chunk(slot, row0 + kInFlight * kChunkRows);
+
 #pragma unroll
         for (int ms = 0; ms < 2; ++ms) {
 #pragma unroll
