@@ -73,7 +73,7 @@ class ExtensionMissingError(RuntimeError):
 
 @dataclass(frozen=True)
 class BackendReport:
-    """Why a particular implementation is being used."""
+    """Which backend serves GPU calls here, and the facts that decided it."""
 
     extension_loaded: bool
     cuda_compiled: bool
@@ -232,7 +232,7 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.T
 
 
 def softmax(x: torch.Tensor) -> torch.Tensor:
-    """Numerically stable softmax over the last dimension."""
+    """Row softmax over the last dimension (max-subtracted, fp32 arithmetic)."""
     if x.numel() == 0:
         return x.clone()
     x = x.contiguous()
@@ -306,14 +306,13 @@ def lora_linear(
     lora_b: torch.Tensor,
     scale: float = 1.0,
 ) -> torch.Tensor:
-    """LoRA-adapted linear layer: ``x @ weight + scale * (x @ lora_a) @ lora_b``.
+    """``y = x @ weight + scale * (x @ lora_a) @ lora_b`` (operator layout).
 
-    Args:
-        x: ``[batch, in_features]``
-        weight: ``[in_features, out_features]``, the frozen base weight.
-        lora_a: ``[in_features, rank]``
-        lora_b: ``[rank, out_features]``
-        scale: usually ``alpha / rank``.
+    Shapes, with M rows, K input and N output features and adapter rank r:
+    ``x`` is ``[M, K]``; the frozen ``weight`` is ``[K, N]`` (columns are output
+    features); the down-projection ``lora_a`` is ``[K, r]`` and the
+    up-projection ``lora_b`` is ``[r, N]``. ``scale`` multiplies the adapter
+    term only; LoRA training sets it to alpha / r.
 
     A PEFT-layout layer (W ``[out, in]``, A ``[r, in]``, B ``[out, r]``) maps to
     ``lora_linear(x, W.t().contiguous(), A.t().contiguous(), B.t().contiguous(), alpha / r)``.
@@ -355,12 +354,11 @@ def lora_linear(
 def fused_residual_rmsnorm(
     x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Residual add followed by RMSNorm in one pass.
+    """``h = x + residual``, then RMSNorm of ``h``, both from one pass.
 
-    Returns ``(rmsnorm(x + residual), x + residual)``.
-
-    Raises:
-        ValueError: if the shapes disagree.
+    Returns ``(rmsnorm(h, weight, eps), h)``; a ``ValueError`` is raised when
+    ``x`` and ``residual`` differ in shape or ``weight`` does not match their
+    last dimension.
     """
     if x.shape != residual.shape:
         raise ValueError(
@@ -410,10 +408,10 @@ def gelu(x: torch.Tensor) -> torch.Tensor:
 
 
 def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
-    """SwiGLU: ``silu(gate) * up``, fp32 arithmetic for half inputs.
+    """``silu(gate) * up`` elementwise (fp32 arithmetic for 16-bit inputs).
 
-    Raises:
-        ValueError: if the shapes or dtypes differ.
+    ``gate`` and ``up`` must agree in shape and dtype; otherwise a
+    ``ValueError`` is raised before anything runs.
     """
     if gate.shape != up.shape:
         raise ValueError(
