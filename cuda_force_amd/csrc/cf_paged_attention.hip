@@ -11,9 +11,12 @@
 //
 // Design on gfx950 (HBM-bound: every K and V element of a context is read once
 // per KV head, 2 * context * D * sizeof(T) bytes per (sequence, KV head)):
-//   * One workgroup (4 waves) per (sequence, KV head, group of up to 8 query
-//     heads, context split): all query heads of a GQA group are served from
+//   * One workgroup (4 waves) per (sequence, KV head, group of up to 4 query
+//     heads, context split): the query heads of a GQA group are served from
 //     one pass over K and V, instead of re-reading the KV head per query head.
+//     Larger groups take several workgroups per KV head (each reads K and V;
+//     the per-head state of 8 heads held the kernel to 2 waves per SIMD and
+//     ran slower: group 8 fp32 32 -> 36%, bf16 25 -> 29% of HBM peak).
 //   * A token's K (and V) row is read by D/4 lanes (fp32) or D/8 lanes (bf16),
 //     16 bytes each, several tokens per wave instruction: whole rows,
 //     coalesced. Each lane keeps its 4 (8) query values and output
@@ -41,7 +44,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWaveSize;
-constexpr int kMaxGroup = 8;          // query heads per workgroup
+constexpr int kMaxGroup = 4;          // query heads per workgroup
 constexpr int kMinSplitTokens = 256;  // tokens per split, at least
 constexpr int kTargetWorkgroups = 1024;
 
@@ -143,24 +146,24 @@ __device__ __forceinline__ void merge_into(HeadState<kVals>& s, float m2, float 
 /// kLanes = D / kVals lanes per token (kVals = 16 bytes of T), kGroup query
 /// heads per workgroup.
 ///
-/// 16-bit caches with up to 4 query heads per group are held to 128 VGPRs (4
-/// waves per SIMD instead of 3; 2-8 registers spill): at the usual grids
-/// (1024-2048 workgroups of 4 waves) every workgroup is then resident at
-/// once instead of leaving a second partial round, and each wave's short
-/// token range no longer waits on the previous round. Measured on bf16
-/// D = 128: GQA group 4 41.5 -> 50.0% and 38.8 -> 45.3% of HBM peak (64 x
-/// 1024 and 128 x 256 tokens), group 2 55.4 -> 61.3%, group 1 unchanged;
-/// group 8 (168 VGPRs) fell from 24.7 to 8.5% when forced, so it keeps the
-/// compiler's choice, as does fp32.
+/// 16-bit caches are held to 128 VGPRs (4 waves per SIMD instead of 3; up
+/// to 2 registers spill): at the usual grids (1024-2048 workgroups of 4
+/// waves) every workgroup is then resident at once instead of leaving a
+/// second partial round, and each wave's short token range no longer waits
+/// on the previous round. Measured on bf16 D = 128: GQA group 4 41.5 ->
+/// 50.0% and 38.8 -> 45.3% of HBM peak (64 x 1024 and 128 x 256 tokens),
+/// group 1 unchanged. fp32 keeps the compiler's choice (4-6 waves).
 template <typename T, int kLanes, int kGroup>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && kGroup <= 4 ? 4 : 1, 8))) void paged_decode_kernel(PagedArgs a) {
+__attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 4 : 1, 8))) void paged_decode_kernel(PagedArgs a) {
     constexpr int kVals = vals_per_lane<T>();
     constexpr int kTokensPerStep = kWaveSize / kLanes;
     constexpr int kDim = kVals * kLanes;
-    // Token steps whose loads are issued together: fewer for larger head
-    // groups, whose per-head state already takes the registers.
-    constexpr int kStepsPerLoad = kGroup <= 2 ? 4 : (kGroup == 4 ? 2 : 1);
+    // Token steps whose loads are issued together (two buffers of them in
+    // flight). Two rather than four for groups of one or two heads: the
+    // staging registers then leave room for 4-6 waves per SIMD (fp32 GQA
+    // group 2: 59 -> 74% of HBM peak; group 1 unchanged).
+    constexpr int kStepsPerLoad = 2;
     constexpr int kChunk = kStepsPerLoad * kTokensPerStep;  // tokens per load batch
     __shared__ float lds_m[kWaves][kGroup];
     __shared__ float lds_l[kWaves][kGroup];
@@ -551,8 +554,7 @@ void launch_streaming(const PagedArgs& args, int gs, int64_t workgroups, hipStre
     switch (gs) {
         case 1: launch(paged_decode_kernel<T, kLanes, 1>, dim3(grid), dim3(kThreads), 0, stream, args); break;
         case 2: launch(paged_decode_kernel<T, kLanes, 2>, dim3(grid), dim3(kThreads), 0, stream, args); break;
-        case 4: launch(paged_decode_kernel<T, kLanes, 4>, dim3(grid), dim3(kThreads), 0, stream, args); break;
-        default: launch(paged_decode_kernel<T, kLanes, 8>, dim3(grid), dim3(kThreads), 0, stream, args); break;
+        default: launch(paged_decode_kernel<T, kLanes, 4>, dim3(grid), dim3(kThreads), 0, stream, args); break;
     }
 }
 
