@@ -496,6 +496,243 @@ __global__ __launch_bounds__(kWaveSize) void paged_decode_wide_kernel(PagedArgs 
     }
 }
 
+/// 16-bit caches on the matrix cores: one workgroup (4 waves) per (sequence,
+/// KV head, context split) serves every query head of the GQA group (up to
+/// kMfmaHeads). Each wave takes chunks of 16 tokens (chunks wave, wave + 4,
+/// ... of the split) and, per chunk, computes
+///   S^T [16 tokens x 16 heads] = K [16 x D] Q^T [D x 16]
+/// with D / 32 v_mfma_f32_16x16x32_bf16: the A fragments are the tokens' K
+/// rows straight from memory (lane j % 16 = token, 16 bytes of dims), Q^T
+/// stays in registers, and lane (g = lane / 16, j = lane % 16) receives the
+/// scores of tokens 4 g .. 4 g + 3 for head j. After the online-softmax
+/// update of head j (one cross-lane max per chunk),
+///   O^T [D x 16 heads] += V^T [D x 16 tokens] P^T [16 tokens x 16 heads]
+/// with D / 16 v_mfma_f32_16x16x16_bf16: the B operand is the lane's own four
+/// probabilities as bf16 (exactly the score layout), the A operand is V^T
+/// read transposed (ds_read_b64_tr_b16) out of a per-wave LDS copy of the
+/// chunk's V rows. The next chunk's K and V loads are in flight while a chunk
+/// is computed. The 4 waves' states merge through LDS at the end.
+constexpr int kMfmaHeads = 16;
+constexpr int kMfmaChunk = 16;
+
+typedef __bf16 bf16x8_m __attribute__((ext_vector_type(8)));
+typedef short s16x4_m __attribute__((ext_vector_type(4)));
+typedef float f32x4_m __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_m lds_s16x4_m;
+typedef __attribute__((address_space(3))) uint8_t lds_u8_m;
+
+template <int kD>
+__global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
+    constexpr int kS = kD / 32;                             // score MFMAs per chunk
+    constexpr int kB = kD / 16;                             // P.V MFMAs (output blocks)
+    constexpr int kRowBytes = kD * 2;                       // one token's K or V row
+    constexpr int kPiecesPerRow = kRowBytes / 16;
+    constexpr int kVPieces = kMfmaChunk * kPiecesPerRow / kWaveSize;  // V 16-byte pieces per lane
+    constexpr int kVBytes = kMfmaChunk * kRowBytes;         // one wave's V buffer
+    static_assert(kD % 32 == 0 && kD <= 256 && kVPieces >= 1, "head size");
+    // Two V buffers per wave; after the loop the same bytes hold the waves'
+    // output accumulators for the merge ([wave][head][dim] fp32).
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kWaves * 2 * kVBytes];
+    static_assert(kWaves * 2 * kVBytes == kWaves * kMfmaHeads * kD * 4, "merge area");
+    __shared__ float lds_m[kWaves][kMfmaHeads];
+    __shared__ float lds_l[kWaves][kMfmaHeads];
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & (kWaveSize - 1);
+    const int wave = tid / kWaveSize;
+    const int g = lane >> 4;
+    const int j = lane & 15;
+
+    int64_t id = blockIdx.x;
+    const int split = static_cast<int>(id % a.splits);
+    id /= a.splits;
+    const int64_t kv_head = id % a.kv_heads;
+    const int64_t seq = id / a.kv_heads;
+    const int64_t group = a.heads / a.kv_heads;  // <= kMfmaHeads (checked on the host)
+    const int64_t head0 = kv_head * group;
+
+    // Q^T fragments: lane holds q[head j][dims 32 s + 8 g .. +7]; heads past
+    // the group are zero (their scores are never used).
+    bf16x8_m qfrag[kS];
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+        u32x4_t raw = {0u, 0u, 0u, 0u};
+        if (j < group) raw = load16(a.query, ((seq * a.heads + head0 + j) * kD + 32 * s + 8 * g) * 2);
+        qfrag[s] = __builtin_bit_cast(bf16x8_m, raw);
+    }
+
+    const int64_t capacity = a.max_blocks * a.block_size;
+    const int64_t stored = a.context[seq] > 0 ? a.context[seq] : 0;
+    const int64_t context = stored < capacity ? stored : capacity;
+    const int64_t t_lo = static_cast<int64_t>(split) * a.split_tokens;
+    const int64_t t_hi = context < t_lo + a.split_tokens ? context : t_lo + a.split_tokens;
+    const int64_t row_stride = a.kv_heads * kRowBytes;
+    const int64_t head_bytes = kv_head * kRowBytes;
+    const uint32_t* table = a.tables + seq * a.max_blocks;
+
+    // 64 block-table entries in lane registers (a lane shuffle per token).
+    int64_t window_base = 0;
+    int window = 0;
+    auto load_window = [&](int64_t base) {
+        const int64_t entry = base + lane < a.max_blocks ? base + lane : a.max_blocks - 1;
+        window_base = base;
+        window = static_cast<int>(table[entry]);
+    };
+    // Byte offset of token t's row (t < t_hi; the chunk's blocks are in the window).
+    auto row_offset = [&](int64_t t) {
+        const int64_t block =
+            static_cast<uint32_t>(__shfl(window, static_cast<int>(t / a.block_size - window_base)));
+        return (block * a.block_size + t % a.block_size) * row_stride + head_bytes;
+    };
+
+    bf16x8_m kfrag[kS];
+    u32x4_t vraw[kVPieces];
+    // Issue the loads of the chunk starting at c0 (< t_hi). Tokens past t_hi
+    // read the last valid token (their scores are masked).
+    auto fetch = [&](int64_t c0) {
+        const int64_t last = (c0 + kMfmaChunk - 1 < t_hi - 1 ? c0 + kMfmaChunk - 1 : t_hi - 1);
+        if (last / a.block_size - window_base >= kWaveSize || c0 / a.block_size < window_base) {
+            load_window(c0 / a.block_size);
+        }
+        {
+            const int64_t t = c0 + j < t_hi ? c0 + j : t_hi - 1;
+            const int64_t off = row_offset(t);
+#pragma unroll
+            for (int s = 0; s < kS; ++s) kfrag[s] = __builtin_bit_cast(bf16x8_m, load16(a.k_cache, off + (32 * s + 8 * g) * 2));
+        }
+#pragma unroll
+        for (int i = 0; i < kVPieces; ++i) {
+            const int p = lane + kWaveSize * i;
+            const int64_t t0 = c0 + p / kPiecesPerRow;
+            const int64_t t = t0 < t_hi ? t0 : t_hi - 1;
+            vraw[i] = load16(a.v_cache, row_offset(t) + (p % kPiecesPerRow) * 16);
+        }
+    };
+    auto stage_v = [&](int buf) {
+        uint8_t* base = lds + (wave * 2 + buf) * kVBytes;
+#pragma unroll
+        for (int i = 0; i < kVPieces; ++i) {
+            const int p = lane + kWaveSize * i;
+            *reinterpret_cast<u32x4_t*>(base + (p / kPiecesPerRow) * kRowBytes + (p % kPiecesPerRow) * 16) = vraw[i];
+        }
+    };
+
+    float m = -INFINITY;   // running max of head j (the same in all four lane groups)
+    float l = 0.0f;        // this lane's share of head j's running sum (tokens 4 g .. 4 g + 3)
+    f32x4_m acc[kB];       // O^T[dim 16 b + 4 g + t][head j]
+#pragma unroll
+    for (int b = 0; b < kB; ++b) acc[b] = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int64_t first = t_lo + static_cast<int64_t>(wave) * kMfmaChunk;
+    constexpr int64_t kStride = static_cast<int64_t>(kWaves) * kMfmaChunk;
+    int buf = 0;
+    if (first < t_hi) {
+        load_window(first / a.block_size);
+        fetch(first);
+        stage_v(0);
+    }
+    for (int64_t c0 = first; c0 < t_hi; c0 += kStride) {
+        bf16x8_m kcur[kS];
+#pragma unroll
+        for (int s = 0; s < kS; ++s) kcur[s] = kfrag[s];
+        const int64_t next = c0 + kStride;
+        if (next < t_hi) fetch(next);
+
+        f32x4_m sc = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < kS; ++s) sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kcur[s], qfrag[s], sc, 0, 0, 0);
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            sc[t] = c0 + 4 * g + t < t_hi ? sc[t] * a.scale : -INFINITY;
+            cmax = fmaxf(cmax, sc[t]);
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        // Every chunk holds at least one valid token, so cmax is finite.
+        const float m_new = fmaxf(m, cmax);
+        const float c = m == -INFINITY ? 0.0f : __expf(m - m_new);
+        m = m_new;
+        s16x4_m pb;
+        float psum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float pt = sc[t] == -INFINITY ? 0.0f : __expf(sc[t] - m_new);
+            psum += pt;
+            pb[t] = static_cast<short>(f32_to_bf16_bits(pt));
+        }
+        l = l * c + psum;
+#pragma unroll
+        for (int b = 0; b < kB; ++b) acc[b] *= c;
+
+        // V^T fragments: lane (g, j) reads 8 bytes of token row 4 g + j / 4 at
+        // dims 16 b + 4 (j % 4) .. +3 and receives V[tokens 4 g .. 4 g + 3][dim 16 b + j].
+        // This wave's own writes of the buffer must have landed.
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14));
+        asm volatile("" ::: "memory");
+        const uint8_t* vb = lds + (wave * 2 + buf) * kVBytes;
+#pragma unroll
+        for (int b = 0; b < kB; ++b) {
+            const int off = (4 * g + (j >> 2)) * kRowBytes + (16 * b + 4 * (j & 3)) * 2;
+            const s16x4_m vfrag = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4_m*)((lds_u8_m*)(const_cast<uint8_t*>(vb)) + off));
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vfrag, pb, acc[b], 0, 0, 0);
+        }
+        if (next < t_hi) {
+            buf ^= 1;
+            stage_v(buf);
+        }
+    }
+
+    // Head j's sum over the wave's tokens: add the four lane groups.
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+
+    __syncthreads();  // every wave is done with its V buffers
+    float* macc = reinterpret_cast<float*>(lds);  // [wave][head][dim]
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) macc[(wave * kMfmaHeads + j) * kD + 16 * b + 4 * g + t] = acc[b][t];
+    }
+    if (g == 0) {
+        lds_m[wave][j] = m;
+        lds_l[wave][j] = l;
+    }
+    __syncthreads();
+
+    // Merge: thread tid handles (head, dim) pairs tid, tid + kThreads, ...
+    for (int pair = tid; pair < kMfmaHeads * kD; pair += kThreads) {
+        const int h = pair / kD;
+        const int d = pair % kD;
+        if (h >= group) continue;
+        float mm = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, lds_m[w][h]);
+        float ll = 0.0f;
+        float oo = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float cw = lds_m[w][h] == -INFINITY ? 0.0f : __expf(lds_m[w][h] - mm);
+            ll = fmaf(lds_l[w][h], cw, ll);
+            oo = fmaf(macc[(w * kMfmaHeads + h) * kD + d], cw, oo);
+        }
+        const int64_t head = head0 + h;
+        if (a.splits == 1) {
+            const float v = ll > 0.0f ? oo / ll : 0.0f;
+            static_cast<uint16_t*>(a.out)[(seq * a.heads + head) * kD + d] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+        } else {
+            float* part = a.partial + ((seq * a.heads + head) * a.splits + split) * (kD + 2);
+            if (d == 0) {
+                part[0] = mm;
+                part[1] = ll;
+            }
+            part[2 + d] = oo;
+        }
+    }
+}
+
 /// Lanes per token for the streaming kernel (16 bytes per lane), or 0 when D
 /// needs the wide one.
 int lanes_for(int64_t head_dim, int64_t elem_bytes) {
@@ -520,6 +757,9 @@ struct Plan {
     int64_t split_tokens;
 };
 
+/// Plan.lanes value that selects paged_mfma_kernel.
+constexpr int kMfmaPlan = -1;
+
 Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_dim,
               int64_t block_size, int64_t max_blocks, int64_t elem_bytes, bool may_split) {
     Plan p{};
@@ -527,6 +767,16 @@ Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_d
     const int64_t group = heads / kv_heads;
     p.gs = group_size_for(group);
     p.head_groups = static_cast<int>((group + p.gs - 1) / p.gs);
+    // The matrix-core kernel for 16-bit caches with GQA groups of 4 to 16
+    // heads. For one or two heads per KV head the streaming kernel is faster
+    // (bf16 D = 128: MHA 51.6% of HBM peak against 47.5%, group 2 68.7%
+    // against 65.4%); for groups of 4 and 8 the matrix cores are (47.3 ->
+    // 56.5% and 29.8 -> 54.8%).
+    if (elem_bytes == 2 && head_dim % 32 == 0 && head_dim <= 256 && group >= 4 && group <= kMfmaHeads) {
+        p.lanes = kMfmaPlan;
+        p.gs = kMfmaHeads;
+        p.head_groups = 1;
+    }
     const int64_t max_context = max_blocks * block_size;
     p.splits = 1;
     p.split_tokens = max_context > 0 ? max_context : 1;
@@ -577,6 +827,26 @@ void launch_typed(const PagedArgs& args, const Plan& plan, int64_t sequences, hi
         return;
     }
     const int64_t workgroups = sequences * args.kv_heads * plan.head_groups * plan.splits;
+    if constexpr (!std::is_same<T, float>::value) {
+      if (plan.lanes == kMfmaPlan) {
+        const dim3 grid(static_cast<unsigned>(workgroups));
+        switch (args.head_dim / 32) {
+            case 1: launch(paged_mfma_kernel<32>, grid, dim3(kThreads), 0, stream, args); break;
+            case 2: launch(paged_mfma_kernel<64>, grid, dim3(kThreads), 0, stream, args); break;
+            case 3: launch(paged_mfma_kernel<96>, grid, dim3(kThreads), 0, stream, args); break;
+            case 4: launch(paged_mfma_kernel<128>, grid, dim3(kThreads), 0, stream, args); break;
+            case 5: launch(paged_mfma_kernel<160>, grid, dim3(kThreads), 0, stream, args); break;
+            case 6: launch(paged_mfma_kernel<192>, grid, dim3(kThreads), 0, stream, args); break;
+            case 7: launch(paged_mfma_kernel<224>, grid, dim3(kThreads), 0, stream, args); break;
+            default: launch(paged_mfma_kernel<256>, grid, dim3(kThreads), 0, stream, args); break;
+        }
+        if (plan.splits > 1) {
+            launch(paged_combine_kernel<T>, dim3(static_cast<unsigned>(sequences * args.heads)), dim3(kWaveSize), 0,
+                   stream, args);
+        }
+        return;
+      }
+    }
     switch (plan.lanes) {
         case 1: launch_streaming<T, 1>(args, plan.gs, workgroups, stream); break;
         case 2: launch_streaming<T, 2>(args, plan.gs, workgroups, stream); break;

@@ -123,6 +123,44 @@ def test_bf16_cache():
     assert np.abs(got - expected).max() <= 1e-2 * scale
 
 
+@pytest.mark.parametrize(
+    "dims",
+    [
+        (2, 1, 1, 128, 16, [300, 17]),      # MHA: the streaming kernel
+        (2, 4, 2, 64, 16, [33, 0]),         # GQA group 2 (streaming), an empty sequence
+        (3, 8, 2, 128, 16, [200, 17, 1]),   # group 4: the matrix-core kernel
+        (2, 8, 2, 64, 16, [0, 40]),         # group 4, an empty sequence
+        (2, 16, 2, 128, 16, [300, 16]),     # group 8
+        (1, 32, 2, 32, 8, [100]),           # group 16, the widest the matrix-core kernel takes
+        (1, 32, 1, 64, 16, [50]),           # group 32: the streaming kernel
+        (2, 16, 4, 96, 2, [15, 64]),        # group 4, head size 96, two-token blocks
+        (1, 8, 2, 256, 1, [70]),            # group 4, head size 256, one-token blocks (window reloads)
+        (2, 16, 4, 160, 64, [129, 300]),    # group 4, head size 160, 64-token blocks
+        (1, 8, 2, 80, 16, [100]),           # head size 80 (not a multiple of 32): the streaming kernel
+        (1, 16, 2, 128, 16, [1100]),        # a long context: split across workgroups, or not
+    ],
+    ids=str,
+)
+def test_bf16_paths(dims):
+    """bf16 caches: head sizes that are multiples of 32 (up to 256) with GQA
+    groups of 4 to 16 take the matrix-core kernel (scores and P.V on MFMA,
+    probabilities rounded to bf16 for P.V), the rest the streaming kernel;
+    each within 1e-2 of the output scale of the float64 oracle on the same
+    bf16 inputs, with and without the split workspace. An empty sequence
+    gives zeros."""
+    announce(f"paged attention bf16 {dims}")
+    case = make_case(*dims, seed=sum(dims[:5]) + len(dims[5]))
+    expected = expected_for(case, "bf16")
+    scale = np.abs(expected).max()
+    for workspace in (True, False):
+        got = run_gpu(case, "bf16", workspace=workspace)
+        err = np.abs(got - expected).max()
+        assert err <= 1e-2 * scale, f"workspace={workspace}: max err {err:.3e} (scale {scale:.3e})"
+    for s, n in enumerate(dims[5]):
+        if n == 0:
+            assert (got[s] == 0).all()
+
+
 def test_benchmark_sized_batch():
     announce("paged attention 64 seq x 1024 ctx, 32 heads / 8 kv, d128")
     case = make_case(64, 32, 8, 128, 16, [1024] * 64, seed=9, spare=0)
