@@ -521,19 +521,23 @@ typedef float f32x4_m __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_m lds_s16x4_m;
 typedef __attribute__((address_space(3))) uint8_t lds_u8_m;
 
-template <int kD>
+template <int kD, int kSubs>
 __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
-    constexpr int kS = kD / 32;                             // score MFMAs per chunk
-    constexpr int kB = kD / 16;                             // P.V MFMAs (output blocks)
+    // kSubs 16-token sub-chunks per step (one or two): two keep twice the
+    // bytes in flight per wave.
+    constexpr int kTok = kMfmaChunk * kSubs;                // tokens per step
+    constexpr int kS = kD / 32;                             // score MFMAs per sub-chunk
+    constexpr int kB = kD / 16;                             // P.V output blocks
     constexpr int kRowBytes = kD * 2;                       // one token's K or V row
     constexpr int kPiecesPerRow = kRowBytes / 16;
-    constexpr int kVPieces = kMfmaChunk * kPiecesPerRow / kWaveSize;  // V 16-byte pieces per lane
-    constexpr int kVBytes = kMfmaChunk * kRowBytes;         // one wave's V buffer
-    static_assert(kD % 32 == 0 && kD <= 256 && kVPieces >= 1, "head size");
+    constexpr int kVPieces = kTok * kPiecesPerRow / kWaveSize;  // V 16-byte pieces per lane
+    constexpr int kVBytes = kTok * kRowBytes;               // one wave's V buffer
+    static_assert(kD % 32 == 0 && kD <= 256 && kVPieces >= 1 && (kSubs == 1 || kSubs == 2), "shape");
     // Two V buffers per wave; after the loop the same bytes hold the waves'
     // output accumulators for the merge ([wave][head][dim] fp32).
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kWaves * 2 * kVBytes];
-    static_assert(kWaves * 2 * kVBytes == kWaves * kMfmaHeads * kD * 4, "merge area");
+    constexpr int kLdsBytes = kWaves * 2 * kVBytes;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    static_assert(kLdsBytes >= kWaves * kMfmaHeads * kD * 4, "merge area");
     __shared__ float lds_m[kWaves][kMfmaHeads];
     __shared__ float lds_l[kWaves][kMfmaHeads];
 
@@ -585,20 +589,23 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
         return (block * a.block_size + t % a.block_size) * row_stride + head_bytes;
     };
 
-    bf16x8_m kfrag[kS];
+    bf16x8_m kfrag[kSubs][kS];
     u32x4_t vraw[kVPieces];
     // Issue the loads of the chunk starting at c0 (< t_hi). Tokens past t_hi
     // read the last valid token (their scores are masked).
     auto fetch = [&](int64_t c0) {
-        const int64_t last = (c0 + kMfmaChunk - 1 < t_hi - 1 ? c0 + kMfmaChunk - 1 : t_hi - 1);
+        const int64_t last = (c0 + kTok - 1 < t_hi - 1 ? c0 + kTok - 1 : t_hi - 1);
         if (last / a.block_size - window_base >= kWaveSize || c0 / a.block_size < window_base) {
             load_window(c0 / a.block_size);
         }
-        {
-            const int64_t t = c0 + j < t_hi ? c0 + j : t_hi - 1;
-            const int64_t off = row_offset(t);
 #pragma unroll
-            for (int s = 0; s < kS; ++s) kfrag[s] = __builtin_bit_cast(bf16x8_m, load16(a.k_cache, off + (32 * s + 8 * g) * 2));
+        for (int u = 0; u < kSubs; ++u) {
+            const int64_t t0 = c0 + kMfmaChunk * u + j;
+            const int64_t off = row_offset(t0 < t_hi ? t0 : t_hi - 1);
+#pragma unroll
+            for (int s = 0; s < kS; ++s) {
+                kfrag[u][s] = __builtin_bit_cast(bf16x8_m, load16(a.k_cache, off + (32 * s + 8 * g) * 2));
+            }
         }
 #pragma unroll
         for (int i = 0; i < kVPieces; ++i) {
@@ -623,8 +630,8 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
 #pragma unroll
     for (int b = 0; b < kB; ++b) acc[b] = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int64_t first = t_lo + static_cast<int64_t>(wave) * kMfmaChunk;
-    constexpr int64_t kStride = static_cast<int64_t>(kWaves) * kMfmaChunk;
+    const int64_t first = t_lo + static_cast<int64_t>(wave) * kTok;
+    constexpr int64_t kStride = static_cast<int64_t>(kWaves) * kTok;
     int buf = 0;
     if (first < t_hi) {
         load_window(first / a.block_size);
@@ -632,42 +639,55 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
         stage_v(0);
     }
     for (int64_t c0 = first; c0 < t_hi; c0 += kStride) {
-        bf16x8_m kcur[kS];
+        bf16x8_m kcur[kSubs][kS];
 #pragma unroll
-        for (int s = 0; s < kS; ++s) kcur[s] = kfrag[s];
+        for (int u = 0; u < kSubs; ++u) {
+#pragma unroll
+            for (int s = 0; s < kS; ++s) kcur[u][s] = kfrag[u][s];
+        }
         const int64_t next = c0 + kStride;
         if (next < t_hi) fetch(next);
 
-        f32x4_m sc = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < kS; ++s) sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kcur[s], qfrag[s], sc, 0, 0, 0);
+        f32x4_m sc[kSubs];
         float cmax = -INFINITY;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            sc[t] = c0 + 4 * g + t < t_hi ? sc[t] * a.scale : -INFINITY;
-            cmax = fmaxf(cmax, sc[t]);
+        for (int u = 0; u < kSubs; ++u) {
+            sc[u] = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < kS; ++s) sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kcur[u][s], qfrag[s], sc[u], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                sc[u][t] = c0 + kMfmaChunk * u + 4 * g + t < t_hi ? sc[u][t] * a.scale : -INFINITY;
+                cmax = fmaxf(cmax, sc[u][t]);
+            }
         }
         cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
         cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-        // Every chunk holds at least one valid token, so cmax is finite.
+        // Every step holds at least one valid token, so cmax is finite.
         const float m_new = fmaxf(m, cmax);
         const float c = m == -INFINITY ? 0.0f : __expf(m - m_new);
         m = m_new;
-        s16x4_m pb;
+        s16x4_m pb[kSubs];
         float psum = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const float pt = sc[t] == -INFINITY ? 0.0f : __expf(sc[t] - m_new);
-            psum += pt;
-            pb[t] = static_cast<short>(f32_to_bf16_bits(pt));
+        for (int u = 0; u < kSubs; ++u) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float pt = sc[u][t] == -INFINITY ? 0.0f : __expf(sc[u][t] - m_new);
+                psum += pt;
+                pb[u][t] = static_cast<short>(f32_to_bf16_bits(pt));
+            }
         }
         l = l * c + psum;
 #pragma unroll
         for (int b = 0; b < kB; ++b) acc[b] *= c;
 
-        // V^T fragments: lane (g, j) reads 8 bytes of token row 4 g + j / 4 at
-        // dims 16 b + 4 (j % 4) .. +3 and receives V[tokens 4 g .. 4 g + 3][dim 16 b + j].
-        // This wave's own writes of the buffer must have landed.
+        // V^T fragments: lane (g, j) reads 8 bytes of token row 4 g + j / 4 (of
+        // each sub-chunk) at dims 16 b + 4 (j % 4) .. +3 and receives
+        // V[tokens 4 g .. 4 g + 3][dim 16 b + j]. With two sub-chunks the MFMA's
+        // k index 8 g + t is token 4 g + t % 4 of sub-chunk t / 4, in both the
+        // V^T and the P^T operand. This wave's own writes of the buffer must
+        // have landed.
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14));
         asm volatile("" ::: "memory");
@@ -675,9 +695,18 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
 #pragma unroll
         for (int b = 0; b < kB; ++b) {
             const int off = (4 * g + (j >> 2)) * kRowBytes + (16 * b + 4 * (j & 3)) * 2;
-            const s16x4_m vfrag = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            const s16x4_m v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_s16x4_m*)((lds_u8_m*)(const_cast<uint8_t*>(vb)) + off));
-            acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vfrag, pb, acc[b], 0, 0, 0);
+            if constexpr (kSubs == 1) {
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v0, pb[0], acc[b], 0, 0, 0);
+            } else {
+                const s16x4_m v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4_m*)((lds_u8_m*)(const_cast<uint8_t*>(vb)) + off + kMfmaChunk * kRowBytes));
+                const bf16x8_m vv = __builtin_bit_cast(bf16x8_m, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+                const bf16x8_m pp =
+                    __builtin_bit_cast(bf16x8_m, __builtin_shufflevector(pb[0], pb[1], 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, pp, acc[b], 0, 0, 0);
+            }
         }
         if (next < t_hi) {
             buf ^= 1;
@@ -782,7 +811,10 @@ Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_d
     p.split_tokens = max_context > 0 ? max_context : 1;
     if (p.lanes == 0 || !may_split) return p;
     const int64_t base = sequences * kv_heads * p.head_groups;
-    int64_t splits = (kTargetWorkgroups + base - 1) / base;
+    // The matrix-core kernel's workgroups take 33-66 KiB of LDS, two per CU:
+    // split only as far as one round of them fills the GPU.
+    const int64_t target = p.lanes == kMfmaPlan ? 2 * static_cast<int64_t>(cu_count()) : kTargetWorkgroups;
+    int64_t splits = (target + base - 1) / base;
     const int64_t by_length = (max_context + kMinSplitTokens - 1) / kMinSplitTokens;
     if (splits > by_length) splits = by_length;
     if (splits < 1) splits = 1;
@@ -830,15 +862,17 @@ void launch_typed(const PagedArgs& args, const Plan& plan, int64_t sequences, hi
     if constexpr (!std::is_same<T, float>::value) {
       if (plan.lanes == kMfmaPlan) {
         const dim3 grid(static_cast<unsigned>(workgroups));
+        // Two sub-chunks per step up to D = 128 (64 KiB of LDS), one above.
+        constexpr int kSubsSmall = 2;
         switch (args.head_dim / 32) {
-            case 1: launch(paged_mfma_kernel<32>, grid, dim3(kThreads), 0, stream, args); break;
-            case 2: launch(paged_mfma_kernel<64>, grid, dim3(kThreads), 0, stream, args); break;
-            case 3: launch(paged_mfma_kernel<96>, grid, dim3(kThreads), 0, stream, args); break;
-            case 4: launch(paged_mfma_kernel<128>, grid, dim3(kThreads), 0, stream, args); break;
-            case 5: launch(paged_mfma_kernel<160>, grid, dim3(kThreads), 0, stream, args); break;
-            case 6: launch(paged_mfma_kernel<192>, grid, dim3(kThreads), 0, stream, args); break;
-            case 7: launch(paged_mfma_kernel<224>, grid, dim3(kThreads), 0, stream, args); break;
-            default: launch(paged_mfma_kernel<256>, grid, dim3(kThreads), 0, stream, args); break;
+            case 1: launch(paged_mfma_kernel<32, kSubsSmall>, grid, dim3(kThreads), 0, stream, args); break;
+            case 2: launch(paged_mfma_kernel<64, kSubsSmall>, grid, dim3(kThreads), 0, stream, args); break;
+            case 3: launch(paged_mfma_kernel<96, kSubsSmall>, grid, dim3(kThreads), 0, stream, args); break;
+            case 4: launch(paged_mfma_kernel<128, kSubsSmall>, grid, dim3(kThreads), 0, stream, args); break;
+            case 5: launch(paged_mfma_kernel<160, 1>, grid, dim3(kThreads), 0, stream, args); break;
+            case 6: launch(paged_mfma_kernel<192, 1>, grid, dim3(kThreads), 0, stream, args); break;
+            case 7: launch(paged_mfma_kernel<224, 1>, grid, dim3(kThreads), 0, stream, args); break;
+            default: launch(paged_mfma_kernel<256, 1>, grid, dim3(kThreads), 0, stream, args); break;
         }
         if (plan.splits > 1) {
             launch(paged_combine_kernel<T>, dim3(static_cast<unsigned>(sequences * args.heads)), dim3(kWaveSize), 0,
