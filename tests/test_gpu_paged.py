@@ -126,9 +126,9 @@ def test_bf16_cache():
 @pytest.mark.parametrize(
     "dims",
     [
-        (2, 1, 1, 128, 16, [300, 17]),      # MHA: the streaming kernel
+        (2, 1, 1, 128, 16, [300, 17]),      # MHA: the matrix-core kernel
         (2, 4, 2, 64, 16, [33, 0]),         # GQA group 2 (streaming), an empty sequence
-        (3, 8, 2, 128, 16, [200, 17, 1]),   # group 4: the matrix-core kernel
+        (3, 8, 2, 128, 16, [200, 17, 1]),   # group 4
         (2, 8, 2, 64, 16, [0, 40]),         # group 4, an empty sequence
         (2, 16, 2, 128, 16, [300, 16]),     # group 8
         (1, 32, 2, 32, 8, [100]),           # group 16, the widest the matrix-core kernel takes
@@ -143,7 +143,7 @@ def test_bf16_cache():
 )
 def test_bf16_paths(dims):
     """bf16 caches: head sizes that are multiples of 32 (up to 256) with GQA
-    groups of 4 to 16 take the matrix-core kernel (scores and P.V on MFMA,
+    groups of 1 and 4 to 16 take the matrix-core kernel (scores and P.V on MFMA,
     probabilities rounded to bf16 for P.V), the rest the streaming kernel;
     each within 1e-2 of the output scale of the float64 oracle on the same
     bf16 inputs, with and without the split workspace. An empty sequence
