@@ -37,6 +37,7 @@ HIP_SOURCES = (
     "cf_lora_fused.hip",
     "cf_lora_bwd.hip",
     "cf_lora_f32.hip",
+    "cf_matmul_f32.hip",
     "cf_scheduler.hip",
     "cf_paged_attention.hip",
     "cf_tensor_core.hip",

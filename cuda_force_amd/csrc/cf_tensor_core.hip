@@ -19,18 +19,22 @@
 // is more accurate than TF32 (about 16 significant bits per product against
 // 11) at three bf16 MFMA passes; A' and B' live in a caller workspace.
 //
-// Small outputs split K: with few 256 x 256 output tiles (1024 x 1024 is 16
-// tiles, 16 of 256 CUs), the K' range is cut into up to 8 slices (at most 256
-// workgroups); each slice writes an fp32 partial product into the workspace
-// and sum_splits_kernel adds them in slice order (the result is
-// deterministic and independent of the device). Both operand splits run as
-// one launch.
+// Small outputs (fewer than 64 of these 256 x 256 tiles) with 16-byte aligned
+// operands and k a multiple of 4 take the kernel of cf_matmul_f32.hip
+// instead: 128 x 128 tiles that split the operands on their way into LDS, no
+// split pass, fixed-order split K. Otherwise small outputs split K here: with
+// few 256 x 256 output tiles (1024 x 1024 is 16 tiles, 16 of 256 CUs), the K'
+// range is cut into up to 8 slices (at most 256 workgroups); each slice
+// writes an fp32 partial product into the workspace and sum_splits_kernel
+// adds them in slice order (the result is deterministic and independent of
+// the device). Both operand splits run as one launch.
 //
 // Shapes: any m and k; n a multiple of 8 (16-byte output rows), and the
 // tensors 16-byte aligned. The reference accepted m, n multiples of 16 and k
 // a multiple of 8; every shape it took is taken here.
 #include "cf_common.hpp"
 #include "cf_lora_fused.hpp"
+#include "cf_matmul_f32.hpp"
 
 namespace cf {
 namespace {
@@ -56,6 +60,16 @@ int k_splits(int64_t m, int64_t n, int64_t kk) {
         if (tiles * s <= kSplitTarget && granules % s == 0) splits = s;
     }
     return splits;
+}
+
+/// True when the split-while-staging kernel (128 x 128 tiles, cf_matmul_f32.hip)
+/// is the faster path: fewer than 64 of this path's 256 x 256 output tiles.
+/// Measured (us): 1024^3 36.5 -> 24.7-26.7, 128 x 4096 x 4096 93 -> 39,
+/// 512^3 25 -> 15; from 2048^3 (64 tiles: 92 against 94-98) and 8192 x 1024 x
+/// 4096 (128 tiles: 316 against 327) up, and at 4096^3 (406 against 613),
+/// this path is.
+bool tensor_core_prefers_staged(int64_t m, int64_t n) {
+    return ceil_div<int64_t>(m, kTile) * ceil_div<int64_t>(n, kTile) < 64;
 }
 
 /// c = sum over slices of part[s] (s = 0, 1, ...), four floats per thread.
@@ -172,7 +186,12 @@ size_t cf_matmul_tensor_core_workspace_bytes(int64_t m, int64_t n, int64_t k) {
     const size_t b_bytes = static_cast<size_t>(kk * n) * 2;
     const int splits = cf::k_splits(m, n, kk);
     const size_t part_bytes = splits > 1 ? static_cast<size_t>(splits) * m * n * 4 : 0;
-    return ((a_bytes + 255) / 256) * 256 + ((b_bytes + 255) / 256) * 256 + part_bytes;
+    const size_t split_path = ((a_bytes + 255) / 256) * 256 + ((b_bytes + 255) / 256) * 256 + part_bytes;
+    // The split-while-staging kernel (taken for small outputs with 16-byte
+    // aligned operands and k a multiple of 4) needs only its slices' partial
+    // outputs; the query covers whichever path the call takes.
+    const size_t staged_path = cf::matmul_f32_workspace_bytes(m, n, cf::matmul_f32_splits(m, n, k));
+    return split_path > staged_path ? split_path : staged_path;
 }
 
 cf_status cf_matmul_tensor_core(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
@@ -194,6 +213,10 @@ cf_status cf_matmul_tensor_core(const float* a, const float* b, float* c, int64_
         return cf::fail(CF_ERR_INVALID_ARGUMENT, "cf_matmul_tensor_core: workspace of %zu bytes, %zu needed",
                         workspace_bytes, cf_matmul_tensor_core_workspace_bytes(m, n, k));
     }
+    auto s = static_cast<hipStream_t>(stream);
+    if (cf::matmul_f32_eligible(a, b, c, m, n, k) && cf::tensor_core_prefers_staged(m, n)) {
+        return cf::launch_matmul_f32(a, b, c, m, n, k, cf::matmul_f32_splits(m, n, k), workspace, s);
+    }
     const int64_t kp = cf::padded_k(k);
     const size_t a_bytes = static_cast<size_t>(m * 3 * kp) * 2;
     const size_t b_bytes = static_cast<size_t>(3 * kp * n) * 2;
@@ -202,7 +225,6 @@ cf_status cf_matmul_tensor_core(const float* a, const float* b, float* c, int64_
     auto* partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ((a_bytes + 255) / 256) * 256 +
                                               ((b_bytes + 255) / 256) * 256);
     const int splits = cf::k_splits(m, n, 3 * kp);
-    auto s = static_cast<hipStream_t>(stream);
     cf::launch(cf::split_operands_kernel, dim3(cf::split_grid(m * 3 * kp / 4 + 3 * kp * n / 4)),
                dim3(cf::kDefaultBlockSize), 0, s, a, b, a_split, b_split, m, n, k, kp);
     const cf_status split = cf::check_launch("splitting the fp32 operands into bf16 parts", s);

@@ -85,20 +85,45 @@ def test_refuses_shapes_it_cannot_tile():
     assert torch.count_nonzero(c) == 0  # nothing launched
 
 
-def test_agrees_with_the_fp32_core_path_without_being_identical():
-    announce("tensor-core matmul vs the fp32 tiled path")
+def test_agrees_with_an_fp32_fma_path_without_being_identical():
+    """The reference compares its tensor-core result with its CUDA-core fp32
+    path: close, not bit-identical. Here cf_matmul's fp32 path also runs on
+    the matrix cores (the same three-product split), so the fp32 FMA product
+    compared against is torch's."""
+    announce("tensor-core matmul vs an fp32 FMA product")
     gen = torch.Generator(device="cuda").manual_seed(11)
     a = torch.randn(128, 64, generator=gen, device="cuda")
     b = torch.randn(64, 128, generator=gen, device="cuda")
     tc = tensor_core(a, b)
-    tiled = torch.empty(128, 128, device="cuda")
-    lib = _lib.load()
-    _lib.check(lib.cf_matmul(a.data_ptr(), b.data_ptr(), tiled.data_ptr(), _lib.CF_F32, 128, 128, 64,
-                             torch.cuda.current_stream().cuda_stream))
+    plain = a @ b
     torch.cuda.synchronize()
-    diff = (tc - tiled).abs()
-    assert diff.max().item() <= 2e-2 * tiled.abs().max().item() + 3e-3 * 8
+    diff = (tc - plain).abs()
+    assert diff.max().item() <= 2e-2 * plain.abs().max().item() + 3e-3 * 8
     assert diff.max().item() > 1e-7  # a different arithmetic path, not a copy of the fp32 one
+
+
+@pytest.mark.parametrize("shape", [(300, 136, 260), (1000, 1000, 1000), (77, 4096, 512), (129, 8, 4)], ids=str)
+def test_staged_kernel_shapes_and_the_fallback(shape):
+    """Small outputs with 16-byte aligned operands and k a multiple of 4 take
+    the kernel that splits fp32 into bf16 parts on the way into LDS (128 x 128
+    tiles, fixed-order split K); a misaligned `a` takes the split-pass kernel.
+    Both within 1e-4 sqrt(k) of the float64 product, and close to each other."""
+    m, n, k = shape
+    announce(f"tensor-core matmul staged kernel {shape}")
+    gen = torch.Generator(device="cuda").manual_seed(m + n + k)
+    a = torch.randn(m, k, generator=gen, device="cuda")
+    b = torch.randn(k, n, generator=gen, device="cuda")
+    expected = reference_product(a, b)
+    staged = tensor_core(a, b)
+    assert np.abs(staged.cpu().numpy() - expected).max() <= 1e-4 * math.sqrt(k)
+    assert torch.equal(staged.view(torch.int32), tensor_core(a, b).view(torch.int32))
+    # The same values at a 4-byte offset: a is no longer 16-byte aligned.
+    storage = torch.empty(m * k + 1, device="cuda")
+    shifted = storage[1:].view(m, k)
+    shifted.copy_(a)
+    fallback = tensor_core(shifted, b)
+    assert np.abs(fallback.cpu().numpy() - expected).max() <= 1e-4 * math.sqrt(k)
+    assert (fallback - staged).abs().max().item() <= 2e-4 * math.sqrt(k)
 
 
 def test_large_square():
@@ -115,9 +140,9 @@ def test_large_square():
 
 @pytest.mark.parametrize("shape", [(1024, 1024, 1024), (2048, 1024, 2048), (512, 256, 4096)], ids=str)
 def test_split_reduction_range_is_accurate_and_deterministic(shape):
-    """Outputs of fewer than 128 tiles cut K' = 3 kp into 2-16 slices whose fp32
-    partial products are summed in slice order: as accurate as one pass, and
-    bit-identical from call to call."""
+    """Small outputs cut the reduction into slices whose fp32 partial products
+    are summed in slice order: as accurate as one pass, and bit-identical
+    from call to call."""
     m, n, k = shape
     announce(f"tensor-core matmul split K {shape}")
     gen = torch.Generator(device="cuda").manual_seed(k + 3)
