@@ -329,18 +329,21 @@ int cf_tensor_cores_available(void);
  * (cuda/include/cudaforge/tensor_core_matmul.cuh:51). */
 int cf_matmul_tensor_core_shape_supported(int64_t m, int64_t n, int64_t k);
 
-/* Workspace for the bf16 operand parts and, for outputs of at most 128
- * 256 x 256 tiles, the fp32 partial products of the split reduction range
- * (2-8 slices)
- * (0 for an unsupported shape). It has no counterpart in the reference, whose
- * TF32 kernel read fp32 directly. */
+/* Workspace for the bf16 operand parts and, for small outputs, the fp32
+ * partial products of the split reduction range (2-8 slices); the size covers
+ * whichever of the two kernels below the call takes (0 for an unsupported
+ * shape). It has no counterpart in the reference, whose TF32 kernel read fp32
+ * directly. */
 size_t cf_matmul_tensor_core_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
 /* c[m, n] = a[m, k] b[k, n], row-major fp32, on the bf16 MFMA units: each
  * operand is split into bf16 high and low parts and the three significant
- * cross products run as one bf16 GEMM with fp32 accumulation (about 16
- * significant bits per product; the reference's TF32 kept 11). b, c and the
- * workspace 16-byte aligned. An unsupported shape is CF_ERR_UNSUPPORTED
+ * cross products are accumulated in fp32 (about 16 significant bits per
+ * product; the reference's TF32 kept 11). Outputs of fewer than 64 256 x 256
+ * tiles with a 16-byte aligned and k a multiple of 4 split the operands while
+ * staging them (one launch, or two with a split reduction range); the rest
+ * write the bf16 parts to the workspace and run one bf16 GEMM over them. b, c
+ * and the workspace 16-byte aligned. An unsupported shape is CF_ERR_UNSUPPORTED
  * without launching, where the reference returned false.
  * Replaces launch_matmul_tensor_core (cuda/include/cudaforge/tensor_core_matmul.cuh:40-41). */
 cf_status cf_matmul_tensor_core(const float* a, const float* b, float* c, int64_t m, int64_t n,
