@@ -138,6 +138,10 @@ def test_bf16_cache():
         (2, 16, 4, 160, 64, [129, 300]),    # group 4, head size 160, 64-token blocks
         (1, 8, 2, 80, 16, [100]),           # head size 80 (not a multiple of 32): the streaming kernel
         (1, 16, 2, 128, 16, [1100]),        # a long context: split across workgroups, or not
+        (2, 12, 4, 64, 16, [90, 33]),       # group 3 (not a power of two)
+        (1, 10, 2, 224, 8, [61]),           # group 5, head size 224
+        (2, 24, 2, 192, 32, [250, 5]),      # group 12, head size 192
+        (3, 6, 2, 32, 16, [1, 16, 17]),     # group 3, one token, exactly one chunk, one past it
     ],
     ids=str,
 )
