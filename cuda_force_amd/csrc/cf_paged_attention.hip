@@ -762,6 +762,227 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
     }
 }
 
+/// fp32 caches on the matrix cores (v_mfma_f32_16x16x4_f32: fp32 products,
+/// fp32 sums, the accuracy of the streaming kernel). Same organisation as
+/// paged_mfma_kernel (workgroup per sequence, KV head and split; 16-token
+/// chunks per wave; waves merged through LDS), with these operand layouts:
+///   scores, step 4 u + e (u < D / 16, e < 4): A = K[token j][dim 16 u + 4 g + e]
+///     (lane (g, j) holds dims 16 u + 4 g .. +3 from one 16-byte load), B =
+///     Q[head j][the same dim] (registers), so MFMA slot g of every step pairs
+///     one dim of K with the same dim of Q; lane (g, j) receives the scores of
+///     tokens 4 g .. 4 g + 3 for head j;
+///   P.V, step c < 4 of output block b: slot g stands for token 4 g + c, so the
+///     B operand is the lane's own probability p[c] and the A operand is
+///     V[token 4 g + c][dim 16 b + j], one ds_read_b32 from a per-wave LDS copy
+///     of the chunk's V rows (rows padded by 16 bytes, so rows 4 apart start
+///     64 bytes apart in the banks and the four lane groups of a read use
+///     different banks).
+template <int kD>
+__global__ __launch_bounds__(kThreads) void paged_mfma_f32_kernel(PagedArgs a) {
+    constexpr int kU = kD / 16;                             // 16-dim blocks
+    constexpr int kRowBytes = kD * 4;
+    constexpr int kLdsRow = kRowBytes + 16;                 // padded V row in LDS
+    constexpr int kPiecesPerRow = kRowBytes / 16;
+    constexpr int kVPieces = kMfmaChunk * kPiecesPerRow / kWaveSize;
+    constexpr int kVBytes = kMfmaChunk * kLdsRow;           // one wave's V buffer
+    static_assert(kD % 16 == 0 && kD <= 128 && kVPieces >= 1, "head size");
+    constexpr int kLdsBytes = kWaves * 2 * kVBytes;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    static_assert(kLdsBytes >= kWaves * kMfmaHeads * kD * 4, "merge area");
+    __shared__ float lds_m[kWaves][kMfmaHeads];
+    __shared__ float lds_l[kWaves][kMfmaHeads];
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & (kWaveSize - 1);
+    const int wave = tid / kWaveSize;
+    const int g = lane >> 4;
+    const int j = lane & 15;
+
+    int64_t id = blockIdx.x;
+    const int split = static_cast<int>(id % a.splits);
+    id /= a.splits;
+    const int64_t kv_head = id % a.kv_heads;
+    const int64_t seq = id / a.kv_heads;
+    const int64_t group = a.heads / a.kv_heads;  // <= kMfmaHeads (checked on the host)
+    const int64_t head0 = kv_head * group;
+
+    // q[head j][dims 16 u + 4 g .. +3], pre-scaled; heads past the group are zero.
+    f32x4_m qv[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        u32x4_t raw = {0u, 0u, 0u, 0u};
+        if (j < group) raw = load16(a.query, ((seq * a.heads + head0 + j) * kD + 16 * u + 4 * g) * 4);
+        qv[u] = f32x4_m{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                        __uint_as_float(raw[3])} * a.scale;
+    }
+
+    const int64_t capacity = a.max_blocks * a.block_size;
+    const int64_t stored = a.context[seq] > 0 ? a.context[seq] : 0;
+    const int64_t context = stored < capacity ? stored : capacity;
+    const int64_t t_lo = static_cast<int64_t>(split) * a.split_tokens;
+    const int64_t t_hi = context < t_lo + a.split_tokens ? context : t_lo + a.split_tokens;
+    const int64_t row_stride = a.kv_heads * kRowBytes;
+    const int64_t head_bytes = kv_head * kRowBytes;
+    const uint32_t* table = a.tables + seq * a.max_blocks;
+
+    int64_t window_base = 0;
+    int window = 0;
+    auto load_window = [&](int64_t base) {
+        const int64_t entry = base + lane < a.max_blocks ? base + lane : a.max_blocks - 1;
+        window_base = base;
+        window = static_cast<int>(table[entry]);
+    };
+    auto row_offset = [&](int64_t t) {
+        const int64_t block =
+            static_cast<uint32_t>(__shfl(window, static_cast<int>(t / a.block_size - window_base)));
+        return (block * a.block_size + t % a.block_size) * row_stride + head_bytes;
+    };
+
+    u32x4_t kraw[kU];
+    u32x4_t vraw[kVPieces];
+    auto fetch = [&](int64_t c0) {
+        const int64_t last = (c0 + kMfmaChunk - 1 < t_hi - 1 ? c0 + kMfmaChunk - 1 : t_hi - 1);
+        if (last / a.block_size - window_base >= kWaveSize || c0 / a.block_size < window_base) {
+            load_window(c0 / a.block_size);
+        }
+        {
+            const int64_t t = c0 + j < t_hi ? c0 + j : t_hi - 1;
+            const int64_t off = row_offset(t);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) kraw[u] = load16(a.k_cache, off + (16 * u + 4 * g) * 4);
+        }
+#pragma unroll
+        for (int i = 0; i < kVPieces; ++i) {
+            const int p = lane + kWaveSize * i;
+            const int64_t t0 = c0 + p / kPiecesPerRow;
+            const int64_t t = t0 < t_hi ? t0 : t_hi - 1;
+            vraw[i] = load16(a.v_cache, row_offset(t) + (p % kPiecesPerRow) * 16);
+        }
+    };
+    auto stage_v = [&](int buf) {
+        uint8_t* base = lds + (wave * 2 + buf) * kVBytes;
+#pragma unroll
+        for (int i = 0; i < kVPieces; ++i) {
+            const int p = lane + kWaveSize * i;
+            *reinterpret_cast<u32x4_t*>(base + (p / kPiecesPerRow) * kLdsRow + (p % kPiecesPerRow) * 16) = vraw[i];
+        }
+    };
+
+    float m = -INFINITY;
+    float l = 0.0f;
+    f32x4_m acc[kU];  // O^T[dim 16 b + 4 g + t][head j]
+#pragma unroll
+    for (int b = 0; b < kU; ++b) acc[b] = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int64_t first = t_lo + static_cast<int64_t>(wave) * kMfmaChunk;
+    constexpr int64_t kStride = static_cast<int64_t>(kWaves) * kMfmaChunk;
+    int buf = 0;
+    if (first < t_hi) {
+        load_window(first / a.block_size);
+        fetch(first);
+        stage_v(0);
+    }
+    for (int64_t c0 = first; c0 < t_hi; c0 += kStride) {
+        f32x4_m kcur[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            kcur[u] = f32x4_m{__uint_as_float(kraw[u][0]), __uint_as_float(kraw[u][1]), __uint_as_float(kraw[u][2]),
+                              __uint_as_float(kraw[u][3])};
+        }
+        const int64_t next = c0 + kStride;
+        if (next < t_hi) fetch(next);
+
+        f32x4_m sc = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kcur[u][e], qv[u][e], sc, 0, 0, 0);
+        }
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            sc[t] = c0 + 4 * g + t < t_hi ? sc[t] : -INFINITY;
+            cmax = fmaxf(cmax, sc[t]);
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float m_new = fmaxf(m, cmax);  // finite: every chunk has a valid token
+        const float c = m == -INFINITY ? 0.0f : __expf(m - m_new);
+        m = m_new;
+        float p[4];
+        float psum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            p[t] = sc[t] == -INFINITY ? 0.0f : __expf(sc[t] - m_new);
+            psum += p[t];
+        }
+        l = l * c + psum;
+#pragma unroll
+        for (int b = 0; b < kU; ++b) acc[b] *= c;
+
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14));
+        asm volatile("" ::: "memory");
+        const uint8_t* vb = lds + (wave * 2 + buf) * kVBytes;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const float* vrow = reinterpret_cast<const float*>(vb + (4 * g + cc) * kLdsRow);
+#pragma unroll
+            for (int b = 0; b < kU; ++b) {
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * b + j], p[cc], acc[b], 0, 0, 0);
+            }
+        }
+        if (next < t_hi) {
+            buf ^= 1;
+            stage_v(buf);
+        }
+    }
+
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+
+    __syncthreads();
+    float* macc = reinterpret_cast<float*>(lds);  // [wave][head][dim]
+#pragma unroll
+    for (int b = 0; b < kU; ++b) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) macc[(wave * kMfmaHeads + j) * kD + 16 * b + 4 * g + t] = acc[b][t];
+    }
+    if (g == 0) {
+        lds_m[wave][j] = m;
+        lds_l[wave][j] = l;
+    }
+    __syncthreads();
+
+    for (int pair = tid; pair < kMfmaHeads * kD; pair += kThreads) {
+        const int h = pair / kD;
+        const int d = pair % kD;
+        if (h >= group) continue;
+        float mm = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, lds_m[w][h]);
+        float ll = 0.0f;
+        float oo = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float cw = lds_m[w][h] == -INFINITY ? 0.0f : __expf(lds_m[w][h] - mm);
+            ll = fmaf(lds_l[w][h], cw, ll);
+            oo = fmaf(macc[(w * kMfmaHeads + h) * kD + d], cw, oo);
+        }
+        const int64_t head = head0 + h;
+        if (a.splits == 1) {
+            static_cast<float*>(a.out)[(seq * a.heads + head) * kD + d] = ll > 0.0f ? oo / ll : 0.0f;
+        } else {
+            float* part = a.partial + ((seq * a.heads + head) * a.splits + split) * (kD + 2);
+            if (d == 0) {
+                part[0] = mm;
+                part[1] = ll;
+            }
+            part[2 + d] = oo;
+        }
+    }
+}
+
 /// Lanes per token for the streaming kernel (16 bytes per lane), or 0 when D
 /// needs the wide one.
 int lanes_for(int64_t head_dim, int64_t elem_bytes) {
@@ -786,8 +1007,10 @@ struct Plan {
     int64_t split_tokens;
 };
 
-/// Plan.lanes value that selects paged_mfma_kernel.
+/// Plan.lanes values that select paged_mfma_kernel (16-bit caches) and
+/// paged_mfma_f32_kernel (fp32 caches).
 constexpr int kMfmaPlan = -1;
+constexpr int kMfmaF32Plan = -2;
 
 Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_dim,
               int64_t block_size, int64_t max_blocks, int64_t elem_bytes, bool may_split) {
@@ -805,6 +1028,19 @@ Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_d
         p.gs = kMfmaHeads;
         p.head_groups = 1;
     }
+    // fp32 caches on the matrix cores where that is faster (fp32 D = 128):
+    // groups of 8 or more (64 x 1024 tokens, 8 KV heads: 35.9 -> 64.6% of HBM
+    // peak), and groups of 4 when one round of two workgroups per CU holds
+    // every (sequence, KV head) (64 x 1024: 60.6 -> 65.1%; with 128 x 256,
+    // two rounds: 59.8 -> 51.6%, so not). MHA (64.4 against 60.2%) and
+    // groups of 2 (75.3 against 70.9%) stay on the streaming kernel.
+    const bool one_round = sequences * kv_heads <= 2 * static_cast<int64_t>(cu_count());
+    if (elem_bytes == 4 && head_dim % 16 == 0 && head_dim <= 128 && group <= kMfmaHeads &&
+        (group >= 8 || (group >= 4 && one_round))) {
+        p.lanes = kMfmaF32Plan;
+        p.gs = kMfmaHeads;
+        p.head_groups = 1;
+    }
     const int64_t max_context = max_blocks * block_size;
     p.splits = 1;
     p.split_tokens = max_context > 0 ? max_context : 1;
@@ -812,7 +1048,8 @@ Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_d
     const int64_t base = sequences * kv_heads * p.head_groups;
     // The matrix-core kernel's workgroups take 33-66 KiB of LDS, two per CU:
     // split only as far as one round of them fills the GPU.
-    const int64_t target = p.lanes == kMfmaPlan ? 2 * static_cast<int64_t>(cu_count()) : kTargetWorkgroups;
+    const int64_t target =
+        p.lanes == kMfmaPlan || p.lanes == kMfmaF32Plan ? 2 * static_cast<int64_t>(cu_count()) : kTargetWorkgroups;
     int64_t splits = (target + base - 1) / base;
     const int64_t by_length = (max_context + kMinSplitTokens - 1) / kMinSplitTokens;
     if (splits > by_length) splits = by_length;
@@ -858,6 +1095,26 @@ void launch_typed(const PagedArgs& args, const Plan& plan, int64_t sequences, hi
         return;
     }
     const int64_t workgroups = sequences * args.kv_heads * plan.head_groups * plan.splits;
+    if constexpr (std::is_same<T, float>::value) {
+        if (plan.lanes == kMfmaF32Plan) {
+            const dim3 grid(static_cast<unsigned>(workgroups));
+            switch (args.head_dim / 16) {
+                case 1: launch(paged_mfma_f32_kernel<16>, grid, dim3(kThreads), 0, stream, args); break;
+                case 2: launch(paged_mfma_f32_kernel<32>, grid, dim3(kThreads), 0, stream, args); break;
+                case 3: launch(paged_mfma_f32_kernel<48>, grid, dim3(kThreads), 0, stream, args); break;
+                case 4: launch(paged_mfma_f32_kernel<64>, grid, dim3(kThreads), 0, stream, args); break;
+                case 5: launch(paged_mfma_f32_kernel<80>, grid, dim3(kThreads), 0, stream, args); break;
+                case 6: launch(paged_mfma_f32_kernel<96>, grid, dim3(kThreads), 0, stream, args); break;
+                case 7: launch(paged_mfma_f32_kernel<112>, grid, dim3(kThreads), 0, stream, args); break;
+                default: launch(paged_mfma_f32_kernel<128>, grid, dim3(kThreads), 0, stream, args); break;
+            }
+            if (plan.splits > 1) {
+                launch(paged_combine_kernel<T>, dim3(static_cast<unsigned>(sequences * args.heads)), dim3(kWaveSize),
+                       0, stream, args);
+            }
+            return;
+        }
+    }
     if constexpr (!std::is_same<T, float>::value) {
       if (plan.lanes == kMfmaPlan) {
         const dim3 grid(static_cast<unsigned>(workgroups));

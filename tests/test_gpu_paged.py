@@ -114,6 +114,30 @@ def test_long_contexts(workspace):
                                atol=FP32_MARGIN)
 
 
+@pytest.mark.parametrize(
+    "dims",
+    [
+        (2, 16, 2, 128, 16, [300, 17]),     # group 8
+        (1, 16, 1, 48, 8, [77]),            # group 16, head size 48
+        (2, 32, 4, 80, 4, [129, 0]),        # group 8, head size 80, an empty sequence
+        (1, 8, 2, 112, 16, [600]),          # group 4 (one round), head size 112, split or not
+        (3, 24, 3, 16, 2, [5, 40, 16]),     # group 8, head size 16, two-token blocks
+    ],
+    ids=str,
+)
+def test_fp32_matrix_core_path(dims):
+    """fp32 caches with GQA groups of 8 or more (or 4, when one round of
+    workgroups holds every sequence and KV head) run on the fp32 matrix-core
+    kernel (v_mfma_f32_16x16x4_f32: fp32 products and sums), within the
+    reference's 2e-5 margin of the float64 oracle, with and without the split
+    workspace."""
+    announce(f"paged attention fp32 matrix cores {dims}")
+    case = make_case(*dims, seed=sum(dims[:5]) * 3 + len(dims[5]))
+    expected = run_oracle(case)
+    for workspace in (True, False):
+        np.testing.assert_allclose(run_gpu(case, workspace=workspace), expected, rtol=0, atol=FP32_MARGIN)
+
+
 def test_bf16_cache():
     announce("paged attention bf16")
     case = make_case(3, 8, 2, 128, 16, [200, 17, 1], seed=8)
