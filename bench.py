@@ -827,9 +827,12 @@ def bench_tensor_core(torch, cf, warmup: int, runs: int) -> dict:
 
 
 def bench_fp8(torch, cf, warmup: int, runs: int) -> dict:
-    """fp8 (e4m3fn) MFMA matmul, bf16 output, at 8192^3 and 4096^3; FLOP/s
-    counts 2 m n k against the dense fp8 peak, with hipBLASLt's fp8 GEMM
-    (torch._scaled_mm, per-tensor scales) for context where torch offers it."""
+    """fp8 (e4m3fn) MFMA matmul, bf16 output, at 8192^3 and 4096^3, with w
+    row-major [K, N] (cf_matmul_fp8) and K-major as w_t [N, K]
+    (cf_matmul_fp8_wt, the operand layout hipBLASLt's fp8 GEMM is given
+    below); FLOP/s counts 2 m n k against the dense fp8 peak, with hipBLASLt's
+    fp8 GEMM (torch._scaled_mm, per-tensor scales) for context where torch
+    offers it."""
     lib = cf._lib.load()
     gen = torch.Generator(device="cuda").manual_seed(9)
     stream = torch.cuda.current_stream().cuda_stream
@@ -843,11 +846,17 @@ def bench_fp8(torch, cf, warmup: int, runs: int) -> dict:
         def fp8():
             cf._lib.check(lib.cf_matmul_fp8(x.data_ptr(), w.data_ptr(), y.data_ptr(), n, n, n, 1.0, stream))
 
-        r = summary(time_launches(torch, [fp8], warmup, runs))
+        w_t = w.t().contiguous()
+
+        def fp8_wt():
+            cf._lib.check(lib.cf_matmul_fp8_wt(x.data_ptr(), w_t.data_ptr(), y.data_ptr(), n, n, n, 1.0, stream))
+
         flops = 2 * n ** 3
-        with_kernel_time(torch, cf, r, [fp8], flops=flops, peak=PEAK_FP8_TFLOPS)
-        tflops = flops / (r["median_ms"] * 1e-3) / 1e12
-        out[f"matmul_fp8_{n}"] = {**r, "TFLOP/s": tflops, "frac_fp8_peak": tflops / PEAK_FP8_TFLOPS}
+        for name, fn in ((f"matmul_fp8_{n}", fp8), (f"matmul_fp8_wt_{n}", fp8_wt)):
+            r = summary(time_launches(torch, [fn], warmup, runs))
+            with_kernel_time(torch, cf, r, [fn], flops=flops, peak=PEAK_FP8_TFLOPS)
+            tflops = flops / (r["median_ms"] * 1e-3) / 1e12
+            out[name] = {**r, "TFLOP/s": tflops, "frac_fp8_peak": tflops / PEAK_FP8_TFLOPS}
         try:
             xf = x.view(torch.float8_e4m3fn)
             wf = w.view(torch.float8_e4m3fn).t().contiguous().t()  # column-major right operand
@@ -860,7 +869,7 @@ def bench_fp8(torch, cf, warmup: int, runs: int) -> dict:
                 **r, "TFLOP/s": flops / (r["median_ms"] * 1e-3) / 1e12}
         except (RuntimeError, AttributeError) as exc:
             out[f"torch_scaled_mm_fp8_{n}_context"] = {"unavailable": str(exc).splitlines()[0][:160]}
-        del codes, y
+        del codes, y, w_t
         torch.cuda.empty_cache()
     return out
 

@@ -4,7 +4,9 @@
 //
 // x and w row-major fp8 codes (the operator layout of the LoRA linear and of
 // the matmul the reference demonstrates tensor cores with,
-// cuda/include/cudaforge/tensor_core_matmul.cuh:40-41), fp32 accumulation,
+// cuda/include/cudaforge/tensor_core_matmul.cuh:40-41), or w given K-major as
+// w_t[N, K] (row-major; the weight layout of a torch Linear, y = x w_t^T, and
+// the one fp8 GEMM libraries take), fp32 accumulation,
 // one per-tensor scale (the product of the two operands' dequantisation
 // scales) applied in the epilogue, bf16 output. The reference has no fp8
 // path; this is the fp8 half of a bf16/fp8 MFMA matmul replacing its TF32
@@ -28,13 +30,18 @@
 //     l % 32 from an N-major tile, transposed on the way out of LDS by four
 //     ds_read_b64_tr_b8 (each hands a lane 8 k values of one column). Both
 //     tiles are swizzled so every read is free of bank conflicts.
+//   * K-major w (kWT): w_t rows are K-contiguous like x rows, so w travels
+//     and is read exactly as x is (128-byte row lines in a ring of two
+//     two-K-step slots, two ds_read_b128 per fragment): half the LDS read
+//     instructions of the transposed form, the same LDS footprint.
 //   * Epilogue: scale, round to bf16, staged per wave in LDS and stored as
 //     whole 256-byte row pieces.
 //   * Workgroup ids are remapped so that the tiles of one XCD share x
 //     row-panels in its L2 (tile_of).
 //
 // Shapes: any M; K a positive multiple of 128; N a positive multiple of 16;
-// x, w and y 16-byte aligned.
+// x, w and y 16-byte aligned; 32-bit buffer offsets over all of w (w[K, N])
+// or over one 256-row panel of x and of w_t.
 #include "cf_common.hpp"
 #include "cf_lds_dma.hpp"
 
@@ -61,6 +68,7 @@ constexpr int kTileW = kBK * kBN;             // 16 KiB: [64 k][256 n]
 constexpr int kOffW = kXSlots * kXPair;
 constexpr int kLdsBytes = kOffW + kStages * kTileW;  // 128 KiB
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 workgroup");
+static_assert(kStages * kTileW == kXSlots * kXPair, "w_t slots take the place of the w stages");
 static_assert(kThreads / 64 * 64 * 256 <= kLdsBytes, "output staging fits the operand area");
 
 constexpr int kUnitScale = 127;  // E8M0 code of 2^0
@@ -105,6 +113,7 @@ struct Fp8Args {
     int tiles_n;
 };
 
+template <bool kWT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void matmul_fp8_kernel(Fp8Args args) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
@@ -138,24 +147,39 @@ void matmul_fp8_kernel(Fp8Args args) {
         const int chunk = (lane & 7) ^ x_swizzle(row);
         x_dma[i] = static_cast<uint32_t>(row * K + chunk * 16);
     }
-    // w: share vw = k-row quads q = 2 vw + i % 2; lane -> row 4 q + l/16,
+    // w[K, N]: share vw = k-row quads q = 2 vw + i % 2; lane -> row 4 q + l/16,
     // physical chunk l % 16. Columns past N read as zero.
-    const i32x4_t wbuf = uniform(raw_buffer_words(args.w, static_cast<uint32_t>(K * N)));
+    // w_t[N, K]: the 256 rows n0 .. +255 of the tile, mapped exactly as x's
+    // rows (the same offsets, x_dma, in its own buffer). Rows past N read as
+    // zero.
+    const int64_t cols_here = N - n0 < kBN ? N - n0 : kBN;
+    const i32x4_t wbuf = kWT ? uniform(raw_buffer_words(args.w + n0 * K, static_cast<uint32_t>(cols_here * K)))
+                             : uniform(raw_buffer_words(args.w, static_cast<uint32_t>(K * N)));
     uint32_t w_dma[4];
+    if constexpr (!kWT) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int vw = (wave & 3) + 4 * (i >> 1);
-        const int row = 4 * (vw * 2 + (i & 1)) + (lane >> 4);
-        const int64_t col = n0 + 16 * ((lane & 15) ^ w_swizzle(row));
-        w_dma[i] = col < N ? static_cast<uint32_t>(row * N + col) : kOutOfRange;
+        for (int i = 0; i < 4; ++i) {
+            const int vw = (wave & 3) + 4 * (i >> 1);
+            const int row = 4 * (vw * 2 + (i & 1)) + (lane >> 4);
+            const int64_t col = n0 + 16 * ((lane & 15) ^ w_swizzle(row));
+            w_dma[i] = col < N ? static_cast<uint32_t>(row * N + col) : kOutOfRange;
+        }
     }
 
     const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)lds));
-    auto issue_w = [&](int64_t kt, int piece) {
-        const uint32_t stage = lds_addr + kOffW + static_cast<uint32_t>(kt % kStages) * kTileW;
-        const int vw = (wave & 3) + 4 * (piece >> 1);
-        dma16(wbuf, stage + (vw * 2 + (piece & 1)) * 1024, w_dma[piece],
-              static_cast<uint32_t>(kt * kBK * N));
+    // issue_w takes a K-step for w[K, N], a pair of K-steps for w_t.
+    auto issue_w = [&](int64_t t, int piece) {
+        if constexpr (kWT) {
+            const uint32_t slot = lds_addr + kOffW + static_cast<uint32_t>(t % kXSlots) * kXPair;
+            const int vw = (wave & 3) + 4 * (piece >> 2);
+            dma16(wbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
+                  static_cast<uint32_t>(t * 2 * kBK));
+        } else {
+            const uint32_t stage = lds_addr + kOffW + static_cast<uint32_t>(t % kStages) * kTileW;
+            const int vw = (wave & 3) + 4 * (piece >> 1);
+            dma16(wbuf, stage + (vw * 2 + (piece & 1)) * 1024, w_dma[piece],
+                  static_cast<uint32_t>(t * kBK * N));
+        }
     };
     auto issue_x = [&](int64_t pair, int piece) {
         const uint32_t slot = lds_addr + static_cast<uint32_t>(pair % kXSlots) * kXPair;
@@ -163,8 +187,8 @@ void matmul_fp8_kernel(Fp8Args args) {
         dma16(xbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
               static_cast<uint32_t>(pair * 2 * kBK));
     };
-    constexpr int kWLoads = 4;  // w DMA per K-step per issuing wave
-    constexpr int kXLoads = 8;  // x DMA per pair of K-steps per issuing wave
+    constexpr int kWLoads = kWT ? 8 : 4;  // w DMA per pair of K-steps (w_t) or per K-step, per issuing wave
+    constexpr int kXLoads = 8;            // x DMA per pair of K-steps per issuing wave
 
     // ---- LDS -> register fragment roles ----
     // x (B operand), row block i of the wave: row wm*64 + 32 i + l % 32,
@@ -190,6 +214,11 @@ void matmul_fp8_kernel(Fp8Args args) {
         w_rd[jb] = row * kBN + ((chunk ^ w_swizzle(row)) << 4) + (jl & 1) * 8;
     }
     // Rows r * 8 further keep row & 7, hence the same swizzle.
+    // w_t (A operand, K-major), column block jb of the wave: lane l reads 32
+    // consecutive k bytes of tile row wn*128 + 32 jb + l % 32, as x is read
+    // (the swizzle again depends on lane bits 0-3 only).
+    const int wt_rd0 = (wn * 128 + (lane & 31)) * (2 * kBK) + (((2 * h) ^ x_swizzle(lane)) << 4);
+    const int wt_rd1 = (wn * 128 + (lane & 31)) * (2 * kBK) + (((2 * h + 1) ^ x_swizzle(lane)) << 4);
 
     struct XFrags {
         i32x8_t x[2];
@@ -205,6 +234,13 @@ void matmul_fp8_kernel(Fp8Args args) {
         }
     };
     auto read_w = [&](int64_t kt, int jb) {
+        if constexpr (kWT) {
+            const uint8_t* sw = lds + kOffW + static_cast<int>((kt >> 1) % kXSlots) * kXPair;
+            const int odd = static_cast<int>(kt & 1) << 6;
+            const i32x4v_t lo = *reinterpret_cast<const i32x4v_t*>(sw + ((wt_rd0 ^ odd) + jb * 32 * 2 * kBK));
+            const i32x4v_t hi = *reinterpret_cast<const i32x4v_t*>(sw + ((wt_rd1 ^ odd) + jb * 32 * 2 * kBK));
+            return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
         const uint8_t* sw = lds + kOffW + static_cast<int>(kt % kStages) * kTileW;
         const i32x2_t r0 = lds_read_tr8(sw, w_rd[jb]);
         const i32x2_t r1 = lds_read_tr8(sw, w_rd[jb] + 8 * kBN);
@@ -229,7 +265,8 @@ void matmul_fp8_kernel(Fp8Args args) {
     // is read into it once the two MFMAs of this step that use it have
     // issued. x is double-buffered. On step kt the issuing waves send out
     // the DMA for K-step kt + 3 (w) and, on odd steps, for x pair
-    // (kt + 3) / 2, spread over the step's eight MFMAs.
+    // (kt + 3) / 2, spread over the step's eight MFMAs. With w_t, odd steps
+    // send out both operands' pair (kt + 3) / 2 and even steps send nothing.
     i32x8_t wf[4];
     auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next, auto issue, auto odd,
                         auto issuer) {
@@ -241,8 +278,15 @@ void matmul_fp8_kernel(Fp8Args args) {
                     wf[jb], f.x[i], acc[jb][i], 0, 0, 0, kUnitScale, 0, kUnitScale);
                 if constexpr (decltype(issue)::value && decltype(issuer)::value) {
                     const int s = 2 * jb + i;
-                    if constexpr (decltype(odd)::value) issue_x((next_kt + 2) >> 1, s);
-                    if (s & 1) issue_w(next_kt + 2, s >> 1);
+                    if constexpr (kWT) {
+                        if constexpr (decltype(odd)::value) {
+                            issue_x((next_kt + 2) >> 1, s);
+                            issue_w((next_kt + 2) >> 1, s);
+                        }
+                    } else {
+                        if constexpr (decltype(odd)::value) issue_x((next_kt + 2) >> 1, s);
+                        if (s & 1) issue_w(next_kt + 2, s >> 1);
+                    }
                 }
             }
             if constexpr (decltype(read_next)::value) wf[jb] = read_w(next_kt, jb);
@@ -260,7 +304,18 @@ void matmul_fp8_kernel(Fp8Args args) {
             for (int piece = 0; piece < kXLoads; ++piece) issue_x(pair, piece);
         };
         // Issue order as if steps -2 and -1 had run: x pair 0, w 0, w 1 | x pair 1, w 2.
-        if constexpr (decltype(issuer)::value) {
+        // With w_t: pair 0 of both | pair 1 of both.
+        if constexpr (decltype(issuer)::value && kWT) {
+            issue_x_all(0);
+            issue_w_all(0);
+            if (k_tiles > 2) {
+                issue_x_all(1);
+                issue_w_all(1);
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads + kXLoads));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            }
+        } else if constexpr (decltype(issuer)::value) {
             issue_x_all(0);
             issue_w_all(0);
             issue_w_all(1);
@@ -286,13 +341,15 @@ void matmul_fp8_kernel(Fp8Args args) {
         // barrier; x pair p goes out on step 2p - 3 into the slot pair p - 2
         // left. DMA completes in issue order, so the wait leaves exactly the
         // previous step's loads in flight: w after an even step, w and an x
-        // pair after an odd one.
+        // pair after an odd one. With w_t both operands' pair p goes out on
+        // step 2p - 3 and even steps issue nothing, so an even step leaves
+        // one pair of both in flight and an odd step waits for everything.
         using yes = std::true_type;
         using no = std::false_type;
         auto step = [&](int64_t kt, XFrags& cur, XFrags& nxt, auto issue, auto wait_all, auto read,
                         auto odd) {
             if constexpr (decltype(read)::value) {
-                if constexpr (decltype(wait_all)::value) {
+                if constexpr (decltype(wait_all)::value || (kWT && decltype(odd)::value)) {
                     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
                 } else if constexpr (decltype(odd)::value) {
                     __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
@@ -370,6 +427,44 @@ void matmul_fp8_kernel(Fp8Args args) {
     }
 }
 
+template <bool kWT>
+cf_status launch_fp8(const char* name, const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k,
+                     float scale, void* stream) {
+    Fp8Args args;
+    args.x = static_cast<const uint8_t*>(x);
+    args.w = static_cast<const uint8_t*>(w);
+    args.y = static_cast<uint16_t*>(y);
+    args.M = m;
+    args.N = n;
+    args.K = k;
+    args.scale = scale;
+    args.tiles_m = static_cast<int>(ceil_div<int64_t>(m, kBM));
+    args.tiles_n = static_cast<int>(ceil_div<int64_t>(n, kBN));
+    auto s = static_cast<hipStream_t>(stream);
+    launch(matmul_fp8_kernel<kWT>, dim3(args.tiles_m * args.tiles_n), dim3(kThreads), 0, s, args);
+    return check_launch(name, s);
+}
+
+cf_status validate_fp8(const char* entry, int supported, const void* x, const void* w, void* y, int64_t m,
+                       int64_t n, int64_t k) {
+    if (!supported) {
+        return fail(CF_ERR_UNSUPPORTED,
+                    "%s: shape %lld x %lld x %lld is not tiled (k must be a positive multiple of 128, n of 16)",
+                    entry, static_cast<long long>(m), static_cast<long long>(n), static_cast<long long>(k));
+    }
+    if (x == nullptr || w == nullptr || y == nullptr) {
+        return fail(CF_ERR_INVALID_ARGUMENT, "%s: null pointer", entry);
+    }
+    if (!host_aligned(x, 16) || !host_aligned(w, 16) || !host_aligned(y, 16)) {
+        return fail(CF_ERR_UNSUPPORTED, "%s: x, w and y must be 16-byte aligned", entry);
+    }
+    return CF_OK;
+}
+
+bool tiles_fit(int64_t m, int64_t n) {
+    return ceil_div<int64_t>(m, kBM) * ceil_div<int64_t>(n, kBN) < (1LL << 31);
+}
+
 }  // namespace
 }  // namespace cf
 
@@ -379,38 +474,31 @@ int cf_matmul_fp8_shape_supported(int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0 || n % 16 != 0 || k % (2 * cf::kBK) != 0) return 0;
     // 32-bit buffer offsets: all of w, and one 256-row panel of x.
     if (k * n >= (1LL << 31) || static_cast<int64_t>(cf::kBM) * k >= (1LL << 31)) return 0;
-    return cf::ceil_div<int64_t>(m, cf::kBM) * cf::ceil_div<int64_t>(n, cf::kBN) < (1LL << 31) ? 1 : 0;
+    return cf::tiles_fit(m, n) ? 1 : 0;
+}
+
+int cf_matmul_fp8_wt_shape_supported(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0 || n % 16 != 0 || k % (2 * cf::kBK) != 0) return 0;
+    // 32-bit buffer offsets: one 256-row panel of x and of w_t.
+    if (static_cast<int64_t>(cf::kBM) * k >= (1LL << 31)) return 0;
+    return cf::tiles_fit(m, n) ? 1 : 0;
 }
 
 cf_status cf_matmul_fp8(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k, float scale,
                         void* stream) {
     CF_ENTRY();
-    if (!cf_matmul_fp8_shape_supported(m, n, k)) {
-        return cf::fail(CF_ERR_UNSUPPORTED,
-                        "cf_matmul_fp8: shape %lld x %lld x %lld is not tiled (k must be a positive multiple "
-                        "of 128, n of 16)",
-                        static_cast<long long>(m), static_cast<long long>(n), static_cast<long long>(k));
-    }
-    if (x == nullptr || w == nullptr || y == nullptr) {
-        return cf::fail(CF_ERR_INVALID_ARGUMENT, "cf_matmul_fp8: null pointer");
-    }
-    if (!cf::host_aligned(x, 16) || !cf::host_aligned(w, 16) || !cf::host_aligned(y, 16)) {
-        return cf::fail(CF_ERR_UNSUPPORTED, "cf_matmul_fp8: x, w and y must be 16-byte aligned");
-    }
-    cf::Fp8Args args;
-    args.x = static_cast<const uint8_t*>(x);
-    args.w = static_cast<const uint8_t*>(w);
-    args.y = static_cast<uint16_t*>(y);
-    args.M = m;
-    args.N = n;
-    args.K = k;
-    args.scale = scale;
-    args.tiles_m = static_cast<int>(cf::ceil_div<int64_t>(m, cf::kBM));
-    args.tiles_n = static_cast<int>(cf::ceil_div<int64_t>(n, cf::kBN));
-    auto s = static_cast<hipStream_t>(stream);
-    cf::launch(cf::matmul_fp8_kernel, dim3(args.tiles_m * args.tiles_n), dim3(cf::kThreads), 0, s,
-               args);
-    return cf::check_launch("launching the fp8 MFMA matmul", s);
+    const cf_status st = cf::validate_fp8("cf_matmul_fp8", cf_matmul_fp8_shape_supported(m, n, k), x, w, y, m, n, k);
+    if (st != CF_OK) return st;
+    return cf::launch_fp8<false>("launching the fp8 MFMA matmul", x, w, y, m, n, k, scale, stream);
+}
+
+cf_status cf_matmul_fp8_wt(const void* x, const void* w_t, void* y, int64_t m, int64_t n, int64_t k, float scale,
+                           void* stream) {
+    CF_ENTRY();
+    const cf_status st =
+        cf::validate_fp8("cf_matmul_fp8_wt", cf_matmul_fp8_wt_shape_supported(m, n, k), x, w_t, y, m, n, k);
+    if (st != CF_OK) return st;
+    return cf::launch_fp8<true>("launching the fp8 MFMA matmul (K-major w)", x, w_t, y, m, n, k, scale, stream);
 }
 
 }  // extern "C"

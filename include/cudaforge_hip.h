@@ -366,6 +366,20 @@ int cf_matmul_fp8_shape_supported(int64_t m, int64_t n, int64_t k);
 cf_status cf_matmul_fp8(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k,
                         float scale, void* stream);
 
+/* 1 when cf_matmul_fp8_wt takes this shape: m >= 1, k a positive multiple of
+ * 128, n a positive multiple of 16, 256 k < 2^31. It has no counterpart in
+ * the reference (no fp8 path there). */
+int cf_matmul_fp8_wt_shape_supported(int64_t m, int64_t n, int64_t k);
+
+/* cf_matmul_fp8 with the right operand K-major: y[m, n] = bf16(scale * (x[m, k]
+ * w_t[n, k]^T)), w_t row-major [n, k] (the weight layout of a torch Linear and
+ * the operand order fp8 GEMM libraries take). Both operands then stream into
+ * LDS as whole row lines and need no transposing reads. Same numerics,
+ * alignment and error behaviour as cf_matmul_fp8; no workspace, no
+ * allocation. It has no counterpart in the reference, which has no fp8 path. */
+cf_status cf_matmul_fp8_wt(const void* x, const void* w_t, void* y, int64_t m, int64_t n, int64_t k,
+                           float scale, void* stream);
+
 /* ---- paged-attention decode ---------------------------------------------- */
 
 /* Workspace bytes cf_paged_attention uses to split long contexts across

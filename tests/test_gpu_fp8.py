@@ -1,4 +1,5 @@
-"""GPU tests of the fp8 (e4m3fn) MFMA matmul (cf_matmul_fp8).
+"""GPU tests of the fp8 (e4m3fn) MFMA matmul (cf_matmul_fp8, and
+cf_matmul_fp8_wt, which takes the right operand K-major as w_t[N, K]).
 
 The reference has no fp8 path, so the oracle is oracle.matmul_fp8 (float64 sum
 of the exact fp8 products, pinned in tests/test_fp8_oracle.py).
@@ -15,7 +16,8 @@ Two kinds of check:
   the bf16 rounding at k = 128, less at larger k). The bound used is
   2^-8 |y| + 2^-13 scale (|x| |w|), four times the measured excess.
 Also: every finite code (subnormals, +-448, negative zero), the scale, and the
-refusal of shapes the kernel cannot tile.
+refusal of shapes the kernel cannot tile. Both layouts feed the MFMA the same
+fragments, so their outputs must agree bit for bit.
 """
 
 from __future__ import annotations
@@ -47,12 +49,21 @@ def small_codes(gen: np.random.Generator, shape) -> np.ndarray:
     return ((sign << 7) | (exponent << 3) | mantissa).astype(np.uint8)
 
 
-def run_fp8(x: torch.Tensor, w: torch.Tensor, scale: float) -> torch.Tensor:
+LAYOUTS = ("kn", "nk")  # w[K, N] through cf_matmul_fp8, w_t[N, K] through cf_matmul_fp8_wt
+
+
+def run_fp8(x: torch.Tensor, w: torch.Tensor, scale: float, layout: str = "kn") -> torch.Tensor:
+    """y = bf16(scale x w) for w[K, N]; layout "nk" hands the kernel w^T."""
     m, k = x.shape
     n = w.shape[1]
     y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=x.device)
-    _lib.check(_lib.load().cf_matmul_fp8(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k, scale,
-                                        torch.cuda.current_stream().cuda_stream))
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    if layout == "kn":
+        _lib.check(lib.cf_matmul_fp8(x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k, scale, stream))
+    else:
+        w_t = w.t().contiguous()
+        _lib.check(lib.cf_matmul_fp8_wt(x.data_ptr(), w_t.data_ptr(), y.data_ptr(), m, n, k, scale, stream))
     torch.cuda.synchronize()
     return y
 
@@ -65,18 +76,18 @@ def powers_of_two(gen: np.random.Generator, shape) -> np.ndarray:
     return np.where(gen.random(shape) < 0.3, np.uint8(0), codes)
 
 
-def check_exact(x_codes: np.ndarray, w_codes: np.ndarray) -> None:
-    got = run_fp8(torch.from_numpy(x_codes).cuda(), torch.from_numpy(w_codes).cuda(), 1.0)
+def check_exact(x_codes: np.ndarray, w_codes: np.ndarray, layout: str) -> None:
+    got = run_fp8(torch.from_numpy(x_codes).cuda(), torch.from_numpy(w_codes).cuda(), 1.0, layout)
     expected = oracle.round_bf16(oracle.matmul_fp8(x_codes, w_codes, 1.0))
     got = got.float().cpu().numpy().astype(np.float64)
     bad = np.argwhere(got != expected)
     assert len(bad) == 0, f"{len(bad)} outputs differ, first at {tuple(bad[0])}"
 
 
-def check_against_oracle(x_codes: np.ndarray, w_codes: np.ndarray, scale: float) -> None:
+def check_against_oracle(x_codes: np.ndarray, w_codes: np.ndarray, scale: float, layout: str) -> None:
     x = torch.from_numpy(x_codes).cuda()
     w = torch.from_numpy(w_codes).cuda()
-    got = run_fp8(x, w, scale).float().cpu().numpy().astype(np.float64)
+    got = run_fp8(x, w, scale, layout).float().cpu().numpy().astype(np.float64)
     expected = oracle.matmul_fp8(x_codes, w_codes, scale)
     magnitude = abs(scale) * (np.abs(oracle.e4m3fn_to_f64(x_codes)) @ np.abs(oracle.e4m3fn_to_f64(w_codes)))
     bound = 2.0**-8 * np.abs(expected) + MFMA_REL * magnitude
@@ -90,45 +101,63 @@ def check_against_oracle(x_codes: np.ndarray, w_codes: np.ndarray, scale: float)
     [(1, 16, 128), (256, 256, 128), (300, 272, 384), (513, 528, 256), (64, 1024, 1152), (1000, 48, 640)],
     ids=str,
 )
-def test_against_the_oracle(shape):
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_against_the_oracle(shape, layout):
     m, n, k = shape
-    announce(f"fp8 matmul {shape}")
+    announce(f"fp8 matmul {shape} {layout}")
     gen = np.random.default_rng(m * 7 + n * 3 + k)
-    check_against_oracle(small_codes(gen, (m, k)), small_codes(gen, (k, n)), 1.0)
+    check_against_oracle(small_codes(gen, (m, k)), small_codes(gen, (k, n)), 1.0, layout)
 
 
 @pytest.mark.parametrize("shape", [(256, 256, 128), (300, 272, 384), (513, 528, 1152)], ids=str)
-def test_data_movement_is_exact(shape):
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_data_movement_is_exact(shape, layout):
     m, n, k = shape
-    announce(f"fp8 matmul exact cases {shape}")
+    announce(f"fp8 matmul exact cases {shape} {layout}")
     gen = np.random.default_rng(m + n + k)
     one_hot_x = np.zeros((m, k), np.uint8)
     one_hot_x[np.arange(m), (np.arange(m) * 7 + 3) % k] = 0x38
-    check_exact(one_hot_x, finite_codes(gen, (k, n)))
+    check_exact(one_hot_x, finite_codes(gen, (k, n)), layout)
     one_hot_w = np.zeros((k, n), np.uint8)
     one_hot_w[(np.arange(n) * 5 + 1) % k, np.arange(n)] = 0x38
-    check_exact(finite_codes(gen, (m, k)), one_hot_w)
-    check_exact(powers_of_two(gen, (m, k)), powers_of_two(gen, (k, n)))
+    check_exact(finite_codes(gen, (m, k)), one_hot_w, layout)
+    check_exact(powers_of_two(gen, (m, k)), powers_of_two(gen, (k, n)), layout)
 
 
-def test_every_finite_code_and_the_scale():
-    announce("fp8 matmul every code")
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_every_finite_code_and_the_scale(layout):
+    announce(f"fp8 matmul every code {layout}")
     gen = np.random.default_rng(11)
     x = finite_codes(gen, (384, 512))
     w = finite_codes(gen, (512, 320))
     x[0, :256] = np.arange(256, dtype=np.uint8)  # every code once, NaN codes replaced
     x[0] = np.where((x[0] & 0x7F) == 0x7F, np.uint8(0x80), x[0])
-    check_against_oracle(x, w, 0.375)
+    check_against_oracle(x, w, 0.375, layout)
 
 
-def test_identity_reproduces_the_decoded_operand():
-    announce("fp8 matmul identity")
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_identity_reproduces_the_decoded_operand(layout):
+    announce(f"fp8 matmul identity {layout}")
     gen = np.random.default_rng(12)
     x = finite_codes(gen, (260, 256))
     eye = np.where(np.eye(256, dtype=bool), np.uint8(0x38), np.uint8(0))
-    got = run_fp8(torch.from_numpy(x).cuda(), torch.from_numpy(eye).cuda(), 1.0).cpu()
+    got = run_fp8(torch.from_numpy(x).cuda(), torch.from_numpy(eye).cuda(), 1.0, layout).cpu()
     expected = torch.from_numpy(x).view(torch.float8_e4m3fn).to(torch.bfloat16)  # exact in bf16
     assert torch.equal(got, expected)
+
+
+@pytest.mark.parametrize("shape", [(1, 16, 128), (300, 272, 384), (777, 1040, 2560)], ids=str)
+def test_both_layouts_agree_bit_for_bit(shape):
+    """The MFMA receives the same fragments from either layout, so general
+    codes give identical bits, ragged tiles included."""
+    m, n, k = shape
+    announce(f"fp8 matmul layouts agree {shape}")
+    gen = np.random.default_rng(m + 3 * n + 5 * k)
+    x = torch.from_numpy(finite_codes(gen, (m, k))).cuda()
+    w = torch.from_numpy(finite_codes(gen, (k, n))).cuda()
+    a = run_fp8(x, w, 0.75, "kn")
+    b = run_fp8(x, w, 0.75, "nk")
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
 def test_unsupported_shapes_are_refused():
@@ -146,6 +175,16 @@ def test_unsupported_shapes_are_refused():
     assert status == _lib.CF_ERR_UNSUPPORTED
     status = lib.cf_matmul_fp8(None, x.data_ptr(), y.data_ptr(), 16, 16, 128, 1.0, None)
     assert status == _lib.CF_ERR_INVALID_ARGUMENT
+    # K-major w: only one 256-row panel of w_t needs 32-bit offsets.
+    assert lib.cf_matmul_fp8_wt_shape_supported(16, 65536, 32768) == 1
+    assert lib.cf_matmul_fp8_wt_shape_supported(16, 16, 1 << 23) == 0  # 256 k = 2^31
+    assert lib.cf_matmul_fp8_wt_shape_supported(16, 24, 128) == 0
+    assert lib.cf_matmul_fp8_wt_shape_supported(16, 16, 64) == 0
+    status = lib.cf_matmul_fp8_wt(x.data_ptr(), x.data_ptr(), y.data_ptr(), 16, 16, 64, 1.0,
+                                  torch.cuda.current_stream().cuda_stream)
+    assert status == _lib.CF_ERR_UNSUPPORTED
+    status = lib.cf_matmul_fp8_wt(x.data_ptr(), None, y.data_ptr(), 16, 16, 128, 1.0, None)
+    assert status == _lib.CF_ERR_INVALID_ARGUMENT
 
 
 def test_full_size_against_torch_fp32():
@@ -162,6 +201,7 @@ def test_full_size_against_torch_fp32():
     got = run_fp8(pow2[0], pow2[1], 1.0)
     exact = pow2[0].view(torch.float8_e4m3fn).float() @ pow2[1].view(torch.float8_e4m3fn).float()
     assert torch.equal(got, exact.to(torch.bfloat16))
+    assert torch.equal(run_fp8(pow2[0], pow2[1], 1.0, "nk"), got)
     del pow2, zero, exponent, exact
 
     # Moderate magnitudes, no NaN code: exponent field 3 or 7 (bit 6 clear,
@@ -176,3 +216,4 @@ def test_full_size_against_torch_fp32():
     bound = 2.0**-8 * expected.abs() + (MFMA_REL + size * 2.0**-24) * magnitude
     assert bool(((got - expected).abs() <= bound).all())
     assert bool(torch.isfinite(got).all())
+    assert torch.equal(run_fp8(x, w, 0.5, "nk").float(), got)
