@@ -46,9 +46,10 @@ HIP_SOURCES = (
 
 # Per-source additions. The fused LoRA kernel accumulates in VGPRs: the
 # compiler's AGPR accumulator allocation rotates registers every K-step.
+# (cf_matmul_fp8.hip must not take this flag: its one-wave-per-SIMD kernel
+# keeps 256 accumulators per lane in the accumulation registers.)
 HIPCC_EXTRA_FLAGS = {
     "cf_lora_fused.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
-    "cf_matmul_fp8.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
 }
 
 HIP_LIBRARY = PACKAGE_DIR / "libcudaforge_hip.so"

@@ -46,6 +46,19 @@ __device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t lds_dst, uint32_t v
         : "memory");
 }
 
+/// dma16 with the LDS base handed to the compiler as an M0 operand instead of
+/// being saved, set and restored inside the assembly: the compiler writes M0
+/// itself (one scalar instruction, often folded into the address add) and
+/// knows its value afterwards. The s_nop covers the one wait state an M0
+/// write needs before an LDS DMA reads it.
+__device__ __forceinline__ void dma16_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
+                                         uint32_t soffset) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_dst)
+                 : "memory");
+}
+
 __device__ __forceinline__ void dma4(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
                                      uint32_t soffset) {
     int saved_m0;

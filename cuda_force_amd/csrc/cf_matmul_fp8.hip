@@ -427,6 +427,220 @@ void matmul_fp8_kernel(Fp8Args args) {
     }
 }
 
+// ---- One wave per SIMD (K-major operands) --------------------------------
+// matmul_fp8_w4_kernel: the same 256x256 output tile with four waves, each
+// owning a 128x128 sub-tile as 4x4 v_mfma_scale_f32_32x32x64_f8f6f4
+// accumulators (256 fp32 per lane, in the accumulation registers; one wave
+// per SIMD has 512 registers). Per MFMA this reads half the LDS bytes of a
+// 64x128 sub-tile and issues half the scalar and barrier work per SIMD.
+//   * K-tiles of 128 bytes, double-buffered in LDS for both operands: x and
+//     w_t rows as whole 128-byte lines (32 KiB per operand and slot, the x
+//     swizzle), every wave copying 64 rows of each (16 DMA per K-tile).
+//   * Fragments double-buffered in registers by K-half: the 16 MFMAs of one
+//     half issue while the fragments of the next half are read.
+//   * One barrier per K-tile, between its halves: by then every wave has
+//     read all of K-tile t (so slot t % 2 takes K-tile t + 2, one DMA after
+//     each MFMA of the second half) and K-tile t + 1 has landed (its DMA
+//     went out one K-tile earlier).
+constexpr int kW4Threads = 256;
+constexpr int kW4Slot = kBM * 2 * kBK;  // 32 KiB: [256 rows][128 k]
+constexpr int kW4OffW = 2 * kW4Slot;    // x slots 0 and 1, then w_t slots 0 and 1
+constexpr int kW4Lds = 4 * kW4Slot;     // 128 KiB
+static_assert(kW4Lds >= 4 * 128 * 256, "output staging (4 waves x 128 x 128 bf16) fits the operand area");
+
+/// Reduction depths up to this take the eight-wave kernel: its shorter
+/// prologue and epilogue outweigh this kernel's faster K-loop (equal at
+/// 2048; at 8192 x 8192 x 1024 the eight-wave kernel is 4% faster, at
+/// 8192^3 this one 8%).
+constexpr int64_t kW4MinK = 2048;
+
+/// s_waitcnt immediate that waits for every LDS operation of this wave.
+constexpr int lgkmcnt0_imm() { return 15 | (3 << 14) | (7 << 4); }
+
+__global__ __launch_bounds__(kW4Threads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void matmul_fp8_w4_kernel(Fp8Args args) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kW4Lds];
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1;  // 128-row half of the tile
+    const int wn = wave & 1;   // 128-column half of the tile
+    int tm;
+    int tn;
+    tile_of(static_cast<int>(blockIdx.x), args.tiles_m, args.tiles_n, tm, tn);
+    const int64_t m0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+    const int64_t M = args.M;
+    const int64_t N = args.N;
+    const int64_t K = args.K;
+
+    // ---- HBM -> LDS: load i (0..7) of an operand copies tile rows
+    // 64 wave + 8 i + l / 8, physical chunk l % 8 of the row's 128-byte line
+    // (lane l lands at byte 16 l of the load's 1 KiB). With i = 2 a + b the
+    // row's swizzle only depends on l / 8 and b, so two lane offsets serve
+    // all eight loads; 16 a rows go into the scalar offset. Rows past M (x)
+    // or N (w_t) read as zero.
+    const int64_t rows_here = M - m0 < kBM ? M - m0 : kBM;
+    const int64_t cols_here = N - n0 < kBN ? N - n0 : kBN;
+    const i32x4_t xbuf = uniform(raw_buffer_words(args.x + m0 * K, static_cast<uint32_t>(rows_here * K)));
+    const i32x4_t wbuf = uniform(raw_buffer_words(args.w + n0 * K, static_cast<uint32_t>(cols_here * K)));
+    uint32_t dma_off[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int row = 64 * wave + 8 * b + (lane >> 3);
+        dma_off[b] = static_cast<uint32_t>(row * K + (((lane & 7) ^ x_swizzle(row)) << 4));
+    }
+    const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)lds));
+    const uint32_t k16 = static_cast<uint32_t>(16 * K);
+    // Load s (0..15) of K-tile t: x for even s, w_t for odd, row group s / 2.
+    auto issue_load = [&](int t, int slot, int s) {
+        const int i = s >> 1;
+        const uint32_t dst = lds_addr + static_cast<uint32_t>(slot * kW4Slot + wave * 8192 + i * 1024) +
+                             ((s & 1) ? kW4OffW : 0);
+        const uint32_t sofs = static_cast<uint32_t>(t) * (2 * kBK) + static_cast<uint32_t>(i >> 1) * k16;
+        dma16_m0((s & 1) ? wbuf : xbuf, dst, dma_off[i & 1], sofs);
+    };
+
+    // ---- LDS -> registers: block i of x (B operand) is tile row
+    // wm*128 + 32 i + l % 32, block jb of w_t (A operand) tile row
+    // wn*128 + 32 jb + l % 32; lane l takes k bytes 32 (l / 32) .. +31 of
+    // the K-half as two ds_read_b128 (logical chunks 2 (l / 32) and
+    // 2 (l / 32) + 1; the second K-half is chunks 4-7, byte offset ^ 64).
+    const int h = lane >> 5;
+    const int sw = x_swizzle(lane & 31);
+    const int rd0 = (lane & 31) * (2 * kBK) + (((2 * h) ^ sw) << 4);
+    const int rd1 = (lane & 31) * (2 * kBK) + (((2 * h + 1) ^ sw) << 4);
+    const int x_base = wm * 128 * (2 * kBK);
+    const int w_base = kW4OffW + wn * 128 * (2 * kBK);
+
+    struct Frags {
+        i32x8_t a[4];  // w_t blocks jb
+        i32x8_t b[4];  // x blocks i
+    };
+    // `base` has bit 6 clear (slots, row blocks); the K-half flips bit 6 of
+    // the lane's chunk offset.
+    auto read_pair = [&](int base, int half) {
+        const i32x4v_t lo = *reinterpret_cast<const i32x4v_t*>(lds + base + (rd0 ^ (half << 6)));
+        const i32x4v_t hi = *reinterpret_cast<const i32x4v_t*>(lds + base + (rd1 ^ (half << 6)));
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    // Fragment r (0..7) of a K-half in the order the MFMAs below first use
+    // them: a0, b0, b1, b2, b3, a1, a2, a3.
+    auto read_frag = [&](Frags& f, int slot, int half, int r) {
+        if (r >= 1 && r <= 4) {
+            f.b[r - 1] = read_pair(x_base + slot * kW4Slot + (r - 1) * 32 * (2 * kBK), half);
+        } else {
+            const int j = r == 0 ? 0 : r - 4;
+            f.a[j] = read_pair(w_base + slot * kW4Slot + j * 32 * (2 * kBK), half);
+        }
+    };
+
+    f32x16_t acc[4][4];  // [w_t block jb][x block i]
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) acc[jb][i][t] = 0.0f;
+        }
+    }
+    // The 16 MFMAs of one K-half, each followed by its share of the other
+    // work: on even MFMAs a fragment of the next K-half (read_next), on
+    // every MFMA one of the 16 DMA of K-tile t + 2 (issue). The scheduling
+    // barriers keep this order.
+    auto multiply = [&](const Frags& f, Frags& next, int next_slot, int next_half, int issue_t, int issue_slot,
+                        auto read_next, auto issue) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int jb = s >> 2;
+            const int i = s & 3;
+            acc[jb][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                f.a[jb], f.b[i], acc[jb][i], 0, 0, 0, kUnitScale, 0, kUnitScale);
+            if constexpr (decltype(read_next)::value) {
+                if ((s & 1) == 0) read_frag(next, next_slot, next_half, s >> 1);
+            }
+            if constexpr (decltype(issue)::value) issue_load(issue_t, issue_slot, s);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    const int k_tiles = static_cast<int>(K / (2 * kBK));  // >= 1
+#pragma unroll
+    for (int s = 0; s < 16; ++s) issue_load(0, 0, s);
+    if (k_tiles > 1) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) issue_load(1, 1, s);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));
+    } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+    bare_barrier();  // K-tile 0 in LDS
+
+    Frags f0;
+    Frags f1;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) read_frag(f0, 0, 0, r);
+    // K-tile t (slot t % 2). The last two K-tiles are peeled so that the
+    // loop body has no branch for the compiler to move the MFMAs across.
+    using yes = std::true_type;
+    using no = std::false_type;
+    auto k_tile = [&](int t, auto issue, auto more) {
+        const int slot = t & 1;
+        // First half: multiply f0 while reading the second half into f1.
+        multiply(f0, f1, slot, 1, 0, 0, yes{}, no{});
+        // Every wave done reading slot `slot`; K-tile t + 1 landed.
+        __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+        if constexpr (decltype(more)::value) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        bare_barrier();
+        // Second half: multiply f1 while reading K-tile t + 1's first half
+        // and sending K-tile t + 2 into the slot just finished.
+        multiply(f1, f0, slot ^ 1, 0, t + 2, slot, more, issue);
+    };
+    int t = 0;
+    for (; t + 2 < k_tiles; ++t) k_tile(t, yes{}, yes{});
+    if (k_tiles >= 2) k_tile(t++, no{}, yes{});
+    k_tile(t, no{}, no{});
+
+    // Store: acc[jb][i] element t of lane l is y[row wm*128 + 32 i + l % 32]
+    // [column wn*128 + 32 jb + 8 (t / 4) + 4 (l / 32) + t % 4], staged per
+    // wave as a 128 x 128 bf16 sub-tile (rows of 256 bytes, chunk c of row r
+    // at c ^ (r & 15), rows with bit 4 set swapping the 8-byte halves of
+    // their chunks) and stored as whole 256-byte row pieces.
+    __syncthreads();
+    const float scale = args.scale;
+    uint8_t* stage = lds + wave * (128 * 256);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 32 * i + (lane & 31);
+        const int flip = (r >> 4) & 1;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            const f32x16_t& a = acc[jb][i];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int c = 4 * jb + q;
+                uint2 packed;
+                packed.x = f32_to_bf16_bits(scale * a[4 * q]) | (f32_to_bf16_bits(scale * a[4 * q + 1]) << 16);
+                packed.y = f32_to_bf16_bits(scale * a[4 * q + 2]) | (f32_to_bf16_bits(scale * a[4 * q + 3]) << 16);
+                *reinterpret_cast<uint2*>(stage + r * 256 + ((c ^ (r & 15)) << 4) + ((h ^ flip) << 3)) = packed;
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const int c = lane & 15;
+    const int64_t col = n0 + wn * 128 + 8 * c;
+#pragma unroll
+    for (int s = 0; s < 32; ++s) {
+        const int r = 4 * s + (lane >> 4);
+        uint4 v = *reinterpret_cast<const uint4*>(stage + r * 256 + ((c ^ (r & 15)) << 4));
+        if ((r >> 4) & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        const int64_t grow = m0 + wm * 128 + r;
+        if (grow < M && col < N) store_stream16(args.y + grow * N + col, v);
+    }
+}
+
 template <bool kWT>
 cf_status launch_fp8(const char* name, const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k,
                      float scale, void* stream) {
@@ -498,7 +712,22 @@ cf_status cf_matmul_fp8_wt(const void* x, const void* w_t, void* y, int64_t m, i
     const cf_status st =
         cf::validate_fp8("cf_matmul_fp8_wt", cf_matmul_fp8_wt_shape_supported(m, n, k), x, w_t, y, m, n, k);
     if (st != CF_OK) return st;
-    return cf::launch_fp8<true>("launching the fp8 MFMA matmul (K-major w)", x, w_t, y, m, n, k, scale, stream);
+    if (k <= cf::kW4MinK) {
+        return cf::launch_fp8<true>("launching the fp8 MFMA matmul (K-major w)", x, w_t, y, m, n, k, scale, stream);
+    }
+    cf::Fp8Args args;
+    args.x = static_cast<const uint8_t*>(x);
+    args.w = static_cast<const uint8_t*>(w_t);
+    args.y = static_cast<uint16_t*>(y);
+    args.M = m;
+    args.N = n;
+    args.K = k;
+    args.scale = scale;
+    args.tiles_m = static_cast<int>(cf::ceil_div<int64_t>(m, cf::kBM));
+    args.tiles_n = static_cast<int>(cf::ceil_div<int64_t>(n, cf::kBN));
+    auto s = static_cast<hipStream_t>(stream);
+    cf::launch(cf::matmul_fp8_w4_kernel, dim3(args.tiles_m * args.tiles_n), dim3(cf::kW4Threads), 0, s, args);
+    return cf::check_launch("launching the fp8 MFMA matmul (K-major w, one wave per SIMD)", s);
 }
 
 }  // extern "C"

@@ -98,18 +98,21 @@ def check_against_oracle(x_codes: np.ndarray, w_codes: np.ndarray, scale: float,
 
 @pytest.mark.parametrize(
     "shape",
-    [(1, 16, 128), (256, 256, 128), (300, 272, 384), (513, 528, 256), (64, 1024, 1152), (1000, 48, 640)],
+    [(1, 16, 128), (256, 256, 128), (300, 272, 384), (513, 528, 256), (64, 1024, 1152), (1000, 48, 640),
+     (300, 272, 2176)],
     ids=str,
 )
 @pytest.mark.parametrize("layout", LAYOUTS)
 def test_against_the_oracle(shape, layout):
+    """Reduction depths above 2048 with K-major w take the one-wave-per-SIMD
+    kernel (here 17 K-tiles of 128: an odd count through its peeled tail)."""
     m, n, k = shape
     announce(f"fp8 matmul {shape} {layout}")
     gen = np.random.default_rng(m * 7 + n * 3 + k)
     check_against_oracle(small_codes(gen, (m, k)), small_codes(gen, (k, n)), 1.0, layout)
 
 
-@pytest.mark.parametrize("shape", [(256, 256, 128), (300, 272, 384), (513, 528, 1152)], ids=str)
+@pytest.mark.parametrize("shape", [(256, 256, 128), (300, 272, 384), (513, 528, 1152), (513, 528, 2304)], ids=str)
 @pytest.mark.parametrize("layout", LAYOUTS)
 def test_data_movement_is_exact(shape, layout):
     m, n, k = shape
@@ -146,10 +149,13 @@ def test_identity_reproduces_the_decoded_operand(layout):
     assert torch.equal(got, expected)
 
 
-@pytest.mark.parametrize("shape", [(1, 16, 128), (300, 272, 384), (777, 1040, 2560)], ids=str)
+@pytest.mark.parametrize("shape", [(1, 16, 128), (300, 272, 384), (777, 1040, 2560), (260, 300 - 300 % 16, 4224)],
+                         ids=str)
 def test_both_layouts_agree_bit_for_bit(shape):
-    """The MFMA receives the same fragments from either layout, so general
-    codes give identical bits, ragged tiles included."""
+    """The MFMA receives the same fragments from either layout and each
+    kernel adds the K-steps in the same order, so general codes give
+    identical bits, ragged tiles included (K above 2048 with K-major w: the
+    one-wave-per-SIMD kernel)."""
     m, n, k = shape
     announce(f"fp8 matmul layouts agree {shape}")
     gen = np.random.default_rng(m + 3 * n + 5 * k)
