@@ -23,6 +23,14 @@ __device__ __forceinline__ i32x4_t raw_buffer_words(const void* base, uint32_t b
                    static_cast<int>(bytes), kRawBufferFormat};
 }
 
+/// A buffer descriptor in scalar registers: the DMA takes it as an SGPR
+/// operand; the value is wave-uniform, but the compiler cannot always prove
+/// it (and an "s" operand it holds in VGPRs does not assemble).
+__device__ __forceinline__ i32x4_t uniform(i32x4_t v) {
+    return i32x4_t{__builtin_amdgcn_readfirstlane(v[0]), __builtin_amdgcn_readfirstlane(v[1]),
+                   __builtin_amdgcn_readfirstlane(v[2]), __builtin_amdgcn_readfirstlane(v[3])};
+}
+
 /// HBM -> LDS copy of 16 (or 4) bytes per lane: lane l's bytes land at LDS
 /// byte lds_dst + 16 l (4 l), read from buffer offset voffset + soffset
 /// (zeros when out of range). Issued from inline assembly on purpose: the

@@ -94,13 +94,6 @@ __device__ __forceinline__ i32x2_t lds_read_tr8(const uint8_t* base, int offset)
         (lds_i32x2_t*)((lds_u8_t*)(const_cast<uint8_t*>(base)) + offset));
 }
 
-/// The descriptor in scalar registers (the DMA takes it as an SGPR operand;
-/// the value is wave-uniform, but the compiler cannot always prove it).
-__device__ __forceinline__ i32x4_t uniform(i32x4_t v) {
-    return i32x4_t{__builtin_amdgcn_readfirstlane(v[0]), __builtin_amdgcn_readfirstlane(v[1]),
-                   __builtin_amdgcn_readfirstlane(v[2]), __builtin_amdgcn_readfirstlane(v[3])};
-}
-
 struct Fp8Args {
     const uint8_t* x;
     const uint8_t* w;
