@@ -420,15 +420,18 @@ void matmul_fp8_kernel(Fp8Args args) {
     }
 }
 
-// ---- One wave per SIMD (K-major operands) --------------------------------
+// ---- One wave per SIMD ------------------------------------------------------
 // matmul_fp8_w4_kernel: the same 256x256 output tile with four waves, each
 // owning a 128x128 sub-tile as 4x4 v_mfma_scale_f32_32x32x64_f8f6f4
 // accumulators (256 fp32 per lane, in the accumulation registers; one wave
 // per SIMD has 512 registers). Per MFMA this reads half the LDS bytes of a
 // 64x128 sub-tile and issues half the scalar and barrier work per SIMD.
-//   * K-tiles of 128 bytes, double-buffered in LDS for both operands: x and
-//     w_t rows as whole 128-byte lines (32 KiB per operand and slot, the x
-//     swizzle), every wave copying 64 rows of each (16 DMA per K-tile).
+//   * K-tiles of 128 bytes, double-buffered in LDS for both operands
+//     (32 KiB per operand and slot): x as whole 128-byte row lines (the x
+//     swizzle); w_t (kWT) the same way, or w [K, N] as 128 k-rows of the
+//     tile's 256 columns (the w swizzle), read transposed as in the
+//     eight-wave kernel. Every wave copies a quarter of each (16 DMA per
+//     K-tile).
 //   * Fragments double-buffered in registers by K-half: the 16 MFMAs of one
 //     half issue while the fragments of the next half are read.
 //   * One barrier per K-tile, between its halves: by then every wave has
@@ -450,6 +453,7 @@ constexpr int64_t kW4MinK = 2048;
 /// s_waitcnt immediate that waits for every LDS operation of this wave.
 constexpr int lgkmcnt0_imm() { return 15 | (3 << 14) | (7 << 4); }
 
+template <bool kWT>
 __global__ __launch_bounds__(kW4Threads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void matmul_fp8_w4_kernel(Fp8Args args) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kW4Lds];
@@ -477,22 +481,42 @@ void matmul_fp8_w4_kernel(Fp8Args args) {
     const int64_t rows_here = M - m0 < kBM ? M - m0 : kBM;
     const int64_t cols_here = N - n0 < kBN ? N - n0 : kBN;
     const i32x4_t xbuf = uniform(raw_buffer_words(args.x + m0 * K, static_cast<uint32_t>(rows_here * K)));
-    const i32x4_t wbuf = uniform(raw_buffer_words(args.w + n0 * K, static_cast<uint32_t>(cols_here * K)));
+    const i32x4_t wbuf = kWT ? uniform(raw_buffer_words(args.w + n0 * K, static_cast<uint32_t>(cols_here * K)))
+                             : uniform(raw_buffer_words(args.w, static_cast<uint32_t>(K * N)));
     uint32_t dma_off[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         const int row = 64 * wave + 8 * b + (lane >> 3);
         dma_off[b] = static_cast<uint32_t>(row * K + (((lane & 7) ^ x_swizzle(row)) << 4));
     }
+    // w [K, N] (kWT false): load i (0..7) copies k rows 32 wave + 4 i + l / 16
+    // of the K-tile, physical chunk l % 16 (16 columns). The swizzle takes row
+    // bits 0-2, i.e. l / 16 and bit 0 of i, so two lane offsets serve the
+    // eight loads; 8 (i / 2) rows go into the scalar offset. Columns past N
+    // read as zero (the out-of-range marker plus a scalar offset below 2^31
+    // stays out of range).
+    uint32_t wkn_off[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int row = 32 * wave + 4 * b + (lane >> 4);
+        const int64_t col = n0 + 16 * ((lane & 15) ^ w_swizzle(row));
+        wkn_off[b] = col < N ? static_cast<uint32_t>(row * N + col) : kOutOfRange;
+    }
     const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)lds));
     const uint32_t k16 = static_cast<uint32_t>(16 * K);
-    // Load s (0..15) of K-tile t: x for even s, w_t for odd, row group s / 2.
+    // Load s (0..15) of K-tile t: x for even s, w for odd, load s / 2 of
+    // the operand (both layouts fill 1 KiB at 8192 wave + 1024 i of the slot).
     auto issue_load = [&](int t, int slot, int s) {
         const int i = s >> 1;
         const uint32_t dst = lds_addr + static_cast<uint32_t>(slot * kW4Slot + wave * 8192 + i * 1024) +
                              ((s & 1) ? kW4OffW : 0);
-        const uint32_t sofs = static_cast<uint32_t>(t) * (2 * kBK) + static_cast<uint32_t>(i >> 1) * k16;
-        dma16_m0((s & 1) ? wbuf : xbuf, dst, dma_off[i & 1], sofs);
+        if (kWT || (s & 1) == 0) {
+            const uint32_t sofs = static_cast<uint32_t>(t) * (2 * kBK) + static_cast<uint32_t>(i >> 1) * k16;
+            dma16_m0((s & 1) ? wbuf : xbuf, dst, dma_off[i & 1], sofs);
+        } else {
+            const uint32_t sofs = static_cast<uint32_t>((static_cast<int64_t>(t) * (2 * kBK) + 8 * (i >> 1)) * N);
+            dma16_m0(wbuf, dst, wkn_off[i & 1], sofs);
+        }
     };
 
     // ---- LDS -> registers: block i of x (B operand) is tile row
@@ -506,6 +530,29 @@ void matmul_fp8_w4_kernel(Fp8Args args) {
     const int rd1 = (lane & 31) * (2 * kBK) + (((2 * h + 1) ^ sw) << 4);
     const int x_base = wm * 128 * (2 * kBK);
     const int w_base = kW4OffW + wn * 128 * (2 * kBK);
+    // w [K, N] (A operand, transposed read), column block jb of the wave:
+    // lane l receives column wn*128 + 32 jb + l % 32, k = 32 (l / 32) + 8 r + e
+    // of the K-half (byte e of read r), as in the eight-wave kernel; the
+    // second K-half is 64 k-rows further (the swizzle takes row bits 0-2).
+    const int g = lane >> 4;
+    const int jl = lane & 15;
+    int wkn_rd[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+        const int row = 32 * (g >> 1) + (jl >> 1);
+        const int chunk = wn * 8 + 2 * jb + (g & 1);
+        wkn_rd[jb] = row * kBN + ((chunk ^ w_swizzle(row)) << 4) + (jl & 1) * 8;
+    }
+    auto read_a = [&](int slot, int half, int j) -> i32x8_t {
+        const uint8_t* sw = lds + kW4OffW + slot * kW4Slot + half * 64 * kBN;
+        const i32x2_t r0 = lds_read_tr8(sw, wkn_rd[j]);
+        const i32x2_t r1 = lds_read_tr8(sw, wkn_rd[j] + 8 * kBN);
+        const i32x2_t r2 = lds_read_tr8(sw, wkn_rd[j] + 16 * kBN);
+        const i32x2_t r3 = lds_read_tr8(sw, wkn_rd[j] + 24 * kBN);
+        const i32x4v_t lo = __builtin_shufflevector(r0, r1, 0, 1, 2, 3);
+        const i32x4v_t hi = __builtin_shufflevector(r2, r3, 0, 1, 2, 3);
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
 
     struct Frags {
         i32x8_t a[4];  // w_t blocks jb
@@ -525,7 +572,11 @@ void matmul_fp8_w4_kernel(Fp8Args args) {
             f.b[r - 1] = read_pair(x_base + slot * kW4Slot + (r - 1) * 32 * (2 * kBK), half);
         } else {
             const int j = r == 0 ? 0 : r - 4;
-            f.a[j] = read_pair(w_base + slot * kW4Slot + j * 32 * (2 * kBK), half);
+            if constexpr (kWT) {
+                f.a[j] = read_pair(w_base + slot * kW4Slot + j * 32 * (2 * kBK), half);
+            } else {
+                f.a[j] = read_a(slot, half, j);
+            }
         }
     };
 
@@ -635,6 +686,24 @@ void matmul_fp8_w4_kernel(Fp8Args args) {
 }
 
 template <bool kWT>
+cf_status launch_fp8_w4(const char* name, const void* x, const void* w, void* y, int64_t m, int64_t n,
+                        int64_t k, float scale, void* stream) {
+    Fp8Args args;
+    args.x = static_cast<const uint8_t*>(x);
+    args.w = static_cast<const uint8_t*>(w);
+    args.y = static_cast<uint16_t*>(y);
+    args.M = m;
+    args.N = n;
+    args.K = k;
+    args.scale = scale;
+    args.tiles_m = static_cast<int>(ceil_div<int64_t>(m, kBM));
+    args.tiles_n = static_cast<int>(ceil_div<int64_t>(n, kBN));
+    auto s = static_cast<hipStream_t>(stream);
+    launch(matmul_fp8_w4_kernel<kWT>, dim3(args.tiles_m * args.tiles_n), dim3(kW4Threads), 0, s, args);
+    return check_launch(name, s);
+}
+
+template <bool kWT>
 cf_status launch_fp8(const char* name, const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k,
                      float scale, void* stream) {
     Fp8Args args;
@@ -696,7 +765,11 @@ cf_status cf_matmul_fp8(const void* x, const void* w, void* y, int64_t m, int64_
     CF_ENTRY();
     const cf_status st = cf::validate_fp8("cf_matmul_fp8", cf_matmul_fp8_shape_supported(m, n, k), x, w, y, m, n, k);
     if (st != CF_OK) return st;
-    return cf::launch_fp8<false>("launching the fp8 MFMA matmul", x, w, y, m, n, k, scale, stream);
+    if (k <= cf::kW4MinK) {
+        return cf::launch_fp8<false>("launching the fp8 MFMA matmul", x, w, y, m, n, k, scale, stream);
+    }
+    return cf::launch_fp8_w4<false>("launching the fp8 MFMA matmul (one wave per SIMD)", x, w, y, m, n, k, scale,
+                                    stream);
 }
 
 cf_status cf_matmul_fp8_wt(const void* x, const void* w_t, void* y, int64_t m, int64_t n, int64_t k, float scale,
@@ -708,19 +781,8 @@ cf_status cf_matmul_fp8_wt(const void* x, const void* w_t, void* y, int64_t m, i
     if (k <= cf::kW4MinK) {
         return cf::launch_fp8<true>("launching the fp8 MFMA matmul (K-major w)", x, w_t, y, m, n, k, scale, stream);
     }
-    cf::Fp8Args args;
-    args.x = static_cast<const uint8_t*>(x);
-    args.w = static_cast<const uint8_t*>(w_t);
-    args.y = static_cast<uint16_t*>(y);
-    args.M = m;
-    args.N = n;
-    args.K = k;
-    args.scale = scale;
-    args.tiles_m = static_cast<int>(cf::ceil_div<int64_t>(m, cf::kBM));
-    args.tiles_n = static_cast<int>(cf::ceil_div<int64_t>(n, cf::kBN));
-    auto s = static_cast<hipStream_t>(stream);
-    cf::launch(cf::matmul_fp8_w4_kernel, dim3(args.tiles_m * args.tiles_n), dim3(cf::kW4Threads), 0, s, args);
-    return cf::check_launch("launching the fp8 MFMA matmul (K-major w, one wave per SIMD)", s);
+    return cf::launch_fp8_w4<true>("launching the fp8 MFMA matmul (K-major w, one wave per SIMD)", x, w_t, y, m, n,
+                                   k, scale, stream);
 }
 
 }  // extern "C"
