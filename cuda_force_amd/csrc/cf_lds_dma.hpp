@@ -67,6 +67,15 @@ __device__ __forceinline__ void dma16_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_
                  : "memory");
 }
 
+/// dma4 (4 bytes per lane) in the form of dma16_m0.
+__device__ __forceinline__ void dma4_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
+                                        uint32_t soffset) {
+    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds"
+                 :
+                 : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_dst)
+                 : "memory");
+}
+
 __device__ __forceinline__ void dma4(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
                                      uint32_t soffset) {
     int saved_m0;

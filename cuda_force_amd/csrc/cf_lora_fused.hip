@@ -376,17 +376,17 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         const int64_t k0 = k_first + kt * kBK;
         if (piece < 4) {
             const int vw = (wave & 3) + 4 * (piece >> 1);
-            dma16(wbuf, stage + (vw * 2 + (piece & 1)) * 1024, w_dma[piece],
+            dma16_m0(wbuf, stage + (vw * 2 + (piece & 1)) * 1024, w_dma[piece],
                   static_cast<uint32_t>(k0 * N * 2));
         } else if (kAdapter) {
-            dma4(abuf, stage + kTileW + (wave & 3) * 256, a_dma,
+            dma4_m0(abuf, stage + kTileW + (wave & 3) * 256, a_dma,
                  static_cast<uint32_t>(k0 * rank * 2));
         }
     };
     auto issue_x = [&](int64_t pair, int piece) {
         const uint32_t slot = lds_addr + static_cast<uint32_t>(pair % kXSlots) * kXPair;
         const int vw = (wave & 3) + 4 * (piece >> 2);
-        dma16(xbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
+        dma16_m0(xbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
               static_cast<uint32_t>(k_first * 2 + pair * 4 * kBK));
     };
     constexpr int kWLoads = kAdapter ? 5 : 4;  // w (+ a) DMA per K-step per issuing wave
@@ -486,7 +486,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         const int64_t col = n0 + 8 * ((lane & 31) ^ b_swizzle(row));
         const uint32_t off =
             row < rank && col < N ? static_cast<uint32_t>((row * N + col) * 2) : kOutOfRange;
-        dma16(bbuf, lds_addr + kOffB + wave * 1024, off, 0);
+        dma16_m0(bbuf, lds_addr + kOffB + wave * 1024, off, 0);
     }
     // The K-loop, instantiated for issuing (waves 0-3) and non-issuing waves;
     // the latter wait for nothing but the barriers (their vmcnt waits find
