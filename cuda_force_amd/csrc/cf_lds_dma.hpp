@@ -38,27 +38,12 @@ __device__ __forceinline__ i32x4_t uniform(i32x4_t v) {
 /// each transposed LDS read it emits, which would serialise the prefetch
 /// pipeline; DMA it does not know about cannot trigger that. The caller
 /// orders the copies itself (s_waitcnt vmcnt + barrier before the stage is
-/// read); compiler-generated vmcnt waits only become more conservative. M0
-/// (the LDS base register of the copy) is restored afterwards.
-__device__ __forceinline__ void dma16(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
-                                      uint32_t soffset) {
-    int saved_m0;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved_m0)
-        : "s"(lds_dst), "v"(voffset), "s"(rsrc), "s"(soffset)
-        : "memory");
-}
-
-/// dma16 with the LDS base handed to the compiler as an M0 operand instead of
-/// being saved, set and restored inside the assembly: the compiler writes M0
-/// itself (one scalar instruction, often folded into the address add) and
-/// knows its value afterwards. The s_nop covers the one wait state an M0
-/// write needs before an LDS DMA reads it.
+/// read); compiler-generated vmcnt waits only become more conservative.
+/// The LDS base travels as an M0 operand: the compiler writes M0 itself (one
+/// scalar instruction, often folded into the address add) and knows its
+/// value afterwards, so nothing is saved or restored around the copy. The
+/// s_nop covers the one wait state an M0 write needs before an LDS DMA
+/// reads it.
 __device__ __forceinline__ void dma16_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
                                          uint32_t soffset) {
     asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
@@ -67,27 +52,12 @@ __device__ __forceinline__ void dma16_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_
                  : "memory");
 }
 
-/// dma4 (4 bytes per lane) in the form of dma16_m0.
 __device__ __forceinline__ void dma4_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
                                         uint32_t soffset) {
     asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds"
                  :
                  : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_dst)
                  : "memory");
-}
-
-__device__ __forceinline__ void dma4(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
-                                     uint32_t soffset) {
-    int saved_m0;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dword %2, %3, %4 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved_m0)
-        : "s"(lds_dst), "v"(voffset), "s"(rsrc), "s"(soffset)
-        : "memory");
 }
 
 /// Workgroup barrier that neither waits on memory counters nor lets the

@@ -165,19 +165,19 @@ void matmul_fp8_kernel(Fp8Args args) {
         if constexpr (kWT) {
             const uint32_t slot = lds_addr + kOffW + static_cast<uint32_t>(t % kXSlots) * kXPair;
             const int vw = (wave & 3) + 4 * (piece >> 2);
-            dma16(wbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
+            dma16_m0(wbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
                   static_cast<uint32_t>(t * 2 * kBK));
         } else {
             const uint32_t stage = lds_addr + kOffW + static_cast<uint32_t>(t % kStages) * kTileW;
             const int vw = (wave & 3) + 4 * (piece >> 1);
-            dma16(wbuf, stage + (vw * 2 + (piece & 1)) * 1024, w_dma[piece],
+            dma16_m0(wbuf, stage + (vw * 2 + (piece & 1)) * 1024, w_dma[piece],
                   static_cast<uint32_t>(t * kBK * N));
         }
     };
     auto issue_x = [&](int64_t pair, int piece) {
         const uint32_t slot = lds_addr + static_cast<uint32_t>(pair % kXSlots) * kXPair;
         const int vw = (wave & 3) + 4 * (piece >> 2);
-        dma16(xbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
+        dma16_m0(xbuf, slot + vw * 4096 + (piece & 3) * 1024, x_dma[piece],
               static_cast<uint32_t>(pair * 2 * kBK));
     };
     constexpr int kWLoads = kWT ? 8 : 4;  // w DMA per pair of K-steps (w_t) or per K-step, per issuing wave
