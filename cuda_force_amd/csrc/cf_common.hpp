@@ -199,6 +199,19 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_v));
 }
 
+/// The bf16 high/low split of two fp32 values, hi = bf16(v) and
+/// lo = bf16(v - hi), as packed words (first value in the low half), for the
+/// kernels that run fp32 products as three bf16 MFMAs (hi*hi + hi*lo +
+/// lo*hi). Two v_cvt_pk_bf16_f32 do the rounding: bit-identical to
+/// f32_to_bf16_bits except that a NaN keeps its payload, which changes
+/// nothing downstream (a NaN element gives NaN products either way). One
+/// conversion per two values instead of the software rounding's several
+/// instructions per value: these kernels spend their VALU time on the split.
+__device__ __forceinline__ void split_pk(float v0, float v1, uint32_t& hi, uint32_t& lo) {
+    hi = f32x2_to_bf16x2_bits(v0, v1);
+    lo = f32x2_to_bf16x2_bits(v0 - __uint_as_float(hi << 16), v1 - __uint_as_float(hi & 0xFFFF0000u));
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
 }

@@ -88,12 +88,6 @@ struct F32Args {
     int want_xa;  // write x @ a (to xa_out or xa_part)
 };
 
-/// hi = bf16(v), lo = bf16(v - hi), as bits.
-__device__ __forceinline__ void split2(float v, uint32_t& hi, uint32_t& lo) {
-    hi = f32_to_bf16_bits(v);
-    lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
-}
-
 __device__ __forceinline__ s16x4_t lds_read_tr(const uint8_t* base, int offset) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (lds_s16x4_t*)((lds_u8_t*)(const_cast<uint8_t*>(base)) + offset));
@@ -191,38 +185,36 @@ __global__ __launch_bounds__(kThreads) void lora_f32_kernel(F32Args args) {
             const int idx = tid + 256 * i;
             const int row = idx >> 3;
             const int k = 4 * (idx & 7);
-            const float v[4] = {st.x[i].x, st.x[i].y, st.x[i].z, st.x[i].w};
-            uint32_t hi[4];
-            uint32_t lo[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) split2(v[e], hi[e], lo[e]);
+            uint2 hi;
+            uint2 lo;
+            split_pk(st.x[i].x, st.x[i].y, hi.x, lo.x);
+            split_pk(st.x[i].z, st.x[i].w, hi.y, lo.y);
             const int off = x_offset(row, k);
-            *reinterpret_cast<uint2*>(base + kOffXHi + off) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-            *reinterpret_cast<uint2*>(base + kOffXLo + off) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
+            *reinterpret_cast<uint2*>(base + kOffXHi + off) = hi;
+            *reinterpret_cast<uint2*>(base + kOffXLo + off) = lo;
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 256 * i;
             const int krow = idx >> 4;
             const int col = 4 * (idx & 15);
-            const float v[4] = {st.w[i].x, st.w[i].y, st.w[i].z, st.w[i].w};
-            uint32_t hi[4];
-            uint32_t lo[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) split2(v[e], hi[e], lo[e]);
+            uint2 hi;
+            uint2 lo;
+            split_pk(st.w[i].x, st.w[i].y, hi.x, lo.x);
+            split_pk(st.w[i].z, st.w[i].w, hi.y, lo.y);
             const int off = krow * (kTN * 2) + col * 2;
-            *reinterpret_cast<uint2*>(base + kOffWHi + off) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-            *reinterpret_cast<uint2*>(base + kOffWLo + off) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
+            *reinterpret_cast<uint2*>(base + kOffWHi + off) = hi;
+            *reinterpret_cast<uint2*>(base + kOffWLo + off) = lo;
         }
+        uint32_t ahi;
+        uint32_t alo;
+        split_pk(st.a[0], st.a[1], ahi, alo);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 256 * i;
-            uint32_t hi;
-            uint32_t lo;
-            split2(st.a[i], hi, lo);
             const int off = a_offset(idx >> 4, (idx & 15) * 2);
-            *reinterpret_cast<uint16_t*>(base + kOffAHi + off) = static_cast<uint16_t>(hi);
-            *reinterpret_cast<uint16_t*>(base + kOffALo + off) = static_cast<uint16_t>(lo);
+            *reinterpret_cast<uint16_t*>(base + kOffAHi + off) = static_cast<uint16_t>(ahi >> (16 * i));
+            *reinterpret_cast<uint16_t*>(base + kOffALo + off) = static_cast<uint16_t>(alo >> (16 * i));
         }
     };
 
@@ -288,27 +280,21 @@ __global__ __launch_bounds__(kThreads) void lora_f32_kernel(F32Args args) {
         const bool ok = j < rank && col < N;
         const __amdgpu_buffer_rsrc_t bbuf = make_buffer(args.b, static_cast<uint32_t>(rank * N * 4));
         const uint4 v = buffer_load16(bbuf, ok ? static_cast<uint32_t>((j * N + col) * 4) : 0x80000000u, 0);
-        const float vals[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
-                               __uint_as_float(v.w)};
-        uint32_t hi[4];
-        uint32_t lo[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) split2(vals[e], hi[e], lo[e]);
+        uint2 hi;
+        uint2 lo;
+        split_pk(__uint_as_float(v.x), __uint_as_float(v.y), hi.x, lo.x);
+        split_pk(__uint_as_float(v.z), __uint_as_float(v.w), hi.y, lo.y);
         const int off = j * (kTN * 2) + 8 * (tid & 15);
-        *reinterpret_cast<uint2*>(lds + kOffBHi + off) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-        *reinterpret_cast<uint2*>(lds + kOffBLo + off) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
+        *reinterpret_cast<uint2*>(lds + kOffBHi + off) = hi;
+        *reinterpret_cast<uint2*>(lds + kOffBLo + off) = lo;
     }
     __syncthreads();
-    s16x4_t uh;
-    s16x4_t ul;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        uint32_t hi;
-        uint32_t lo;
-        split2(args.scale * xacc[t], hi, lo);
-        uh[t] = static_cast<short>(hi);
-        ul[t] = static_cast<short>(lo);
-    }
+    uint2 uhw;
+    uint2 ulw;
+    split_pk(args.scale * xacc[0], args.scale * xacc[1], uhw.x, ulw.x);
+    split_pk(args.scale * xacc[2], args.scale * xacc[3], uhw.y, ulw.y);
+    const s16x4_t uh = __builtin_bit_cast(s16x4_t, uhw);
+    const s16x4_t ul = __builtin_bit_cast(s16x4_t, ulw);
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
         const int row = 4 * g + (jl >> 2);
