@@ -68,11 +68,6 @@ struct Args {
     int n_tiles;
 };
 
-__device__ __forceinline__ void split2(float v, uint32_t& hi, uint32_t& lo) {
-    hi = f32_to_bf16_bits(v);
-    lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
-}
-
 __device__ __forceinline__ int a_offset(int row, int k) {
     return row * (kTK * 2) + ((((k >> 3) ^ (row >> 2)) & 3) << 4) + (k & 7) * 2;
 }
@@ -94,15 +89,13 @@ __device__ __forceinline__ bf16x8_t concat(s16x4_t lo, s16x4_t hi) {
     return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+/// The four values' bf16 high parts (returned) and low parts (lo_out),
+/// packed two per word.
 __device__ __forceinline__ uint2 pack_hi_lo(const float4& v, uint2& lo_out) {
-    uint32_t h[4];
-    uint32_t l[4];
-    split2(v.x, h[0], l[0]);
-    split2(v.y, h[1], l[1]);
-    split2(v.z, h[2], l[2]);
-    split2(v.w, h[3], l[3]);
-    lo_out = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
-    return make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    uint2 hi;
+    split_pk(v.x, v.y, hi.x, lo_out.x);
+    split_pk(v.z, v.w, hi.y, lo_out.y);
+    return hi;
 }
 
 __device__ __forceinline__ float4 as_float4(const uint4& v) {

@@ -89,11 +89,6 @@ __global__ void sum_splits_kernel(const float4* __restrict__ part, float4* __res
     }
 }
 
-__device__ __forceinline__ void split_bf16(float a, uint32_t& hi, uint32_t& lo) {
-    hi = f32_to_bf16_bits(a);
-    lo = f32_to_bf16_bits(a - __uint_as_float(hi << 16));
-}
-
 /// A' [m][3 kp] element quad q (4 consecutive columns of one row).
 __device__ __forceinline__ void split_row_quad(const float* __restrict__ a, uint16_t* __restrict__ out,
                                                int64_t k, int64_t kp, int64_t q) {
@@ -102,19 +97,14 @@ __device__ __forceinline__ void split_row_quad(const float* __restrict__ a, uint
     const int64_t col = (q % quads_per_row) * 4;
     const int64_t part = col / kp;  // 0, 1: hi; 2: lo
     const int64_t j = col % kp;
-    uint32_t bits[4];
+    float v[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float v = j + e < k ? a[row * k + j + e] : 0.0f;
-        uint32_t hi;
-        uint32_t lo;
-        split_bf16(v, hi, lo);
-        bits[e] = part == 2 ? lo : hi;
-    }
-    uint2 packed;
-    packed.x = bits[0] | (bits[1] << 16);
-    packed.y = bits[2] | (bits[3] << 16);
-    *reinterpret_cast<uint2*>(out + row * 3 * kp + col) = packed;
+    for (int e = 0; e < 4; ++e) v[e] = j + e < k ? a[row * k + j + e] : 0.0f;
+    uint2 hi;
+    uint2 lo;
+    split_pk(v[0], v[1], hi.x, lo.x);
+    split_pk(v[2], v[3], hi.y, lo.y);
+    *reinterpret_cast<uint2*>(out + row * 3 * kp + col) = part == 2 ? lo : hi;
 }
 
 /// B' [3 kp][n] element quad q (4 consecutive columns of one row).
@@ -127,19 +117,11 @@ __device__ __forceinline__ void split_col_quad(const float* __restrict__ b, uint
     const int64_t j = row % kp;
     float4 v = float4{0.0f, 0.0f, 0.0f, 0.0f};
     if (j < k) v = *reinterpret_cast<const float4*>(b + j * n + col);
-    const float vals[4] = {v.x, v.y, v.z, v.w};
-    uint32_t bits[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        uint32_t hi;
-        uint32_t lo;
-        split_bf16(vals[e], hi, lo);
-        bits[e] = part == 1 ? lo : hi;
-    }
-    uint2 packed;
-    packed.x = bits[0] | (bits[1] << 16);
-    packed.y = bits[2] | (bits[3] << 16);
-    *reinterpret_cast<uint2*>(out + row * n + col) = packed;
+    uint2 hi;
+    uint2 lo;
+    split_pk(v.x, v.y, hi.x, lo.x);
+    split_pk(v.z, v.w, hi.y, lo.y);
+    *reinterpret_cast<uint2*>(out + row * n + col) = part == 1 ? lo : hi;
 }
 
 /// Both operand splits in one launch: quads [0, a_quads) of the grid-stride
