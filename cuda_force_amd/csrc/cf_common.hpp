@@ -199,6 +199,16 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_v));
 }
 
+/// f32_to_bf16_bits of two values, packed (first value in the low half):
+/// bit-identical on every input, NaN -> 0x7FC0 included. NaNs are replaced by
+/// the canonical quiet NaN before one v_cvt_pk_bf16_f32 (which would keep a
+/// payload): about 2.5 VALU instructions per value against the software
+/// rounding's 6, for epilogues that round whole output tiles.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_canon(float lo, float hi) {
+    const float canon = __uint_as_float(0x7FC00000u);
+    return f32x2_to_bf16x2_bits(lo != lo ? canon : lo, hi != hi ? canon : hi);
+}
+
 /// The bf16 high/low split of two fp32 values, hi = bf16(v) and
 /// lo = bf16(v - hi), as packed words (first value in the low half), for the
 /// kernels that run fp32 products as three bf16 MFMAs (hi*hi + hi*lo +

@@ -170,8 +170,8 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
         for (int t = 0; t < 2; ++t) {
             const int rb = wm * 4 + wn * 2 + t;
             uint2 packed;
-            packed.x = f32_to_bf16_bits(xacc[t][0]) | (f32_to_bf16_bits(xacc[t][1]) << 16);
-            packed.y = f32_to_bf16_bits(xacc[t][2]) | (f32_to_bf16_bits(xacc[t][3]) << 16);
+            packed.x = f32x2_to_bf16x2_canon(xacc[t][0], xacc[t][1]);
+            packed.y = f32x2_to_bf16x2_canon(xacc[t][2], xacc[t][3]);
             xa_lds[rb * 64 + lane] = packed;
             const int64_t row = m0 + rb * 16 + jl;
             if (write_xa && row < M) {
@@ -250,8 +250,8 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
             for (int jb = 0; jb < 8; ++jb) {
                 const int chunk = 2 * jb + (g >> 1);
                 uint2 packed;
-                packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
-                packed.y = f32_to_bf16_bits(acc[jb][i][2]) | (f32_to_bf16_bits(acc[jb][i][3]) << 16);
+                packed.x = f32x2_to_bf16x2_canon(acc[jb][i][0], acc[jb][i][1]);
+                packed.y = f32x2_to_bf16x2_canon(acc[jb][i][2], acc[jb][i][3]);
                 *reinterpret_cast<uint2*>(stage + row * 256 + ((chunk ^ (row & 15)) << 4) +
                                           (g & 1) * 8) = packed;
             }
@@ -288,8 +288,8 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
                                             row * N + col) = acc[jb][i];
             } else if (col < N) {
                 uint2 packed;
-                packed.x = f32_to_bf16_bits(acc[jb][i][0]) | (f32_to_bf16_bits(acc[jb][i][1]) << 16);
-                packed.y = f32_to_bf16_bits(acc[jb][i][2]) | (f32_to_bf16_bits(acc[jb][i][3]) << 16);
+                packed.x = f32x2_to_bf16x2_canon(acc[jb][i][0], acc[jb][i][1]);
+                packed.y = f32x2_to_bf16x2_canon(acc[jb][i][2], acc[jb][i][3]);
                 *reinterpret_cast<uint2*>(yrow + col) = packed;
             }
         }

@@ -398,8 +398,8 @@ void matmul_fp8_kernel(Fp8Args args) {
             for (int q = 0; q < 4; ++q) {
                 const int c = 4 * jb + q;
                 uint2 packed;
-                packed.x = f32_to_bf16_bits(scale * a[4 * q]) | (f32_to_bf16_bits(scale * a[4 * q + 1]) << 16);
-                packed.y = f32_to_bf16_bits(scale * a[4 * q + 2]) | (f32_to_bf16_bits(scale * a[4 * q + 3]) << 16);
+                packed.x = f32x2_to_bf16x2_canon(scale * a[4 * q], scale * a[4 * q + 1]);
+                packed.y = f32x2_to_bf16x2_canon(scale * a[4 * q + 2], scale * a[4 * q + 3]);
                 *reinterpret_cast<uint2*>(stage + r * 256 + ((c ^ (r & 15)) << 4) + ((h ^ flip) << 3)) = packed;
             }
         }
@@ -665,8 +665,8 @@ void matmul_fp8_w4_kernel(Fp8Args args) {
             for (int q = 0; q < 4; ++q) {
                 const int c = 4 * jb + q;
                 uint2 packed;
-                packed.x = f32_to_bf16_bits(scale * a[4 * q]) | (f32_to_bf16_bits(scale * a[4 * q + 1]) << 16);
-                packed.y = f32_to_bf16_bits(scale * a[4 * q + 2]) | (f32_to_bf16_bits(scale * a[4 * q + 3]) << 16);
+                packed.x = f32x2_to_bf16x2_canon(scale * a[4 * q], scale * a[4 * q + 1]);
+                packed.y = f32x2_to_bf16x2_canon(scale * a[4 * q + 2], scale * a[4 * q + 3]);
                 *reinterpret_cast<uint2*>(stage + r * 256 + ((c ^ (r & 15)) << 4) + ((h ^ flip) << 3)) = packed;
             }
         }
