@@ -667,16 +667,21 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
         const float m_new = fmaxf(m, cmax);
         const float c = m == -INFINITY ? 0.0f : __expf(m - m_new);
         m = m_new;
+        // Probabilities rounded to bf16 two at a time (v_cvt_pk_bf16_f32; a
+        // NaN keeps its payload here and the output rounding canonicalises
+        // it).
         s16x4_m pb[kSubs];
         float psum = 0.0f;
 #pragma unroll
         for (int u = 0; u < kSubs; ++u) {
+            float pt[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const float pt = sc[u][t] == -INFINITY ? 0.0f : __expf(sc[u][t] - m_new);
-                psum += pt;
-                pb[u][t] = static_cast<short>(f32_to_bf16_bits(pt));
+                pt[t] = sc[u][t] == -INFINITY ? 0.0f : __expf(sc[u][t] - m_new);
+                psum += pt[t];
             }
+            pb[u] = __builtin_bit_cast(s16x4_m, make_uint2(f32x2_to_bf16x2_bits(pt[0], pt[1]),
+                                                           f32x2_to_bf16x2_bits(pt[2], pt[3])));
         }
         l = l * c + psum;
 #pragma unroll
