@@ -33,7 +33,11 @@ __device__ __forceinline__ i32x4_t uniform(i32x4_t v) {
 
 /// HBM -> LDS copy of 16 (or 4) bytes per lane: lane l's bytes land at LDS
 /// byte lds_dst + 16 l (4 l), read from buffer offset voffset + soffset
-/// (zeros when out of range). Issued from inline assembly on purpose: the
+/// (zeros when out of range). On gfx950 the range check takes the sum: a lane
+/// whose voffset is in range reads zeros once soffset carries it past the
+/// buffer's size, for these copies and for plain buffer loads alike
+/// (measured with in-bounds offsets), so a row offset may travel in soffset
+/// and still be clipped at the buffer's end. Issued from inline assembly on purpose: the
 /// compiler conservatively drains every LDS DMA in flight (vmcnt(0)) before
 /// each transposed LDS read it emits, which would serialise the prefetch
 /// pipeline; DMA it does not know about cannot trigger that. The caller
