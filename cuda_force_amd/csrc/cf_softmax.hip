@@ -35,6 +35,8 @@
 // so a causal score matrix is read about half, and written whole.
 #include "cf_common.hpp"
 
+#include <type_traits>
+
 namespace cf {
 namespace {
 
@@ -53,8 +55,8 @@ __device__ __forceinline__ void store_vec(Tout* p, const float* v) {
         // 4 values into a 16-bit type: one 8-byte store.
         static_assert(kN == 4 && kOutPer == 8, "unsupported store width");
         uint2 w;
-        w.x = Storage<Tout>::to_bits(v[0]) | (Storage<Tout>::to_bits(v[1]) << 16);
-        w.y = Storage<Tout>::to_bits(v[2]) | (Storage<Tout>::to_bits(v[3]) << 16);
+        w.x = Storage<Tout>::to_bits2(v[0], v[1]);
+        w.y = Storage<Tout>::to_bits2(v[2], v[3]);
         store_stream8(p, w);
     }
 }
@@ -92,6 +94,30 @@ __device__ __forceinline__ uint4 buffer_load_stream16(__amdgpu_buffer_rsrc_t rsr
 /// next): rows past the end are loaded from the last row and not stored,
 /// and with kFullCols every lane's vectors are inside the row; otherwise
 /// the missing columns are replaced by -inf after the load.
+/// store_vec for a row's probabilities e * (1 / sum). Each e is in [0, 1]
+/// unless one of them is NaN, and then the sum is NaN and so is every value of
+/// the row; otherwise the sum is at least 1 (the maximum gives e = 1) and no
+/// value is NaN. So for bf16 a row whose 1 / sum is finite is rounded by
+/// v_cvt_pk_bf16_f32 alone, and a NaN row stores the canonical 0x7FC0: the
+/// bits of f32_to_bf16_bits either way, with no per-value NaN test.
+template <typename Tout, int kN>
+__device__ __forceinline__ void store_probs(Tout* p, const float* v, bool row_nan) {
+    if constexpr (std::is_same_v<Tout, bf16_t> && (kN == 8 || kN == 4)) {
+        uint32_t w[kN / 2];
+#pragma unroll
+        for (int i = 0; i < kN / 2; ++i) {
+            w[i] = row_nan ? 0x7FC07FC0u : f32x2_to_bf16x2_bits(v[2 * i], v[2 * i + 1]);
+        }
+        if constexpr (kN == 8) {
+            store_stream16(p, make_uint4(w[0], w[1], w[2], w[3]));
+        } else {
+            store_stream8(p, make_uint2(w[0], w[1]));
+        }
+    } else {
+        store_vec<Tout, kN>(p, v);
+    }
+}
+
 template <typename Tin, typename Tout, int kVecs, int kRows, bool kFullCols, bool kMasked>
 __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const Tin* x, Tout* y,
                                                                          int64_t rows,
@@ -175,6 +201,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
         }
         const float row_sum = wave_reduce_f32<AddF32>(partial[0] + partial[1]);
         const float inv_sum = 1.0f / row_sum;
+        const bool row_nan = inv_sum != inv_sum;
 
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
@@ -182,7 +209,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
             if (kFullCols || idx < vec_cols) {
 #pragma unroll
                 for (int i = 0; i < kPer; ++i) v[j][i] = v[j][i] * inv_sum;
-                store_vec<Tout, kPer>(y + row * cols + idx * kPer, v[j]);
+                store_probs<Tout, kPer>(y + row * cols + idx * kPer, v[j], row_nan);
             }
         }
     }
@@ -254,13 +281,14 @@ __global__ __launch_bounds__(kRowThreads) void softmax_row_kernel(const Tin* x, 
         }
         const float inv_sum =
             1.0f / block_reduce_f32<kRowThreads / kWaveSize, AddF32>(partial[0] + partial[1], slot);
+        const bool row_nan = inv_sum != inv_sum;
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
             const int64_t idx = static_cast<int64_t>(j) * kRowThreads + tid;
             if (kFullCols || idx < vec_cols) {
 #pragma unroll
                 for (int i = 0; i < kPer; ++i) v[j][i] = v[j][i] * inv_sum;
-                store_vec<Tout, kPer>(y + row * cols + idx * kPer, v[j]);
+                store_probs<Tout, kPer>(y + row * cols + idx * kPer, v[j], row_nan);
             }
         }
     }
