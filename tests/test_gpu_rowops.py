@@ -274,6 +274,32 @@ def test_softmax_bf16_logits_fp16_cannot_represent(cols):
     assert_close(oracle.f32_to_bf16_bits(y), oracle.softmax(g.host_values(x, "bf16")), "bf16", "softmax +-1e5")
 
 
+@pytest.mark.parametrize("in_dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("cols", [8, 512, 2048, 32768])
+def test_softmax_bf16_rows_that_turn_nan(in_dtype, cols):
+    """bf16 probabilities: a row holding NaN, +inf, or nothing but -inf is
+    NaN throughout (its sum is NaN), stored as the canonical 0x7FC0 of
+    c10::BFloat16's rounding, bit for bit, in every kernel width (two rows
+    per wave, one row per wave, a workgroup per row, fp32 logits through the
+    8-byte store); the finite rows around them match the oracle."""
+    g.announce(f"softmax bf16 NaN rows, {in_dtype} logits, {cols} columns")
+    rows = 4096 if cols <= 512 else 6  # 4096 rows of 512 bf16: two rows per wave, row 1 beside row 0
+    xf = (rng(cols + 3).standard_normal((rows, cols)) * 2).astype(np.float32)
+    xf[1, cols // 2] = np.nan
+    xf[3, cols - 1] = np.inf
+    xf[4, :] = -np.inf
+    x = g.storage_bits(xf, in_dtype)
+    y = run_softmax(x, in_dtype, "bf16")
+    for r in (1, 3, 4):
+        assert (y[r] == 0x7FC0).all(), f"row {r}: {np.unique(y[r])[:4]}"
+    finite = [r for r in range(rows) if r not in (1, 3, 4)]
+    assert_close(y[finite], oracle.softmax(g.host_values(x, in_dtype)[finite]), "bf16", "finite rows")
+    # The scaled entry point follows the same rule (no mask: period 0).
+    ys = run_softmax_scaled(x, in_dtype, "bf16", 0.5, 0)
+    for r in (1, 3, 4):
+        assert (ys[r] == 0x7FC0).all(), f"scaled row {r}"
+
+
 def test_softmax_bf16_logits_to_fp32_probabilities_and_misaligned():
     x = oracle.f32_to_bf16_bits(causal(128, 512, 8))
     y = run_softmax(x, "bf16", "f32")
