@@ -109,6 +109,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cf_matmul_fp8": (_I32, [_P, _P, _P, _I64, _I64, _I64, _F, _P]),
     "cf_matmul_fp8_wt_shape_supported": (_I32, [_I64, _I64, _I64]),
     "cf_matmul_fp8_wt": (_I32, [_P, _P, _P, _I64, _I64, _I64, _F, _P]),
+    "cf_attention_scores_causal": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P]),
+    "cf_attention_pv_causal": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P]),
     "cf_paged_attention_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "cf_paged_attention": (
         _I32,

@@ -42,6 +42,7 @@ HIP_SOURCES = (
     "cf_paged_attention.hip",
     "cf_tensor_core.hip",
     "cf_matmul_fp8.hip",
+    "cf_attention.hip",
 )
 
 # Per-source additions. The fused LoRA kernel accumulates in VGPRs: the

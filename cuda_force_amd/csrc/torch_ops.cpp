@@ -14,8 +14,10 @@
 //     float32 and bfloat16;
 //   * a few extra operators the Python layer uses: dequantize_int8_to (half
 //     outputs), quantize_dequantize, softmax_as (output dtype),
-//     softmax_scaled (scaled, causally masked attention scores), row_sum, and
-//     lora_linear_fwd / lora_linear_bwd for the adapter autograd path.
+//     softmax_scaled (scaled, causally masked attention scores), row_sum,
+//     lora_linear_fwd / lora_linear_bwd for the adapter autograd path, and
+//     attention_scores_causal / attention_pv_causal, the two causal attention
+//     products of the transformer block.
 #include <c10/hip/HIPStream.h>
 #include <torch/csrc/autograd/autograd_not_implemented_fallback.h>
 #include <torch/extension.h>
@@ -128,6 +130,43 @@ torch::Tensor softmax_scaled_hip(const torch::Tensor& input, double scale, int64
                                    to_cf(out_dtype), input.size(0), input.size(1),
                                    static_cast<float>(scale), causal_period, stream_for(input)));
     return output;
+}
+
+// Causal attention products: q, k, v [batch, seq, heads * head_dim],
+// probs [batch, heads, seq, seq].
+void check_attention(const torch::Tensor& rows, int64_t heads, const char* name) {
+    TORCH_CHECK(rows.dim() == 3, name, " must be [batch, seq, hidden], got ", rows.dim(), " dims");
+    TORCH_CHECK(heads > 0 && rows.size(2) % heads == 0, "hidden ", rows.size(2), " is not divisible by heads ",
+                heads);
+}
+
+torch::Tensor attention_scores_causal_hip(const torch::Tensor& q, const torch::Tensor& k, int64_t heads) {
+    check_attention(q, heads, "q");
+    TORCH_CHECK(k.sizes() == q.sizes(), "q and k differ in shape");
+    check_contiguous(q, "q");
+    check_contiguous(k, "k");
+    const at::DeviceGuard guard(q.device());
+    const int64_t batch = q.size(0), seq = q.size(1);
+    torch::Tensor scores = torch::empty({batch, heads, seq, seq}, q.options());
+    check_status(cf_attention_scores_causal(q.data_ptr(), k.data_ptr(), scores.data_ptr(), to_cf(q, "q"), batch,
+                                            seq, heads, q.size(2) / heads, stream_for(q)));
+    return scores;
+}
+
+torch::Tensor attention_pv_causal_hip(const torch::Tensor& probs, const torch::Tensor& v, int64_t heads) {
+    check_attention(v, heads, "v");
+    const int64_t batch = v.size(0), seq = v.size(1);
+    TORCH_CHECK(probs.dim() == 4 && probs.size(0) == batch && probs.size(1) == heads && probs.size(2) == seq &&
+                    probs.size(3) == seq,
+                "probs must be [batch, heads, seq, seq] = [", batch, ", ", heads, ", ", seq, ", ", seq, "]");
+    TORCH_CHECK(probs.scalar_type() == v.scalar_type(), "probs and v differ in dtype");
+    check_contiguous(probs, "probs");
+    check_contiguous(v, "v");
+    const at::DeviceGuard guard(v.device());
+    torch::Tensor out = torch::empty(v.sizes(), v.options());
+    check_status(cf_attention_pv_causal(probs.data_ptr(), v.data_ptr(), out.data_ptr(), to_cf(v, "v"), batch, seq,
+                                        heads, v.size(2) / heads, stream_for(v)));
+    return out;
 }
 
 std::tuple<torch::Tensor, torch::Tensor> lora_linear_fwd_hip(const torch::Tensor& x,
@@ -389,6 +428,29 @@ torch::Tensor softmax_scaled_cpu(const torch::Tensor& input, double scale, int64
     return torch::softmax(logits, /*dim=*/-1).to(out_dtype);
 }
 
+// The same products on the CPU: heads split out, the full q k^T (the
+// kernel leaves the entries above the diagonal unspecified; these hold their
+// dot products) and the lower triangle of probs times v.
+torch::Tensor attention_scores_causal_cpu(const torch::Tensor& q, const torch::Tensor& k, int64_t heads) {
+    check_attention(q, heads, "q");
+    TORCH_CHECK(k.sizes() == q.sizes(), "q and k differ in shape");
+    const int64_t batch = q.size(0), seq = q.size(1), d = q.size(2) / heads;
+    const torch::Tensor qh = q.view({batch, seq, heads, d}).transpose(1, 2).to(torch::kFloat32);
+    const torch::Tensor kh = k.view({batch, seq, heads, d}).transpose(1, 2).to(torch::kFloat32);
+    return torch::matmul(qh, kh.transpose(-2, -1)).to(q.scalar_type());
+}
+
+torch::Tensor attention_pv_causal_cpu(const torch::Tensor& probs, const torch::Tensor& v, int64_t heads) {
+    check_attention(v, heads, "v");
+    const int64_t batch = v.size(0), seq = v.size(1), d = v.size(2) / heads;
+    TORCH_CHECK(probs.dim() == 4 && probs.size(0) == batch && probs.size(1) == heads && probs.size(2) == seq &&
+                    probs.size(3) == seq,
+                "probs must be [batch, heads, seq, seq] = [", batch, ", ", heads, ", ", seq, ", ", seq, "]");
+    const torch::Tensor vh = v.view({batch, seq, heads, d}).transpose(1, 2).to(torch::kFloat32);
+    const torch::Tensor out = torch::matmul(torch::tril(probs.to(torch::kFloat32)), vh);
+    return out.transpose(1, 2).reshape({batch, seq, heads * d}).to(v.scalar_type());
+}
+
 torch::Tensor lora_linear_cpu(const torch::Tensor& x, const torch::Tensor& w,
                               const torch::Tensor& a, const torch::Tensor& b, double scale) {
     return torch::matmul(x, w) + scale * torch::matmul(torch::matmul(x, a), b);
@@ -518,6 +580,8 @@ TORCH_LIBRARY(cudaforge, m) {
     m.def(
         "lora_linear_bwd(Tensor x, Tensor dy, Tensor b, Tensor xa, float scale) "
         "-> (Tensor, Tensor)");
+    m.def("attention_scores_causal(Tensor q, Tensor k, int heads) -> Tensor");
+    m.def("attention_pv_causal(Tensor probs, Tensor v, int heads) -> Tensor");
 }
 
 // Inference-only operators raise on differentiation instead of silently
@@ -528,7 +592,8 @@ TORCH_LIBRARY_IMPL(cudaforge, Autograd, m) {
     for (const char* name :
          {"rmsnorm", "softmax", "lora_linear", "sum", "silu", "gelu", "swiglu", "quantize_int8",
           "dequantize_int8", "dequantize_int8_to", "quantize_dequantize", "softmax_as",
-          "softmax_scaled", "row_sum", "lora_linear_fwd", "lora_linear_bwd"}) {
+          "softmax_scaled", "row_sum", "lora_linear_fwd", "lora_linear_bwd", "attention_scores_causal",
+          "attention_pv_causal"}) {
         m.impl(name, torch::autograd::autogradNotImplementedFallback());
     }
 }
@@ -552,6 +617,8 @@ TORCH_LIBRARY_IMPL(cudaforge, CPU, m) {
     m.impl("row_sum", &row_sum_cpu);
     m.impl("lora_linear_fwd", &lora_linear_fwd_cpu);
     m.impl("lora_linear_bwd", &lora_linear_bwd_cpu);
+    m.impl("attention_scores_causal", &attention_scores_causal_cpu);
+    m.impl("attention_pv_causal", &attention_pv_causal_cpu);
 }
 
 TORCH_LIBRARY_IMPL(cudaforge, CUDA, m) {
@@ -573,6 +640,8 @@ TORCH_LIBRARY_IMPL(cudaforge, CUDA, m) {
     m.impl("row_sum", &row_sum_hip);
     m.impl("lora_linear_fwd", &lora_linear_fwd_hip);
     m.impl("lora_linear_bwd", &lora_linear_bwd_hip);
+    m.impl("attention_scores_causal", &attention_scores_causal_hip);
+    m.impl("attention_pv_causal", &attention_pv_causal_hip);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

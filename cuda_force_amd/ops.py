@@ -299,6 +299,76 @@ def softmax_scaled(
     return _softmax_scaled_reference(x, scale, causal_period).to(dtype)
 
 
+#: Head sizes the causal attention kernels take (sequence lengths: multiples of 8).
+ATTENTION_HEAD_DIMS = (32, 64, 96, 128)
+
+
+def _attention_kernel_shape(rows: torch.Tensor, heads: int) -> bool:
+    """True when the bf16 attention kernels take [batch, seq, heads * head_dim]."""
+    return (
+        rows.dtype == torch.bfloat16
+        and rows.shape[-1] // heads in ATTENTION_HEAD_DIMS
+        and rows.shape[1] % 8 == 0
+    )
+
+
+def _check_attention_rows(rows: torch.Tensor, heads: int, name: str) -> None:
+    if rows.dim() != 3:
+        raise ValueError(f"{name} must be [batch, seq, hidden], got {tuple(rows.shape)}")
+    if heads <= 0 or rows.shape[-1] % heads:
+        raise ValueError(f"hidden {rows.shape[-1]} is not divisible by heads {heads}")
+
+
+def attention_scores_causal(q: torch.Tensor, k: torch.Tensor, heads: int) -> torch.Tensor:
+    """``q @ k^T`` per head for causal attention: q, k ``[batch, seq, hidden]``
+    (the projections' output, ``hidden = heads * head_dim``) give scores
+    ``[batch, heads, seq, seq]``.
+
+    The product of examples/transformer_block.py:54 without the head
+    transposes. Only the causal half is defined: entries above the diagonal
+    are unspecified (the HIP kernel skips the 128 x 128 tiles above it), so
+    follow it with ``softmax_scaled(..., causal_period=seq)``, which never
+    reads them. bf16 with head_dim 32/64/96/128 and seq a multiple of 8 runs
+    the MFMA kernel on a GPU. Not in the reference's API."""
+    _check_attention_rows(q, heads, "q")
+    if k.shape != q.shape:
+        raise ValueError(f"q and k differ in shape: {tuple(q.shape)} and {tuple(k.shape)}")
+    q, k = q.contiguous(), k.contiguous()
+    if _dispatch_available("attention_scores_causal", q, k) and (not q.is_cuda or _attention_kernel_shape(q, heads)):
+        return torch.ops.cudaforge.attention_scores_causal(q, k, int(heads))
+    _refuse_gpu_fallback("attention_scores_causal", q, k)
+    batch, seq, hidden = q.shape
+    qh = q.view(batch, seq, heads, hidden // heads).transpose(1, 2).float()
+    kh = k.view(batch, seq, heads, hidden // heads).transpose(1, 2).float()
+    return (qh @ kh.transpose(-2, -1)).to(q.dtype)
+
+
+def attention_pv_causal(probs: torch.Tensor, v: torch.Tensor, heads: int) -> torch.Tensor:
+    """``probs @ v`` per head for causal attention, back in the
+    ``[batch, seq, hidden]`` layout: probs ``[batch, heads, seq, seq]``, v
+    ``[batch, seq, hidden]``. Row s of probs contributes keys 0 .. s only;
+    entries above the diagonal are never read as values.
+
+    The product of examples/transformer_block.py:63 with its transpose and
+    reshape folded in. Same kernel rules as ``attention_scores_causal``. Not
+    in the reference's API."""
+    _check_attention_rows(v, heads, "v")
+    batch, seq, hidden = v.shape
+    if probs.shape != (batch, heads, seq, seq):
+        raise ValueError(f"probs must be {(batch, heads, seq, seq)}, got {tuple(probs.shape)}")
+    probs, v = probs.contiguous(), v.contiguous()
+    if (
+        _dispatch_available("attention_pv_causal", probs, v)
+        and probs.dtype == v.dtype
+        and (not v.is_cuda or _attention_kernel_shape(v, heads))
+    ):
+        return torch.ops.cudaforge.attention_pv_causal(probs, v, int(heads))
+    _refuse_gpu_fallback("attention_pv_causal", probs, v)
+    vh = v.view(batch, seq, heads, hidden // heads).transpose(1, 2).float()
+    out = torch.tril(probs.float()) @ vh
+    return out.transpose(1, 2).reshape(batch, seq, hidden).to(v.dtype)
+
+
 def lora_linear(
     x: torch.Tensor,
     weight: torch.Tensor,

@@ -13,8 +13,10 @@ bf16 MFMA kernel, so one block runs
     lora_linear O -> fused_residual_rmsnorm
     -> lora_linear gate, up -> swiglu -> lora_linear down
 
-The two batched attention products go through torch.matmul (hipBLASLt), as in
-the reference; the transposed key operand is made contiguous first.
+The two batched attention products run the causal HIP kernels
+(ops.attention_scores_causal / attention_pv_causal): the reference composes
+them from torch matmuls over the full [seq, seq] block, these compute its lower
+triangle only and read the heads in place.
 
 `reference_forward` restates the same block in fp32 torch operations (from the
 same bf16 parameters) for parity checks; `timed_forward` reports each
@@ -100,22 +102,18 @@ class LlamaBlock:
         q, k, v = self.q(normed), self.k(normed), self.v(normed)
         mark("qkv_lora")
 
-        def heads(t):
-            return t.view(batch, seq, c.heads, c.head_dim).transpose(1, 2).contiguous()
-
-        qh, vh = heads(q), heads(v)
-        # Every operand of the batched products is contiguous: the key is laid
-        # out [batch, heads, head_dim, seq] by one copy, so no transposed view
-        # reaches the bf16 batched GEMM.
-        kt = k.view(batch, seq, c.heads, c.head_dim).permute(0, 2, 3, 1).contiguous()
-        scores = torch.matmul(qh, kt)
+        # The causal products read q, k and v in the projections' [batch,
+        # seq, hidden] layout (no head transposes) and compute only the
+        # lower triangle; the softmax reads only that triangle too.
+        rows = (batch, seq, c.hidden)
+        scores = ops.attention_scores_causal(q.view(rows), k.view(rows), c.heads)
         mark("scores_matmul")
         # softmax(scores / sqrt(d) + causal) in one pass: row r of each
         # head's [seq, seq] block keeps columns 0 .. r; the masked scores
         # are never read.
         weights = ops.softmax_scaled(scores.view(-1, seq), 1.0 / math.sqrt(c.head_dim), seq).view_as(scores)
         mark("softmax")
-        attended = torch.matmul(weights, vh).transpose(1, 2).reshape(batch * seq, c.hidden)
+        attended = ops.attention_pv_causal(weights, v.view(rows), c.heads).view(batch * seq, c.hidden)
         mark("pv_matmul")
         out = self.o(attended)
         mark("o_lora")

@@ -409,6 +409,33 @@ cf_status cf_paged_attention(const void* query, const void* k_cache, const void*
                              int64_t max_blocks_per_sequence, float scale, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/* ---- causal attention products ------------------------------------------ */
+
+/* scores[b, h, s, t] = sum_d q[b, s, h, d] * k[b, t, h, d] for t <= s: the
+ * query @ key^T of examples/transformer_block.py:54 with the head transposes
+ * folded into the addressing. q and k are [batch, seq, heads * head_dim] (the
+ * projections' output), scores [batch, heads, seq, seq]; bfloat16, fp32
+ * accumulation, one rounding. Only the causal half is computed: 128 x 128
+ * tiles wholly above the diagonal are not written, and entries above the
+ * diagonal inside a written tile hold their dot products. A causal softmax
+ * (cf_softmax_scaled with causal_period = seq) reads none of them. head_dim
+ * 32, 64, 96 or 128 and seq a multiple of 8; other shapes and dtypes are
+ * CF_ERR_UNSUPPORTED. Tensors 16-byte aligned. It has no counterpart in the
+ * reference, whose block runs this product through torch. */
+cf_status cf_attention_scores_causal(const void* q, const void* k, void* scores, cf_dtype dtype,
+                                     int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                                     void* stream);
+
+/* out[b, s, h, d] = sum over t <= s of probs[b, h, s, t] * v[b, t, h, d]:
+ * the weights @ value of examples/transformer_block.py:63, written straight
+ * into the [batch, seq, heads * head_dim] layout the output projection takes.
+ * probs [batch, heads, seq, seq]; entries above the diagonal are never read
+ * as values. Same dtype, shape and alignment rules as
+ * cf_attention_scores_causal. It has no counterpart in the reference. */
+cf_status cf_attention_pv_causal(const void* probs, const void* v, void* out, cf_dtype dtype,
+                                 int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                                 void* stream);
+
 /* ---- measurement helper ------------------------------------------------- */
 
 /* Plain device-to-device copy of `bytes` bytes through a streaming kernel

@@ -11,7 +11,8 @@ Contents:
                 independent numpy restatement, cross-checked in the tests.
   floatops.py   float64 restatements of RMSNorm, softmax, the sum, the LoRA
                 linear and its adapter gradients, the activations,
-                paged-attention decode, and the fp8 (e4m3fn) matmul.
+                paged-attention decode, the fp8 (e4m3fn) matmul, and the
+                block's two attention products.
   ref_runner.py runs the reference's own CPU operators (cpp/src/bindings.cpp,
                 compiled by `make -C oracle ref` into oracle/_ref/) in a child
                 process, for golden vectors and the "reference" CPU baseline.
@@ -21,6 +22,8 @@ invariants, planted mistakes) is listed in tests/test_oracle.py.
 """
 
 from oracle.floatops import (  # noqa: F401
+    attention_scores,
+    attention_values,
     bf16_bits_to_f32,
     e4m3fn_to_f64,
     f32_to_bf16_bits,

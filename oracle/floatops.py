@@ -157,6 +157,29 @@ def paged_attention(
     return out
 
 
+def attention_scores(q: np.ndarray, k: np.ndarray, heads: int) -> np.ndarray:
+    """query @ key^T per head (examples/transformer_block.py:51-54, before the
+    1/sqrt(d) and the mask): q, k [batch, seq, heads * d] -> [batch, heads,
+    seq, seq], float64, every entry (the kernels define the lower triangle)."""
+    batch, seq, hidden = q.shape
+    d = hidden // heads
+    qh = np.asarray(q, dtype=np.float64).reshape(batch, seq, heads, d).transpose(0, 2, 1, 3)
+    kh = np.asarray(k, dtype=np.float64).reshape(batch, seq, heads, d).transpose(0, 2, 1, 3)
+    return qh @ kh.transpose(0, 1, 3, 2)
+
+
+def attention_values(probs: np.ndarray, v: np.ndarray, heads: int) -> np.ndarray:
+    """(weights @ value).transpose(1, 2).reshape(batch, seq, hidden) of
+    examples/transformer_block.py:63, with row s of the weights taking keys
+    0 .. s only (the causal lower triangle): probs [batch, heads, seq, seq],
+    v [batch, seq, heads * d] -> [batch, seq, heads * d], float64."""
+    batch, seq, hidden = v.shape
+    d = hidden // heads
+    vh = np.asarray(v, dtype=np.float64).reshape(batch, seq, heads, d).transpose(0, 2, 1, 3)
+    lower = np.tril(np.asarray(probs, dtype=np.float64))
+    return (lower @ vh).transpose(0, 2, 1, 3).reshape(batch, seq, hidden)
+
+
 def e4m3fn_to_f64(codes: np.ndarray) -> np.ndarray:
     """Decode OCP fp8 e4m3fn codes (OCP 8-bit floating point specification
     v1.0, E4M3: sign, 4 exponent bits with bias 7, 3 mantissa bits; exponent

@@ -206,3 +206,25 @@ def test_stream_bytes_host_checks(lib):
     assert lib.cf_stream_bytes(null, fake, 16384, 0, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_stream_bytes(fake, fake, 1000, 4, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_stream_bytes(null, fake, 16384, 4, null) == _lib.CF_ERR_INVALID_ARGUMENT
+
+
+def test_attention_products_host_checks(lib):
+    """The causal attention products reject what they have no kernel for
+    before any launch: empty sizes are no-ops, fp32, a head size outside
+    32/64/96/128 or a sequence length that is not a multiple of 8 are
+    CF_ERR_UNSUPPORTED, null or misaligned tensors CF_ERR_INVALID_ARGUMENT."""
+    null = ctypes.c_void_p(0)
+    fake = ctypes.c_void_p(0x1000)
+    odd = ctypes.c_void_p(0x1008)
+    for name in ("cf_attention_scores_causal", "cf_attention_pv_causal"):
+        fn = getattr(lib, name)
+        assert fn(null, null, null, _lib.CF_BF16, 0, 512, 32, 128, null) == _lib.CF_OK
+        assert fn(null, null, null, _lib.CF_BF16, 8, 0, 32, 128, null) == _lib.CF_OK
+        assert fn(null, fake, fake, _lib.CF_BF16, 8, 512, 32, 128, null) == _lib.CF_ERR_INVALID_ARGUMENT
+        assert fn(fake, fake, fake, _lib.CF_F32, 8, 512, 32, 128, null) == _lib.CF_ERR_UNSUPPORTED
+        assert fn(fake, fake, fake, _lib.CF_BF16, 8, 512, 32, 80, null) == _lib.CF_ERR_UNSUPPORTED
+        assert fn(fake, fake, fake, _lib.CF_BF16, 8, 500, 32, 128, null) == _lib.CF_ERR_UNSUPPORTED
+        assert fn(fake, odd, fake, _lib.CF_BF16, 8, 512, 32, 128, null) == _lib.CF_ERR_INVALID_ARGUMENT
+        assert b"16-byte aligned" in lib.cf_last_error()
+        assert fn(fake, fake, fake, _lib.CF_BF16, 1, 32768, 2, 128, null) == _lib.CF_ERR_INVALID_ARGUMENT
+        assert b"32-bit offsets" in lib.cf_last_error()
