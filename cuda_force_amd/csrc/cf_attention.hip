@@ -26,10 +26,11 @@
 //   * scores are computed transposed, S^T = K Q^T. A and B fragments are
 //     16-byte loads of k and q rows straight from memory (head_dim is the
 //     contiguous reduction index of both), and a lane ends with four
-//     consecutive keys of one query row: one 8-byte store.
+//     consecutive keys of one query row; each wave's 64 x 64 tile is then
+//     staged in LDS and written as whole 128-byte row pieces.
 //   * out is computed transposed too, O^T = V^T P^T. P^T fragments are
 //     16-byte loads of probability rows; V^T fragments come out of an LDS copy
-//     of each 32-key chunk of v (shared by the workgroup's four waves) through
+//     of each 64-key chunk of v (shared by the workgroup's four waves) through
 //     ds_read_b64_tr_b16, which hands each lane 4 consecutive keys of one
 //     head dimension. A lane ends with four consecutive head dimensions of
 //     one query row: one 8-byte store into the [batch, seq, hidden] output.
@@ -47,7 +48,8 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 constexpr int kThreads = 256;
 constexpr int kScoreTile = 128;  // queries and keys per scores workgroup
 constexpr int kPvRows = 64;      // query rows per out workgroup (16 per wave)
-constexpr int kPvChunk = 32;     // keys per step of the out product
+constexpr int kPvChunk = 64;     // keys per step of the out product (two MFMA k-steps)
+constexpr int kPvSub = kPvChunk / 32;
 constexpr int kVPitch = 256;     // LDS bytes per staged v row (head_dim <= 128)
 // A buffer offset past every range this file builds (all below 2^31): the
 // load returns zeros. Rows past seq take it rather than their own offset,
@@ -79,15 +81,25 @@ __device__ __forceinline__ void store4_bf16(uint16_t* p, const f32x4_t& v) {
     *reinterpret_cast<uint2*>(p) = make_uint2(f32x2_to_bf16x2_canon(v[0], v[1]), f32x2_to_bf16x2_canon(v[2], v[3]));
 }
 
-/// scores for the causal tiles. blockIdx.x = bh * tiles + tile, tile
+/// Workgroup ids are dealt round-robin over the 8 XCDs; this renumbering
+/// gives each XCD a contiguous range of logical ids (when the grid divides),
+/// so the workgroups of one head share that XCD's L2.
+__device__ __forceinline__ int64_t xcd_local(int64_t pid, int64_t total) {
+    constexpr int kXcds = 8;
+    return total % kXcds == 0 ? (pid % kXcds) * (total / kXcds) + pid / kXcds : pid;
+}
+
+/// scores for the causal tiles. Logical id = bh * tiles + tile, tile
 /// enumerating the tiles (si, ti) with ti <= si row by row.
 template <int kD>
 __global__ __launch_bounds__(kThreads) void attention_scores_kernel(const uint16_t* __restrict__ q,
                                                                     const uint16_t* __restrict__ k,
                                                                     uint16_t* __restrict__ scores, int64_t seq,
                                                                     int64_t heads, int tiles) {
-    const int64_t bh = blockIdx.x / tiles;
-    const int tile = static_cast<int>(blockIdx.x % tiles);
+    __shared__ __attribute__((aligned(16))) uint8_t score_stage[4][64 * 128];  // 8 KiB per wave
+    const int64_t id = xcd_local(blockIdx.x, static_cast<int64_t>(gridDim.x));
+    const int64_t bh = id / tiles;
+    const int tile = static_cast<int>(id % tiles);
     int si = static_cast<int>((sqrtf(8.0f * static_cast<float>(tile) + 1.0f) - 1.0f) * 0.5f);
     while ((si + 1) * (si + 2) / 2 <= tile) ++si;
     while (si * (si + 1) / 2 > tile) --si;
@@ -157,18 +169,36 @@ __global__ __launch_bounds__(kThreads) void attention_scores_kernel(const uint16
         if (kk + 1 < kSteps) cur = nxt;
     }
 
-    // acc[tb][sb] lane holds S[s0 + 16 sb + j][t0 + 16 tb + 4 g .. +3];
-    // seq is a multiple of 8, so four keys never straddle its end.
-    uint16_t* out = scores + bh * seq * seq;
+    // acc[tb][sb] lane holds S[s0 + 16 sb + j][t0 + 16 tb + 4 g .. +3]. The
+    // wave's 64 x 64 tile goes through its own LDS area (rows of 128 bytes,
+    // 16-byte chunk c of row r at c ^ (r & 7)) so that the stores write
+    // whole 128-byte row pieces.
+    uint8_t* stage = score_stage[wave];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
-        const int64_t s = s0 + 16 * sb + j;
-        if (s >= seq) continue;
+        const int row = 16 * sb + j;
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-            const int64_t t = t0 + 16 * tb + 4 * g;
-            if (t < seq) store4_bf16(out + s * seq + t, acc[tb][sb]);
+            const int chunk = (2 * tb + (g >> 1)) ^ (row & 7);
+            *reinterpret_cast<uint2*>(stage + row * 128 + chunk * 16 + (g & 1) * 8) =
+                make_uint2(f32x2_to_bf16x2_canon(acc[tb][sb][0], acc[tb][sb][1]),
+                           f32x2_to_bf16x2_canon(acc[tb][sb][2], acc[tb][sb][3]));
         }
+    }
+    // Only this wave reads what it wrote; the fence keeps the compiler from
+    // moving the reads above the writes.
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // seq is a multiple of 8, so eight keys never straddle its end.
+    uint16_t* out = scores + bh * seq * seq;
+    const int c = lane & 7;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 8 * i + (lane >> 3);
+        const int64_t s = s0 + row;
+        const int64_t t = t0 + 8 * c;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + row * 128 + ((c ^ (row & 7)) << 4));
+        if (s < seq && t < seq) *reinterpret_cast<uint4*>(out + s * seq + t) = v;
     }
 }
 
@@ -180,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_kernel(const uint16_t* 
                                                                 const uint16_t* __restrict__ v,
                                                                 uint16_t* __restrict__ out, int64_t seq,
                                                                 int64_t heads, int64_t bh_count, int tiles) {
-    __shared__ __attribute__((aligned(16))) uint8_t vt[2][kPvChunk * kVPitch];  // 2 x 8 KiB
+    __shared__ __attribute__((aligned(16))) uint8_t vt[2][kPvChunk * kVPitch];  // 2 x 16 KiB
 
     const int64_t bh = blockIdx.x % bh_count;
     const int tile = tiles - 1 - static_cast<int>(blockIdx.x / bh_count);
@@ -230,11 +260,12 @@ __global__ __launch_bounds__(kThreads) void attention_pv_kernel(const uint16_t* 
         }
     };
 
-    // This lane's query row (B column) and its probabilities for chunk c:
-    // keys 32 c + 8 g .. +7, those past the row's own position zeroed.
+    // This lane's query row (B column) and its probabilities for sub-step u
+    // of chunk c: keys 64 c + 32 u + 8 g .. +7, those past the row's own
+    // position zeroed.
     const int64_t s = s_first + 16 * wave + j;
-    auto load_p = [&](int c) {
-        const int64_t t_first = static_cast<int64_t>(c) * kPvChunk + 8 * g;
+    auto load_p = [&](int c, int u) {
+        const int64_t t_first = static_cast<int64_t>(c) * kPvChunk + 32 * u + 8 * g;
         // Keys past seq lie past the row (and past s): masked below.
         const uint32_t off = s < seq ? static_cast<uint32_t>((s * seq + t_first) * 2) : kPastEnd;
         const uint4 raw = buffer_load16(pbuf, off, 0);
@@ -249,9 +280,10 @@ __global__ __launch_bounds__(kThreads) void attention_pv_kernel(const uint16_t* 
         return as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
     };
 
-    // V^T fragment of head dims 16 db .. +15 (A rows) over the chunk's keys
-    // 8 g .. +7: lane j of group g reads key rows 8 g + j / 4 (and 4 more),
-    // dims 16 db + 4 (j % 4) .. +3, and receives dim 16 db + j's 4 keys.
+    // V^T fragment of head dims 16 db .. +15 (A rows) over keys 32 u + 8 g
+    // .. +7 of the chunk: lane j of group g reads key rows 32 u + 8 g + j / 4
+    // (and 4 more), dims 16 db + 4 (j % 4) .. +3, and receives dim
+    // 16 db + j's 4 keys. Rows 32 apart share the swizzle.
     const int vrow = 8 * g + (j >> 2);
     const int vsw = v_swizzle(vrow);  // the same for vrow + 4
     constexpr int kBlocks = kD / 16;
@@ -261,29 +293,38 @@ __global__ __launch_bounds__(kThreads) void attention_pv_kernel(const uint16_t* 
 
     load_v(0);
     store_v(0);
-    bf16x8_t pcur = load_p(0);
+    bf16x8_t pcur[kPvSub];
+#pragma unroll
+    for (int u = 0; u < kPvSub; ++u) pcur[u] = load_p(0, u);
     __syncthreads();
     for (int c = 0; c < chunks; ++c) {
         const bool more = c + 1 < chunks;  // workgroup-uniform
-        bf16x8_t pnext = pcur;
+        bf16x8_t pnext[kPvSub];
+#pragma unroll
+        for (int u = 0; u < kPvSub; ++u) pnext[u] = pcur[u];
         if (more) {
             load_v(c + 1);
-            pnext = load_p(c + 1);
+#pragma unroll
+            for (int u = 0; u < kPvSub; ++u) pnext[u] = load_p(c + 1, u);
         }
         const uint8_t* tile_v = vt[c & 1];
 #pragma unroll
-        for (int db = 0; db < kBlocks; ++db) {
-            const int chunk = 2 * db + ((j & 3) >> 1);
-            const int off = vrow * kVPitch + ((chunk ^ vsw) << 4) + (j & 1) * 8;
-            const s16x4_t lo = lds_read_tr(tile_v, off);
-            const s16x4_t hi = lds_read_tr(tile_v, off + 4 * kVPitch);
-            const bf16x8_t vfrag =
-                __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-            acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag, pcur, acc[db], 0, 0, 0);
+        for (int u = 0; u < kPvSub; ++u) {
+#pragma unroll
+            for (int db = 0; db < kBlocks; ++db) {
+                const int chunk = 2 * db + ((j & 3) >> 1);
+                const int off = (32 * u + vrow) * kVPitch + ((chunk ^ vsw) << 4) + (j & 1) * 8;
+                const s16x4_t lo = lds_read_tr(tile_v, off);
+                const s16x4_t hi = lds_read_tr(tile_v, off + 4 * kVPitch);
+                const bf16x8_t vfrag =
+                    __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag, pcur[u], acc[db], 0, 0, 0);
+            }
         }
         if (more) store_v((c + 1) & 1);
         __syncthreads();
-        pcur = pnext;
+#pragma unroll
+        for (int u = 0; u < kPvSub; ++u) pcur[u] = pnext[u];
     }
 
     // acc[db] lane holds out[s][16 db + 4 g .. +3].
