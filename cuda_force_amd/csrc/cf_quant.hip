@@ -43,8 +43,13 @@ namespace {
 // (config 1's fp32 [4096, 4096] ran 15.6 us against 16.1 with 8), 8 for the
 // grouped launches of bulk quantisation (bf16 [4096, 4096] x 48 per launch:
 // quantise 68% -> 75.5%, dequantise 65.5% -> 74% of HBM peak against 4).
+// Grouped dequantisation reads 8 codes per lane and step and takes 12 steps:
+// 48 bf16 tensors of config 5's shapes (4.25 GB per launch) 720 -> 694 us
+// (72.9% -> 75.7%) against 8, in a same-process A/B; 10 gave 74.4%, 14 76.1%.
+// 12 steps for the grouped quantiser were slower (70.8% -> 66.3%).
 constexpr int kUnroll = 4;
 constexpr int kGroupUnroll = 8;
+constexpr int kDequantGroupUnroll = 12;
 constexpr float kTieMargin = 6.0e-5f;
 constexpr float kMinFastScale = 7.88860905e-31f;  // 2^-100
 
@@ -431,10 +436,10 @@ __global__ __launch_bounds__(kDefaultBlockSize) void dequantize_group_kernel(Deq
     const int64_t wave = gw - args.first_wave[t];
     Tout* y = static_cast<Tout*>(args.y[t]);
     const int64_t count = args.count[t];
-    if ((wave + 1) * dequant_elements_per_wave<Tout, kGroupUnroll>() <= count) {
-        dequantize_body<Tout, true, true, kGroupUnroll>(args.q[t], args.scales[t], y, count, wave);
+    if ((wave + 1) * dequant_elements_per_wave<Tout, kDequantGroupUnroll>() <= count) {
+        dequantize_body<Tout, true, true, kDequantGroupUnroll>(args.q[t], args.scales[t], y, count, wave);
     } else {
-        dequantize_body<Tout, true, false, kGroupUnroll>(args.q[t], args.scales[t], y, count, wave);
+        dequantize_body<Tout, true, false, kDequantGroupUnroll>(args.q[t], args.scales[t], y, count, wave);
     }
 }
 
@@ -563,7 +568,7 @@ cf_status launch_dequantize_group(const int8_t* const* q, const float* const* sc
         args.y[args.n] = y[i];
         args.count[args.n] = count;
         args.first_wave[args.n] = waves;
-        waves += ceil_div<int64_t>(count, dequant_elements_per_wave<T, kGroupUnroll>());
+        waves += ceil_div<int64_t>(count, dequant_elements_per_wave<T, kDequantGroupUnroll>());
         if (++args.n == kGroupMax) {
             const cf_status status =
                 flush_group(dequantize_group_kernel<T>, args, waves, kWhat, stream);
