@@ -23,11 +23,13 @@
 // MFMA roles (v_mfma_f32_16x16x32_bf16; a lane holds A row l % 16 and B
 // column l % 16, each over k = 8 (l / 16) .. +7, and D rows 4 (l / 16) + i of
 // column l % 16):
-//   * scores are computed transposed, S^T = K Q^T. A and B fragments are
-//     16-byte loads of k and q rows straight from memory (head_dim is the
-//     contiguous reduction index of both), and a lane ends with four
-//     consecutive keys of one query row; each wave's 64 x 64 tile is then
-//     staged in LDS and written as whole 128-byte row pieces.
+//   * scores are computed transposed, S^T = K Q^T. The tile's q and k rows
+//     are copied into LDS by buffer loads with the LDS destination (whole
+//     256-byte rows, chunks swizzled for conflict-free reads); A and B
+//     fragments are ds_read_b128 of k and q rows (head_dim is the contiguous
+//     reduction index of both), and a lane ends with four consecutive keys
+//     of one query row; each wave's 64 x 64 tile is then staged in LDS and
+//     written as whole 128-byte row pieces.
 //   * out is computed transposed too, O^T = V^T P^T. P^T fragments are
 //     16-byte loads of probability rows; V^T fragments come out of an LDS copy
 //     of each 64-key chunk of v (shared by the workgroup's four waves) through
@@ -35,6 +37,7 @@
 //     head dimension. A lane ends with four consecutive head dimensions of
 //     one query row: one 8-byte store into the [batch, seq, hidden] output.
 #include "cf_common.hpp"
+#include "cf_lds_dma.hpp"
 
 namespace cf {
 namespace {
@@ -90,13 +93,18 @@ __device__ __forceinline__ int64_t xcd_local(int64_t pid, int64_t total) {
 }
 
 /// scores for the causal tiles. Logical id = bh * tiles + tile, tile
-/// enumerating the tiles (si, ti) with ti <= si row by row.
+/// enumerating the tiles (si, ti) with ti <= si row by row. The tile's 128
+/// query rows and 128 key rows are copied HBM -> LDS by buffer loads with
+/// the LDS destination (each load 4 whole rows), so every row is read once
+/// per workgroup in whole 256-byte pieces.
 template <int kD>
 __global__ __launch_bounds__(kThreads) void attention_scores_kernel(const uint16_t* __restrict__ q,
                                                                     const uint16_t* __restrict__ k,
                                                                     uint16_t* __restrict__ scores, int64_t seq,
                                                                     int64_t heads, int tiles) {
-    __shared__ __attribute__((aligned(16))) uint8_t score_stage[4][64 * 128];  // 8 KiB per wave
+    // q rows then k rows, 128 each at a 256-byte pitch, 16-byte chunk c of
+    // row r at c ^ (r & 15); afterwards each wave's 8 KiB output staging.
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kScoreTile * kVPitch];  // 64 KiB
     const int64_t id = xcd_local(blockIdx.x, static_cast<int64_t>(gridDim.x));
     const int64_t bh = id / tiles;
     const int tile = static_cast<int>(id % tiles);
@@ -107,73 +115,84 @@ __global__ __launch_bounds__(kThreads) void attention_scores_kernel(const uint16
 
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
-    const int64_t s0 = static_cast<int64_t>(si) * kScoreTile + (wave >> 1) * 64;
-    const int64_t t0 = static_cast<int64_t>(ti) * kScoreTile + (wave & 1) * 64;
-    // Wave-uniform: nothing on or below the diagonal, or no query row.
-    if (t0 > s0 + 63 || s0 >= seq) return;
+    const int64_t q_row0 = static_cast<int64_t>(si) * kScoreTile;
+    const int64_t k_row0 = static_cast<int64_t>(ti) * kScoreTile;
+    const int64_t s0 = q_row0 + (wave >> 1) * 64;
+    const int64_t t0 = k_row0 + (wave & 1) * 64;
+    // Wave-uniform: a wave with nothing on or below the diagonal, or no
+    // query row, still copies its share of the tiles and meets the barriers.
+    const bool active = t0 <= s0 + 63 && s0 < seq;
 
     const int64_t b = bh / heads;
     const int64_t h = bh % heads;
     const int64_t head0 = (b * seq * heads + h) * kD;  // element of row 0, dim 0
+    const int64_t pitch = heads * kD;                  // elements between consecutive rows
     const uint32_t extent = head_extent(seq, heads, kD);
-    const __amdgpu_buffer_rsrc_t qbuf = make_buffer(q + head0, extent);
-    const __amdgpu_buffer_rsrc_t kbuf = make_buffer(k + head0, extent);
+    const i32x4_t qbuf = uniform(raw_buffer_words(q + head0, extent));
+    const i32x4_t kbuf = uniform(raw_buffer_words(k + head0, extent));
+    const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)lds));
+
+    // Load n (0..31) of an operand fills rows 4 n .. 4 n + 3 of its tile:
+    // lane l lands at byte 16 l, i.e. row 4 n + l / 16, physical chunk
+    // l % 16, so it reads logical chunk (l % 16) ^ (row & 15). Rows past
+    // seq and chunks past the head (head_dim < 128) read as zero.
+    const int phys = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int n = 8 * wave + i;
+        const int r = 4 * n + (lane >> 4);
+        const int c = phys ^ (r & 15);
+        const int64_t qr = q_row0 + r;
+        const int64_t kr = k_row0 + r;
+        const uint32_t qoff = qr < seq && c < kD / 8 ? static_cast<uint32_t>((qr * pitch + 8 * c) * 2) : kPastEnd;
+        const uint32_t koff = kr < seq && c < kD / 8 ? static_cast<uint32_t>((kr * pitch + 8 * c) * 2) : kPastEnd;
+        dma16_m0(qbuf, lds_addr + static_cast<uint32_t>(n * 1024), qoff, 0);
+        dma16_m0(kbuf, lds_addr + static_cast<uint32_t>(kScoreTile * kVPitch + n * 1024), koff, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+
     const int j = lane & 15;
     const int g = lane >> 4;
-    const int64_t pitch = heads * kD;  // elements between consecutive rows
-
-    // Row offsets (bytes) of this lane's four key and four query rows; rows
-    // past seq read as zero.
-    uint32_t koff[4];
-    uint32_t qoff[4];
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-        const int64_t t = t0 + 16 * blk + j;
-        const int64_t sq = s0 + 16 * blk + j;
-        koff[blk] = t < seq ? static_cast<uint32_t>((t * pitch + 8 * g) * 2) : kPastEnd;
-        qoff[blk] = sq < seq ? static_cast<uint32_t>((sq * pitch + 8 * g) * 2) : kPastEnd;
-    }
-    struct Frags {
-        bf16x8_t a[4];
-        bf16x8_t b[4];
-    };
-    auto load = [&](Frags& f, int kk) {
-        const uint32_t dim = static_cast<uint32_t>(kk * 64);  // 32 bf16 per step
-#pragma unroll
-        for (int blk = 0; blk < 4; ++blk) {
-            f.a[blk] = as_bf16x8(buffer_load16(kbuf, koff[blk] + dim, 0));
-            f.b[blk] = as_bf16x8(buffer_load16(qbuf, qoff[blk] + dim, 0));
-        }
-    };
-
     f32x4_t acc[4][4];  // [key block][query block]
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
 #pragma unroll
         for (int sb = 0; sb < 4; ++sb) acc[tb][sb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    constexpr int kSteps = kD / 32;
-    Frags cur;
-    load(cur, 0);
+    if (active) {
+        // Fragment rows: key block tb is tile row (wave & 1) * 64 + 16 tb + j
+        // (A), query block sb tile row (wave >> 1) * 64 + 16 sb + j (B); both
+        // have row & 15 == j. K-step kk takes logical chunk 4 kk + g.
+        const uint8_t* kt = lds + kScoreTile * kVPitch + ((wave & 1) * 64 + j) * kVPitch;
+        const uint8_t* qt = lds + ((wave >> 1) * 64 + j) * kVPitch;
 #pragma unroll
-    for (int kk = 0; kk < kSteps; ++kk) {
-        Frags nxt;
-        if (kk + 1 < kSteps) load(nxt, kk + 1);
+        for (int kk = 0; kk < kD / 32; ++kk) {
+            const int off = ((4 * kk + g) ^ j) << 4;
+            bf16x8_t a[4];
+            bf16x8_t bq[4];
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
+            for (int blk = 0; blk < 4; ++blk) {
+                a[blk] = *reinterpret_cast<const bf16x8_t*>(kt + blk * 16 * kVPitch + off);
+                bq[blk] = *reinterpret_cast<const bf16x8_t*>(qt + blk * 16 * kVPitch + off);
+            }
 #pragma unroll
-            for (int sb = 0; sb < 4; ++sb) {
-                acc[tb][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.a[tb], cur.b[sb], acc[tb][sb], 0, 0, 0);
+            for (int tb = 0; tb < 4; ++tb) {
+#pragma unroll
+                for (int sb = 0; sb < 4; ++sb) {
+                    acc[tb][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tb], bq[sb], acc[tb][sb], 0, 0, 0);
+                }
             }
         }
-        if (kk + 1 < kSteps) cur = nxt;
     }
+    __syncthreads();  // every wave is done with the tiles before they are overwritten
+    if (!active) return;
 
     // acc[tb][sb] lane holds S[s0 + 16 sb + j][t0 + 16 tb + 4 g .. +3]. The
     // wave's 64 x 64 tile goes through its own LDS area (rows of 128 bytes,
     // 16-byte chunk c of row r at c ^ (r & 7)) so that the stores write
     // whole 128-byte row pieces.
-    uint8_t* stage = score_stage[wave];
+    uint8_t* stage = lds + wave * (64 * 128);
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
         const int row = 16 * sb + j;
