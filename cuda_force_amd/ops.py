@@ -303,12 +303,14 @@ def softmax_scaled(
 ATTENTION_HEAD_DIMS = (32, 64, 96, 128)
 
 
-def _attention_kernel_shape(rows: torch.Tensor, heads: int) -> bool:
-    """True when the bf16 attention kernels take [batch, seq, heads * head_dim]."""
+def _attention_kernel_shape(rows: torch.Tensor, heads: int, *others: torch.Tensor) -> bool:
+    """True when the bf16 attention kernels take [batch, seq, heads * head_dim]
+    (and the tensors are 16-byte aligned, as the kernels' loads need)."""
     return (
         rows.dtype == torch.bfloat16
         and rows.shape[-1] // heads in ATTENTION_HEAD_DIMS
         and rows.shape[1] % 8 == 0
+        and all(t.data_ptr() % 16 == 0 for t in (rows, *others))
     )
 
 
@@ -334,7 +336,7 @@ def attention_scores_causal(q: torch.Tensor, k: torch.Tensor, heads: int) -> tor
     if k.shape != q.shape:
         raise ValueError(f"q and k differ in shape: {tuple(q.shape)} and {tuple(k.shape)}")
     q, k = q.contiguous(), k.contiguous()
-    if _dispatch_available("attention_scores_causal", q, k) and (not q.is_cuda or _attention_kernel_shape(q, heads)):
+    if _dispatch_available("attention_scores_causal", q, k) and (not q.is_cuda or _attention_kernel_shape(q, heads, k)):
         return torch.ops.cudaforge.attention_scores_causal(q, k, int(heads))
     _refuse_gpu_fallback("attention_scores_causal", q, k)
     batch, seq, hidden = q.shape
@@ -360,7 +362,7 @@ def attention_pv_causal(probs: torch.Tensor, v: torch.Tensor, heads: int) -> tor
     if (
         _dispatch_available("attention_pv_causal", probs, v)
         and probs.dtype == v.dtype
-        and (not v.is_cuda or _attention_kernel_shape(v, heads))
+        and (not v.is_cuda or _attention_kernel_shape(v, heads, probs))
     ):
         return torch.ops.cudaforge.attention_pv_causal(probs, v, int(heads))
     _refuse_gpu_fallback("attention_pv_causal", probs, v)
