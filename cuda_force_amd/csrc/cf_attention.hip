@@ -32,7 +32,8 @@
 //     written as whole 128-byte row pieces.
 //   * out is computed transposed too, O^T = V^T P^T. P^T fragments are
 //     16-byte loads of probability rows; V^T fragments come out of an LDS copy
-//     of each 64-key chunk of v (shared by the workgroup's four waves) through
+//     of each 64-key chunk of v (copied by buffer loads with the LDS
+//     destination, shared by the workgroup's four waves) through
 //     ds_read_b64_tr_b16, which hands each lane 4 consecutive keys of one
 //     head dimension. A lane ends with four consecutive head dimensions of
 //     one query row: one 8-byte store into the [batch, seq, hidden] output.
@@ -246,36 +247,26 @@ __global__ __launch_bounds__(kThreads) void attention_pv_kernel(const uint16_t* 
     const int64_t h = bh % heads;
     const int64_t pitch = heads * kD;
     const int64_t head0 = (b * seq * heads + h) * kD;
-    const __amdgpu_buffer_rsrc_t vbuf = make_buffer(v + head0, head_extent(seq, heads, kD));
+    const i32x4_t vbuf = uniform(raw_buffer_words(v + head0, head_extent(seq, heads, kD)));
     const __amdgpu_buffer_rsrc_t pbuf =
         make_buffer(probs + bh * seq * seq, static_cast<uint32_t>(seq * seq * 2));
+    const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8_t*)&vt[0][0]));
 
-    // v staging: piece p (16 bytes) of a chunk is row p / (kD / 8), chunk
-    // p % (kD / 8) of that row; keys past seq read as zero.
-    constexpr int kPieces = kPvChunk * kD / 8;
-    constexpr int kPerThread = (kPieces + kThreads - 1) / kThreads;
-    uint4 staged[kPerThread];
-    auto load_v = [&](int c) {
+    // v chunk c (64 keys) HBM -> LDS slot by buffer loads with the LDS
+    // destination: load n (0..15, four per wave) fills rows 4 n .. 4 n + 3;
+    // lane l lands at byte 16 l, i.e. row 4 n + l / 16, physical chunk
+    // l % 16, so it reads logical chunk (l % 16) ^ v_swizzle(row). Keys past
+    // seq and chunks past the head (head_dim < 128) read as zero.
+    auto load_v = [&](int c, int slot) {
 #pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int p = tid + i * kThreads;
-            if (kPieces % kThreads == 0 || p < kPieces) {
-                const int64_t t = static_cast<int64_t>(c) * kPvChunk + p / (kD / 8);
-                const uint32_t off =
-                    t < seq ? static_cast<uint32_t>((t * pitch + 8 * (p % (kD / 8))) * 2) : kPastEnd;
-                staged[i] = buffer_load16(vbuf, off, 0);
-            }
-        }
-    };
-    auto store_v = [&](int slot) {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int p = tid + i * kThreads;
-            if (kPieces % kThreads == 0 || p < kPieces) {
-                const int row = p / (kD / 8);
-                const int chunk = p % (kD / 8);
-                *reinterpret_cast<uint4*>(&vt[slot][row * kVPitch + ((chunk ^ v_swizzle(row)) << 4)]) = staged[i];
-            }
+        for (int i = 0; i < kPvChunk / 16; ++i) {
+            const int n = (kPvChunk / 16) * wave + i;
+            const int row = 4 * n + (lane >> 4);
+            const int chunk = (lane & 15) ^ v_swizzle(row);
+            const int64_t t = static_cast<int64_t>(c) * kPvChunk + row;
+            const uint32_t off =
+                t < seq && chunk < kD / 8 ? static_cast<uint32_t>((t * pitch + 8 * chunk) * 2) : kPastEnd;
+            dma16_m0(vbuf, lds_addr + static_cast<uint32_t>(slot * kPvChunk * kVPitch + n * 1024), off, 0);
         }
     };
 
@@ -310,11 +301,11 @@ __global__ __launch_bounds__(kThreads) void attention_pv_kernel(const uint16_t* 
 #pragma unroll
     for (int db = 0; db < kBlocks; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    load_v(0);
-    store_v(0);
+    load_v(0, 0);
     bf16x8_t pcur[kPvSub];
 #pragma unroll
     for (int u = 0; u < kPvSub; ++u) pcur[u] = load_p(0, u);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
     for (int c = 0; c < chunks; ++c) {
         const bool more = c + 1 < chunks;  // workgroup-uniform
@@ -322,7 +313,9 @@ __global__ __launch_bounds__(kThreads) void attention_pv_kernel(const uint16_t* 
 #pragma unroll
         for (int u = 0; u < kPvSub; ++u) pnext[u] = pcur[u];
         if (more) {
-            load_v(c + 1);
+            // Slot (c + 1) % 2 was last read in step c - 1, before the
+            // barrier that ended it.
+            load_v(c + 1, (c + 1) & 1);
 #pragma unroll
             for (int u = 0; u < kPvSub; ++u) pnext[u] = load_p(c + 1, u);
         }
@@ -340,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_kernel(const uint16_t* 
                 acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag, pcur[u], acc[db], 0, 0, 0);
             }
         }
-        if (more) store_v((c + 1) & 1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the next chunk has landed
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < kPvSub; ++u) pcur[u] = pnext[u];
