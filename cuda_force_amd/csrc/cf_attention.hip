@@ -13,8 +13,8 @@
 // Both products only touch the causal half:
 //   * scores: one workgroup per 128 x 128 tile on or below the diagonal of a
 //     head's [seq, seq] block, four waves of 64 x 64. A wave wholly above the
-//     diagonal does nothing, and tiles above it are never written (the causal
-//     softmax does not read them). Entries above the diagonal inside a
+//     diagonal only helps copy the tile's rows, and tiles above it are never
+//     written (the causal softmax does not read them). Entries above the diagonal inside a
 //     written tile hold their dot products.
 //   * out: keys past a query row's own position are skipped chunk by chunk
 //     and masked inside the last chunk, so the probabilities above the
@@ -54,7 +54,7 @@ constexpr int kScoreTile = 128;  // queries and keys per scores workgroup
 constexpr int kPvRows = 64;      // query rows per out workgroup (16 per wave)
 constexpr int kPvChunk = 64;     // keys per step of the out product (two MFMA k-steps)
 constexpr int kPvSub = kPvChunk / 32;
-constexpr int kVPitch = 256;     // LDS bytes per staged v row (head_dim <= 128)
+constexpr int kVPitch = 256;     // LDS bytes per staged q, k or v row (head_dim <= 128)
 // A buffer offset past every range this file builds (all below 2^31): the
 // load returns zeros. Rows past seq take it rather than their own offset,
 // which for a large pitch could wrap around 2^32.
