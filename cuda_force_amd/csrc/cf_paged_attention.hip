@@ -515,6 +515,82 @@ __global__ __launch_bounds__(kWaveSize) void paged_decode_wide_kernel(PagedArgs 
 constexpr int kMfmaHeads = 16;
 constexpr int kMfmaChunk = 16;
 
+/// One wave's walk over the block table of a (sequence, split), for the
+/// matrix-core kernels. A wave takes steps of kTok consecutive tokens,
+/// c0, c0 + stride, ...; lane k of a step reads token c0 + k (k < 32).
+/// 64 block-table entries sit in lane registers (a token's block is a lane
+/// shuffle, not a dependent load). The block and in-block position of c0
+/// (q0, r0; wave uniform) advance by whole steps, so no lane divides by the
+/// block size: token c0 + k is in block q0 + dq with dq = (r0 + k) / block
+/// size, where r0 + k < block size + 32. For blocks of 32 tokens or more dq is
+/// 0 or 1; below that it is the quotient of two numbers under 64, exact from a
+/// float reciprocal and one upward correction (the float product is within
+/// 2^-23 of r / block size, which is at least 1 / 32 from the next integer
+/// unless it is one).
+struct TokenCursor {
+    const uint32_t* table;  // this sequence's block-table row
+    int64_t max_blocks;
+    uint32_t bs;            // block size (< 2^30, checked on the host)
+    float inv_bs;
+    uint32_t q0, r0;        // block and position of the step's first token
+    uint32_t step_q, step_r;
+    int64_t window_base;
+    int window;             // table[window_base + lane]
+
+    __device__ void load_window(int64_t base, int lane) {
+        const int64_t entry = base + lane < max_blocks ? base + lane : max_blocks - 1;
+        window_base = base;
+        window = static_cast<int>(table[entry]);
+    }
+    __device__ void start(const uint32_t* row, int64_t blocks, int64_t block_size, int64_t first,
+                          int64_t stride, int lane) {
+        table = row;
+        max_blocks = blocks;
+        bs = static_cast<uint32_t>(block_size);
+        inv_bs = 1.0f / static_cast<float>(bs);
+        q0 = static_cast<uint32_t>(first / block_size);
+        r0 = static_cast<uint32_t>(first % block_size);
+        step_q = static_cast<uint32_t>(stride / block_size);
+        step_r = static_cast<uint32_t>(stride % block_size);
+        load_window(q0, lane);
+    }
+    /// Move q0, r0 on by one stride.
+    __device__ void advance() {
+        q0 += step_q;
+        r0 += step_r;
+        if (r0 >= bs) {
+            r0 -= bs;
+            ++q0;
+        }
+    }
+    /// Make the window cover the blocks of tokens c0 .. c0 + tokens - 1.
+    __device__ void cover(int tokens, int lane) {
+        if (static_cast<int64_t>(q0) + tokens > window_base + kWaveSize || static_cast<int64_t>(q0) < window_base) {
+            load_window(q0, lane);
+        }
+    }
+    /// Cache row (block * block size + position) of token c0 + k, or of c0
+    /// itself when c0 + k is not below t_hi (such tokens are masked).
+    __device__ int64_t row(int64_t c0, int k, int64_t t_hi) const {
+        uint32_t blk = q0;
+        uint32_t pos = r0;
+        if (c0 + k < t_hi) {
+            const uint32_t r = r0 + static_cast<uint32_t>(k);
+            uint32_t dq;
+            if (bs >= 32) {
+                dq = r >= bs ? 1u : 0u;
+            } else {
+                dq = static_cast<uint32_t>(static_cast<float>(r) * inv_bs);
+                if ((dq + 1) * bs <= r) ++dq;
+            }
+            blk = q0 + dq;
+            pos = r - dq * bs;
+        }
+        const int64_t block = static_cast<uint32_t>(__shfl(window, static_cast<int>(blk - window_base)));
+        return block * bs + pos;
+    }
+};
+
 typedef __bf16 bf16x8_m __attribute__((ext_vector_type(8)));
 typedef short s16x4_m __attribute__((ext_vector_type(4)));
 typedef float f32x4_m __attribute__((ext_vector_type(4)));
@@ -574,53 +650,40 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
     const int64_t head_bytes = kv_head * kRowBytes;
     const uint32_t* table = a.tables + seq * a.max_blocks;
 
-    // 64 block-table entries in lane registers (a lane shuffle per token).
-    int64_t window_base = 0;
-    int window = 0;
-    auto load_window = [&](int64_t base) {
-        const int64_t entry = base + lane < a.max_blocks ? base + lane : a.max_blocks - 1;
-        window_base = base;
-        window = static_cast<int>(table[entry]);
-    };
-    // Byte offset of token t's row (t < t_hi; the chunk's blocks are in the window).
-    auto row_offset = [&](int64_t t) {
-        const int64_t block =
-            static_cast<uint32_t>(__shfl(window, static_cast<int>(t / a.block_size - window_base)));
-        return (block * a.block_size + t % a.block_size) * row_stride + head_bytes;
-    };
-
+    // Lane (g, j) loads the K and V rows of token 16 u + j of each sub-chunk:
+    // K dims 32 s + 8 g .. +7, V 16-byte pieces 4 i + g.
+    TokenCursor cur;
     bf16x8_m kfrag[kSubs][kS];
     u32x4_t vraw[kVPieces];
-    // Issue the loads of the chunk starting at c0 (< t_hi). Tokens past t_hi
-    // read the last valid token (their scores are masked).
     auto fetch = [&](int64_t c0) {
-        const int64_t last = (c0 + kTok - 1 < t_hi - 1 ? c0 + kTok - 1 : t_hi - 1);
-        if (last / a.block_size - window_base >= kWaveSize || c0 / a.block_size < window_base) {
-            load_window(c0 / a.block_size);
-        }
+        cur.cover(kTok, lane);
 #pragma unroll
         for (int u = 0; u < kSubs; ++u) {
-            const int64_t t0 = c0 + kMfmaChunk * u + j;
-            const int64_t off = row_offset(t0 < t_hi ? t0 : t_hi - 1);
+            const int64_t off = cur.row(c0, kMfmaChunk * u + j, t_hi) * row_stride + head_bytes;
 #pragma unroll
             for (int s = 0; s < kS; ++s) {
                 kfrag[u][s] = __builtin_bit_cast(bf16x8_m, load16(a.k_cache, off + (32 * s + 8 * g) * 2));
             }
-        }
 #pragma unroll
-        for (int i = 0; i < kVPieces; ++i) {
-            const int p = lane + kWaveSize * i;
-            const int64_t t0 = c0 + p / kPiecesPerRow;
-            const int64_t t = t0 < t_hi ? t0 : t_hi - 1;
-            vraw[i] = load16(a.v_cache, row_offset(t) + (p % kPiecesPerRow) * 16);
+            for (int i = 0; i < kPiecesPerRow / 4; ++i) {
+                vraw[u * (kPiecesPerRow / 4) + i] = load16(a.v_cache, off + (4 * i + g) * 16);
+            }
         }
     };
+    // Physical 16-byte piece of piece pc of V row rw in a wave's buffer:
+    // rotated by the row, so the 16 rows one store instruction writes fall in
+    // different banks.
+    auto v_piece = [](int rw, int pc) { return (pc + (rw & 15)) % kPiecesPerRow; };
     auto stage_v = [&](int buf) {
         uint8_t* base = lds + (wave * 2 + buf) * kVBytes;
 #pragma unroll
-        for (int i = 0; i < kVPieces; ++i) {
-            const int p = lane + kWaveSize * i;
-            *reinterpret_cast<u32x4_t*>(base + (p / kPiecesPerRow) * kRowBytes + (p % kPiecesPerRow) * 16) = vraw[i];
+        for (int u = 0; u < kSubs; ++u) {
+            const int rw = kMfmaChunk * u + j;
+#pragma unroll
+            for (int i = 0; i < kPiecesPerRow / 4; ++i) {
+                *reinterpret_cast<u32x4_t*>(base + rw * kRowBytes + v_piece(rw, 4 * i + g) * 16) =
+                    vraw[u * (kPiecesPerRow / 4) + i];
+            }
         }
     };
 
@@ -634,27 +697,27 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
     constexpr int64_t kStride = static_cast<int64_t>(kWaves) * kTok;
     int buf = 0;
     if (first < t_hi) {
-        load_window(first / a.block_size);
+        cur.start(table, a.max_blocks, a.block_size, first, kStride, lane);
         fetch(first);
         stage_v(0);
     }
     for (int64_t c0 = first; c0 < t_hi; c0 += kStride) {
-        bf16x8_m kcur[kSubs][kS];
-#pragma unroll
-        for (int u = 0; u < kSubs; ++u) {
-#pragma unroll
-            for (int s = 0; s < kS; ++s) kcur[u][s] = kfrag[u][s];
-        }
-        const int64_t next = c0 + kStride;
-        if (next < t_hi) fetch(next);
-
+        // The scores take this step's K fragments before the next step's
+        // loads reuse their registers.
         f32x4_m sc[kSubs];
-        float cmax = -INFINITY;
 #pragma unroll
         for (int u = 0; u < kSubs; ++u) {
             sc[u] = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int s = 0; s < kS; ++s) sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kcur[u][s], qfrag[s], sc[u], 0, 0, 0);
+            for (int s = 0; s < kS; ++s) sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfrag[u][s], qfrag[s], sc[u], 0, 0, 0);
+        }
+        const int64_t next = c0 + kStride;
+        cur.advance();
+        if (next < t_hi) fetch(next);
+
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kSubs; ++u) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 sc[u][t] = c0 + kMfmaChunk * u + 4 * g + t < t_hi ? sc[u][t] * a.scale : -INFINITY;
@@ -699,12 +762,14 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
         const uint8_t* vb = lds + (wave * 2 + buf) * kVBytes;
 #pragma unroll
         for (int b = 0; b < kB; ++b) {
-            const int off = (4 * g + (j >> 2)) * kRowBytes + (16 * b + 4 * (j & 3)) * 2;
+            const int rw = 4 * g + (j >> 2);
+            const int off = rw * kRowBytes + v_piece(rw, 2 * b + ((j & 3) >> 1)) * 16 + (j & 1) * 8;
             const s16x4_m v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_s16x4_m*)((lds_u8_m*)(const_cast<uint8_t*>(vb)) + off));
             if constexpr (kSubs == 1) {
                 acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v0, pb[0], acc[b], 0, 0, 0);
             } else {
+                // Row rw + 16 has the rotation of row rw.
                 const s16x4_m v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                     (lds_s16x4_m*)((lds_u8_m*)(const_cast<uint8_t*>(vb)) + off + kMfmaChunk * kRowBytes));
                 const bf16x8_m vv = __builtin_bit_cast(bf16x8_m, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -830,46 +895,24 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_f32_kernel(PagedArgs a) {
     const int64_t head_bytes = kv_head * kRowBytes;
     const uint32_t* table = a.tables + seq * a.max_blocks;
 
-    int64_t window_base = 0;
-    int window = 0;
-    auto load_window = [&](int64_t base) {
-        const int64_t entry = base + lane < a.max_blocks ? base + lane : a.max_blocks - 1;
-        window_base = base;
-        window = static_cast<int>(table[entry]);
-    };
-    auto row_offset = [&](int64_t t) {
-        const int64_t block =
-            static_cast<uint32_t>(__shfl(window, static_cast<int>(t / a.block_size - window_base)));
-        return (block * a.block_size + t % a.block_size) * row_stride + head_bytes;
-    };
-
+    // Lane (g, j) loads the K and V rows of token j: K dims 16 u + 4 g .. +3,
+    // V 16-byte pieces 4 i + g.
+    TokenCursor cur;
     u32x4_t kraw[kU];
     u32x4_t vraw[kVPieces];
     auto fetch = [&](int64_t c0) {
-        const int64_t last = (c0 + kMfmaChunk - 1 < t_hi - 1 ? c0 + kMfmaChunk - 1 : t_hi - 1);
-        if (last / a.block_size - window_base >= kWaveSize || c0 / a.block_size < window_base) {
-            load_window(c0 / a.block_size);
-        }
-        {
-            const int64_t t = c0 + j < t_hi ? c0 + j : t_hi - 1;
-            const int64_t off = row_offset(t);
+        cur.cover(kMfmaChunk, lane);
+        const int64_t off = cur.row(c0, j, t_hi) * row_stride + head_bytes;
 #pragma unroll
-            for (int u = 0; u < kU; ++u) kraw[u] = load16(a.k_cache, off + (16 * u + 4 * g) * 4);
-        }
+        for (int u = 0; u < kU; ++u) kraw[u] = load16(a.k_cache, off + (16 * u + 4 * g) * 4);
 #pragma unroll
-        for (int i = 0; i < kVPieces; ++i) {
-            const int p = lane + kWaveSize * i;
-            const int64_t t0 = c0 + p / kPiecesPerRow;
-            const int64_t t = t0 < t_hi ? t0 : t_hi - 1;
-            vraw[i] = load16(a.v_cache, row_offset(t) + (p % kPiecesPerRow) * 16);
-        }
+        for (int i = 0; i < kVPieces; ++i) vraw[i] = load16(a.v_cache, off + (4 * i + g) * 16);
     };
     auto stage_v = [&](int buf) {
         uint8_t* base = lds + (wave * 2 + buf) * kVBytes;
 #pragma unroll
         for (int i = 0; i < kVPieces; ++i) {
-            const int p = lane + kWaveSize * i;
-            *reinterpret_cast<u32x4_t*>(base + (p / kPiecesPerRow) * kLdsRow + (p % kPiecesPerRow) * 16) = vraw[i];
+            *reinterpret_cast<u32x4_t*>(base + j * kLdsRow + (4 * i + g) * 16) = vraw[i];
         }
     };
 
@@ -883,26 +926,25 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_f32_kernel(PagedArgs a) {
     constexpr int64_t kStride = static_cast<int64_t>(kWaves) * kMfmaChunk;
     int buf = 0;
     if (first < t_hi) {
-        load_window(first / a.block_size);
+        cur.start(table, a.max_blocks, a.block_size, first, kStride, lane);
         fetch(first);
         stage_v(0);
     }
     for (int64_t c0 = first; c0 < t_hi; c0 += kStride) {
-        f32x4_m kcur[kU];
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            kcur[u] = f32x4_m{__uint_as_float(kraw[u][0]), __uint_as_float(kraw[u][1]), __uint_as_float(kraw[u][2]),
-                              __uint_as_float(kraw[u][3])};
-        }
-        const int64_t next = c0 + kStride;
-        if (next < t_hi) fetch(next);
-
+        // The scores take this step's K before the next step's loads reuse
+        // its registers.
         f32x4_m sc = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kcur[u][e], qv[u][e], sc, 0, 0, 0);
+            for (int e = 0; e < 4; ++e) {
+                sc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kraw[u][e]), qv[u][e], sc, 0, 0, 0);
+            }
         }
+        const int64_t next = c0 + kStride;
+        cur.advance();
+        if (next < t_hi) fetch(next);
+
         float cmax = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -1016,6 +1058,8 @@ struct Plan {
 /// paged_mfma_f32_kernel (fp32 caches).
 constexpr int kMfmaPlan = -1;
 constexpr int kMfmaF32Plan = -2;
+/// The matrix-core kernels keep block indices and positions in 32 bits.
+constexpr int64_t kMfmaMaxBlockSize = int64_t{1} << 30;
 
 Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_dim,
               int64_t block_size, int64_t max_blocks, int64_t elem_bytes, bool may_split) {
@@ -1028,7 +1072,8 @@ Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_d
     // KV head, except groups of 2, where the streaming kernel is faster (bf16
     // D = 128, 64 x 1024 tokens: 69.0% of HBM peak against 66.8%). MHA 51.6
     // -> 56.3%, group 4 47.3 -> 61.3%, group 8 29.8 -> 60.7%.
-    if (elem_bytes == 2 && head_dim % 32 == 0 && head_dim <= 256 && group != 2 && group <= kMfmaHeads) {
+    if (elem_bytes == 2 && head_dim % 32 == 0 && head_dim <= 256 && group != 2 && group <= kMfmaHeads &&
+        block_size < kMfmaMaxBlockSize) {
         p.lanes = kMfmaPlan;
         p.gs = kMfmaHeads;
         p.head_groups = 1;
@@ -1041,6 +1086,7 @@ Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_d
     // groups of 2 (75.3 against 70.9%) stay on the streaming kernel.
     const bool one_round = sequences * kv_heads <= 2 * static_cast<int64_t>(cu_count());
     if (elem_bytes == 4 && head_dim % 16 == 0 && head_dim <= 128 && group <= kMfmaHeads &&
+        block_size < kMfmaMaxBlockSize &&
         (group >= 8 || (group >= 4 && one_round))) {
         p.lanes = kMfmaF32Plan;
         p.gs = kMfmaHeads;
