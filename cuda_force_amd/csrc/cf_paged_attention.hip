@@ -143,6 +143,91 @@ __device__ __forceinline__ void merge_into(HeadState<kVals>& s, float m2, float 
     s.m = m;
 }
 
+/// One wave's walk over the block table of a (sequence, split). A wave takes
+/// chunks of consecutive tokens c0, c0 + stride, ...; lane-relative token k of
+/// a chunk (k < kSpan) is token c0 + k. The block and in-block position of c0
+/// (q0, r0; wave uniform) advance by whole strides, so no lane divides by the
+/// block size: token c0 + k is in block q0 + dq with dq = (r0 + k) / block
+/// size, where r0 + k < block size + kSpan. For blocks of kSpan tokens or more
+/// dq is 0 or 1; below that it is the quotient of two numbers under 2 kSpan
+/// (<= 128), exact from a float reciprocal and one upward correction (the
+/// float product is within 2^-23 of r / block size, which is at least
+/// 1 / block size from the next integer unless it is one). Token positions
+/// are below 2^31 (int32 context lengths), so q0, r0 and r0 + k fit 32 bits
+/// for any block size; comparisons use the block size saturated to 32 bits.
+/// 64 block-table entries sit in lane registers, so a token's block is a lane
+/// shuffle, not a dependent load. The matrix-core kernels use it. The
+/// streaming kernel keeps its per-token division: with the cursor its fp32
+/// group-4 form needed 141 VGPRs instead of 118, one wave per SIMD fewer, and
+/// ran at 54% of HBM peak instead of 61% (128 x 256 tokens).
+template <int kSpan>
+struct TokenCursor {
+    static_assert(kSpan >= 1 && kSpan <= kWaveSize, "span");
+    const uint32_t* table;  // this sequence's block-table row
+    int64_t max_blocks;
+    int64_t block_size;
+    uint32_t bs;            // block size saturated to 32 bits
+    float inv_bs;
+    uint32_t q0, r0;        // block and position of the chunk's first token
+    uint32_t step_q, step_r;
+    int64_t window_base;
+    int window;             // table[window_base + lane]
+
+    __device__ void load_window(int64_t base, int lane) {
+        const int64_t entry = base + lane < max_blocks ? base + lane : max_blocks - 1;
+        window_base = base;
+        window = static_cast<int>(table[entry]);
+    }
+    __device__ void start(const uint32_t* row, int64_t blocks, int64_t size, int64_t first, int64_t stride,
+                          int lane) {
+        table = row;
+        max_blocks = blocks;
+        block_size = size;
+        bs = size < int64_t{0xFFFFFFFF} ? static_cast<uint32_t>(size) : 0xFFFFFFFFu;
+        inv_bs = 1.0f / static_cast<float>(bs);
+        q0 = static_cast<uint32_t>(first / size);
+        r0 = static_cast<uint32_t>(first % size);
+        step_q = static_cast<uint32_t>(stride / size);
+        step_r = static_cast<uint32_t>(stride % size);
+        load_window(q0, lane);
+    }
+    /// Move q0, r0 on by one stride.
+    __device__ void advance() {
+        q0 += step_q;
+        r0 += step_r;
+        if (r0 >= bs) {
+            r0 -= bs;
+            ++q0;
+        }
+    }
+    /// Make the window cover the blocks of tokens c0 .. c0 + kSpan - 1.
+    __device__ void cover(int lane) {
+        if (static_cast<int64_t>(q0) + kSpan > window_base + kWaveSize || static_cast<int64_t>(q0) < window_base) {
+            load_window(q0, lane);
+        }
+    }
+    /// Cache row (block * block size + position) of token c0 + k, or of c0
+    /// itself when c0 + k is not below t_hi (such tokens are masked).
+    __device__ int64_t row(int64_t c0, int k, int64_t t_hi) const {
+        uint32_t blk = q0;
+        uint32_t pos = r0;
+        if (c0 + k < t_hi) {
+            const uint32_t r = r0 + static_cast<uint32_t>(k);
+            uint32_t dq;
+            if (bs >= static_cast<uint32_t>(kSpan)) {
+                dq = r >= bs ? 1u : 0u;
+            } else {
+                dq = static_cast<uint32_t>(static_cast<float>(r) * inv_bs);
+                if ((dq + 1) * bs <= r) ++dq;
+            }
+            blk = q0 + dq;
+            pos = r - dq * bs;
+        }
+        const int64_t block = static_cast<uint32_t>(__shfl(window, static_cast<int>(blk - window_base)));
+        return block * block_size + pos;
+    }
+};
+
 /// kLanes = D / kVals lanes per token (kVals = 16 bytes of T), kGroup query
 /// heads per workgroup.
 ///
@@ -515,82 +600,6 @@ __global__ __launch_bounds__(kWaveSize) void paged_decode_wide_kernel(PagedArgs 
 constexpr int kMfmaHeads = 16;
 constexpr int kMfmaChunk = 16;
 
-/// One wave's walk over the block table of a (sequence, split), for the
-/// matrix-core kernels. A wave takes steps of kTok consecutive tokens,
-/// c0, c0 + stride, ...; lane k of a step reads token c0 + k (k < 32).
-/// 64 block-table entries sit in lane registers (a token's block is a lane
-/// shuffle, not a dependent load). The block and in-block position of c0
-/// (q0, r0; wave uniform) advance by whole steps, so no lane divides by the
-/// block size: token c0 + k is in block q0 + dq with dq = (r0 + k) / block
-/// size, where r0 + k < block size + 32. For blocks of 32 tokens or more dq is
-/// 0 or 1; below that it is the quotient of two numbers under 64, exact from a
-/// float reciprocal and one upward correction (the float product is within
-/// 2^-23 of r / block size, which is at least 1 / 32 from the next integer
-/// unless it is one).
-struct TokenCursor {
-    const uint32_t* table;  // this sequence's block-table row
-    int64_t max_blocks;
-    uint32_t bs;            // block size (< 2^30, checked on the host)
-    float inv_bs;
-    uint32_t q0, r0;        // block and position of the step's first token
-    uint32_t step_q, step_r;
-    int64_t window_base;
-    int window;             // table[window_base + lane]
-
-    __device__ void load_window(int64_t base, int lane) {
-        const int64_t entry = base + lane < max_blocks ? base + lane : max_blocks - 1;
-        window_base = base;
-        window = static_cast<int>(table[entry]);
-    }
-    __device__ void start(const uint32_t* row, int64_t blocks, int64_t block_size, int64_t first,
-                          int64_t stride, int lane) {
-        table = row;
-        max_blocks = blocks;
-        bs = static_cast<uint32_t>(block_size);
-        inv_bs = 1.0f / static_cast<float>(bs);
-        q0 = static_cast<uint32_t>(first / block_size);
-        r0 = static_cast<uint32_t>(first % block_size);
-        step_q = static_cast<uint32_t>(stride / block_size);
-        step_r = static_cast<uint32_t>(stride % block_size);
-        load_window(q0, lane);
-    }
-    /// Move q0, r0 on by one stride.
-    __device__ void advance() {
-        q0 += step_q;
-        r0 += step_r;
-        if (r0 >= bs) {
-            r0 -= bs;
-            ++q0;
-        }
-    }
-    /// Make the window cover the blocks of tokens c0 .. c0 + tokens - 1.
-    __device__ void cover(int tokens, int lane) {
-        if (static_cast<int64_t>(q0) + tokens > window_base + kWaveSize || static_cast<int64_t>(q0) < window_base) {
-            load_window(q0, lane);
-        }
-    }
-    /// Cache row (block * block size + position) of token c0 + k, or of c0
-    /// itself when c0 + k is not below t_hi (such tokens are masked).
-    __device__ int64_t row(int64_t c0, int k, int64_t t_hi) const {
-        uint32_t blk = q0;
-        uint32_t pos = r0;
-        if (c0 + k < t_hi) {
-            const uint32_t r = r0 + static_cast<uint32_t>(k);
-            uint32_t dq;
-            if (bs >= 32) {
-                dq = r >= bs ? 1u : 0u;
-            } else {
-                dq = static_cast<uint32_t>(static_cast<float>(r) * inv_bs);
-                if ((dq + 1) * bs <= r) ++dq;
-            }
-            blk = q0 + dq;
-            pos = r - dq * bs;
-        }
-        const int64_t block = static_cast<uint32_t>(__shfl(window, static_cast<int>(blk - window_base)));
-        return block * bs + pos;
-    }
-};
-
 typedef __bf16 bf16x8_m __attribute__((ext_vector_type(8)));
 typedef short s16x4_m __attribute__((ext_vector_type(4)));
 typedef float f32x4_m __attribute__((ext_vector_type(4)));
@@ -619,7 +628,7 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
 
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & (kWaveSize - 1);
-    const int wave = tid / kWaveSize;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveSize);  // uniform: scalar wave-level state
     const int g = lane >> 4;
     const int j = lane & 15;
 
@@ -652,11 +661,11 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
 
     // Lane (g, j) loads the K and V rows of token 16 u + j of each sub-chunk:
     // K dims 32 s + 8 g .. +7, V 16-byte pieces 4 i + g.
-    TokenCursor cur;
+    TokenCursor<kTok> cur;
     bf16x8_m kfrag[kSubs][kS];
     u32x4_t vraw[kVPieces];
     auto fetch = [&](int64_t c0) {
-        cur.cover(kTok, lane);
+        cur.cover(lane);
 #pragma unroll
         for (int u = 0; u < kSubs; ++u) {
             const int64_t off = cur.row(c0, kMfmaChunk * u + j, t_hi) * row_stride + head_bytes;
@@ -864,7 +873,7 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_f32_kernel(PagedArgs a) {
 
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & (kWaveSize - 1);
-    const int wave = tid / kWaveSize;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveSize);  // uniform: scalar wave-level state
     const int g = lane >> 4;
     const int j = lane & 15;
 
@@ -897,11 +906,11 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_f32_kernel(PagedArgs a) {
 
     // Lane (g, j) loads the K and V rows of token j: K dims 16 u + 4 g .. +3,
     // V 16-byte pieces 4 i + g.
-    TokenCursor cur;
+    TokenCursor<kMfmaChunk> cur;
     u32x4_t kraw[kU];
     u32x4_t vraw[kVPieces];
     auto fetch = [&](int64_t c0) {
-        cur.cover(kMfmaChunk, lane);
+        cur.cover(lane);
         const int64_t off = cur.row(c0, j, t_hi) * row_stride + head_bytes;
 #pragma unroll
         for (int u = 0; u < kU; ++u) kraw[u] = load16(a.k_cache, off + (16 * u + 4 * g) * 4);
@@ -1058,8 +1067,6 @@ struct Plan {
 /// paged_mfma_f32_kernel (fp32 caches).
 constexpr int kMfmaPlan = -1;
 constexpr int kMfmaF32Plan = -2;
-/// The matrix-core kernels keep block indices and positions in 32 bits.
-constexpr int64_t kMfmaMaxBlockSize = int64_t{1} << 30;
 
 Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_dim,
               int64_t block_size, int64_t max_blocks, int64_t elem_bytes, bool may_split) {
@@ -1072,8 +1079,7 @@ Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_d
     // KV head, except groups of 2, where the streaming kernel is faster (bf16
     // D = 128, 64 x 1024 tokens: 69.0% of HBM peak against 66.8%). MHA 51.6
     // -> 56.3%, group 4 47.3 -> 61.3%, group 8 29.8 -> 60.7%.
-    if (elem_bytes == 2 && head_dim % 32 == 0 && head_dim <= 256 && group != 2 && group <= kMfmaHeads &&
-        block_size < kMfmaMaxBlockSize) {
+    if (elem_bytes == 2 && head_dim % 32 == 0 && head_dim <= 256 && group != 2 && group <= kMfmaHeads) {
         p.lanes = kMfmaPlan;
         p.gs = kMfmaHeads;
         p.head_groups = 1;
@@ -1086,7 +1092,6 @@ Plan plan_for(int64_t sequences, int64_t heads, int64_t kv_heads, int64_t head_d
     // groups of 2 (75.3 against 70.9%) stay on the streaming kernel.
     const bool one_round = sequences * kv_heads <= 2 * static_cast<int64_t>(cu_count());
     if (elem_bytes == 4 && head_dim % 16 == 0 && head_dim <= 128 && group <= kMfmaHeads &&
-        block_size < kMfmaMaxBlockSize &&
         (group >= 8 || (group >= 4 && one_round))) {
         p.lanes = kMfmaF32Plan;
         p.gs = kMfmaHeads;
