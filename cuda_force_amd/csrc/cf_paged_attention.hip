@@ -157,9 +157,9 @@ __device__ __forceinline__ void merge_into(HeadState<kVals>& s, float m2, float 
 /// for any block size; comparisons use the block size saturated to 32 bits.
 /// 64 block-table entries sit in lane registers, so a token's block is a lane
 /// shuffle, not a dependent load. The matrix-core kernels use it. The
-/// streaming kernel keeps its per-token division: with the cursor its fp32
-/// group-4 form needed 141 VGPRs instead of 118, one wave per SIMD fewer, and
-/// ran at 54% of HBM peak instead of 61% (128 x 256 tokens).
+/// streaming kernel keeps a per-token (32-bit) division: with the cursor its
+/// fp32 group-4 form needed 141 VGPRs instead of 118, one wave per SIMD fewer,
+/// and ran at 54% of HBM peak instead of 61% (128 x 256 tokens).
 template <int kSpan>
 struct TokenCursor {
     static_assert(kSpan >= 1 && kSpan <= kWaveSize, "span");
@@ -322,7 +322,10 @@ __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 4 : 1, 8))) void paged_decod
 
     // A window of 64 block-table entries, one per lane, so the K/V addresses
     // of a chunk need a lane shuffle rather than a dependent memory load.
-    int64_t window_base = w_lo / a.block_size;
+    // Token positions are below 2^31 (int32 context lengths): 32-bit
+    // quotients are exact, with the block size saturated to 32 bits.
+    const uint32_t bs32 = a.block_size < int64_t{0xFFFFFFFF} ? static_cast<uint32_t>(a.block_size) : 0xFFFFFFFFu;
+    int64_t window_base = static_cast<uint32_t>(w_lo) / bs32;
     auto load_window = [&](int64_t base) {
         const int64_t entry = base + lane < a.max_blocks ? base + lane : a.max_blocks - 1;
         return static_cast<int>(table[entry]);
@@ -333,8 +336,8 @@ __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 4 : 1, 8))) void paged_decod
         // Uniform decisions: every lane sees the same chunk. A chunk spanning
         // more blocks than the window holds (tiny blocks) reads the table
         // directly.
-        const int64_t first_block = t0 / a.block_size;
-        const int64_t last_block = (t0 + kChunk - 1 < w_hi - 1 ? t0 + kChunk - 1 : w_hi - 1) / a.block_size;
+        const int64_t first_block = static_cast<uint32_t>(t0) / bs32;
+        const int64_t last_block = static_cast<uint32_t>(t0 + kChunk - 1 < w_hi - 1 ? t0 + kChunk - 1 : w_hi - 1) / bs32;
         const bool windowed = last_block - first_block < kWaveSize;
         if (windowed && last_block - window_base >= kWaveSize) {
             window_base = first_block;
@@ -344,10 +347,12 @@ __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 4 : 1, 8))) void paged_decod
         for (int u = 0; u < kStepsPerLoad; ++u) {
             const int64_t t = t0 + u * kTokensPerStep + slot;
             const int64_t tc = t < w_hi ? t : w_hi - 1;  // a valid token even past the end
+            const uint32_t bq = static_cast<uint32_t>(tc) / bs32;
+            const uint32_t br = static_cast<uint32_t>(tc) - bq * bs32;
             const int64_t block =
-                windowed ? static_cast<uint32_t>(__shfl(window, static_cast<int>(tc / a.block_size - window_base)))
-                         : table[tc / a.block_size];
-            const int64_t offset = (block * a.block_size + tc % a.block_size) * row_bytes + piece_bytes;
+                windowed ? static_cast<uint32_t>(__shfl(window, static_cast<int>(bq - window_base)))
+                         : table[bq];
+            const int64_t offset = (block * a.block_size + br) * row_bytes + piece_bytes;
             raw[u][0] = load16(a.k_cache, offset);
             raw[u][1] = load16(a.v_cache, offset);
         }
