@@ -211,3 +211,31 @@ def test_block_sizes_around_the_table_window(block_size):
         case = make_case(*dims, seed=block_size)
         np.testing.assert_allclose(run_gpu(case), run_oracle(case), rtol=0, atol=FP32_MARGIN)
         np.testing.assert_allclose(run_gpu(case, workspace=False), run_oracle(case), rtol=0, atol=FP32_MARGIN)
+
+
+@pytest.mark.parametrize("block_size", [3, 7, 31, 33, 100], ids=lambda b: f"block{b}")
+def test_block_sizes_that_are_not_powers_of_two(block_size):
+    """Block sizes that are not powers of two, through each kernel family:
+    the matrix-core kernels walk the table with a per-wave block cursor (an
+    exact float quotient below 32 tokens per block, a compare from 32 up) and
+    the streaming kernel with a 32-bit quotient per token. Contexts cross
+    steps, blocks and (for small blocks) reloads of the 64-entry table window.
+    fp32 within the reference's 2e-5 margin, bf16 within 1e-2 of the output
+    scale, with and without the split workspace."""
+    announce(f"paged attention block size {block_size} (not a power of two)")
+    cases = [
+        ("f32", (2, 16, 2, 128, [700, 45])),   # group 8: fp32 matrix-core kernel
+        ("f32", (2, 4, 4, 128, [700, 45])),    # MHA: fp32 streaming kernel
+        ("bf16", (2, 8, 2, 128, [700, 45])),   # group 4: bf16 matrix-core kernel
+        ("bf16", (2, 4, 2, 64, [700, 45])),    # group 2: bf16 streaming kernel
+    ]
+    for dtype, (s, h, kvh, d, ctx) in cases:
+        case = make_case(s, h, kvh, d, block_size, ctx, seed=block_size * 7 + h)
+        expected = expected_for(case, dtype)
+        for workspace in (True, False):
+            got = run_gpu(case, dtype, workspace=workspace)
+            if dtype == "f32":
+                np.testing.assert_allclose(got, expected, rtol=0, atol=FP32_MARGIN)
+            else:
+                err = np.abs(got - expected).max()
+                assert err <= 1e-2 * np.abs(expected).max(), f"{dtype} {h}/{kvh} workspace={workspace}: {err:.3e}"
