@@ -601,7 +601,9 @@ __global__ __launch_bounds__(kWaveSize) void paged_decode_wide_kernel(PagedArgs 
 /// probabilities as bf16 (exactly the score layout), the A operand is V^T
 /// read transposed (ds_read_b64_tr_b16) out of a per-wave LDS copy of the
 /// chunk's V rows. The next chunk's K and V loads are in flight while a chunk
-/// is computed. The 4 waves' states merge through LDS at the end.
+/// is computed. The waves' states merge through LDS at the end. Four waves
+/// serve one (sequence, KV head, split), or two when a one-round grid allows
+/// (two per workgroup, half the workgroups, each wave twice the tokens).
 constexpr int kMfmaHeads = 16;
 constexpr int kMfmaChunk = 16;
 
@@ -611,10 +613,11 @@ typedef float f32x4_m __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_m lds_s16x4_m;
 typedef __attribute__((address_space(3))) uint8_t lds_u8_m;
 
-template <int kD, int kSubs>
+template <int kD, int kSubs, int kPW>
 __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
     // kSubs 16-token sub-chunks per step (one or two): two keep twice the
-    // bytes in flight per wave.
+    // bytes in flight per wave. kPW waves (4 or 2) serve one (sequence, KV
+    // head, split); a workgroup holds kWaves / kPW of them.
     constexpr int kTok = kMfmaChunk * kSubs;                // tokens per step
     constexpr int kS = kD / 32;                             // score MFMAs per sub-chunk
     constexpr int kB = kD / 16;                             // P.V output blocks
@@ -637,7 +640,9 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
     const int g = lane >> 4;
     const int j = lane & 15;
 
-    int64_t id = blockIdx.x;
+    const int sub = wave / kPW;  // this wave's (sequence, KV head, split) in the workgroup
+    const int wv = wave % kPW;   // and its place among the kPW waves serving it
+    int64_t id = static_cast<int64_t>(blockIdx.x) * (kWaves / kPW) + sub;
     const int split = static_cast<int>(id % a.splits);
     id /= a.splits;
     const int64_t kv_head = id % a.kv_heads;
@@ -707,8 +712,8 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
 #pragma unroll
     for (int b = 0; b < kB; ++b) acc[b] = f32x4_m{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int64_t first = t_lo + static_cast<int64_t>(wave) * kTok;
-    constexpr int64_t kStride = static_cast<int64_t>(kWaves) * kTok;
+    const int64_t first = t_lo + static_cast<int64_t>(wv) * kTok;
+    constexpr int64_t kStride = static_cast<int64_t>(kPW) * kTok;
     int buf = 0;
     if (first < t_hi) {
         cur.start(table, a.max_blocks, a.block_size, first, kStride, lane);
@@ -815,18 +820,20 @@ __global__ __launch_bounds__(kThreads) void paged_mfma_kernel(PagedArgs a) {
     }
     __syncthreads();
 
-    // Merge: thread tid handles (head, dim) pairs tid, tid + kThreads, ...
-    for (int pair = tid; pair < kMfmaHeads * kD; pair += kThreads) {
+    // Merge the kPW waves w0 .. w0 + kPW - 1: their threads take (head, dim)
+    // pairs in turn.
+    const int w0 = sub * kPW;
+    for (int pair = tid % (kPW * kWaveSize); pair < kMfmaHeads * kD; pair += kPW * kWaveSize) {
         const int h = pair / kD;
         const int d = pair % kD;
         if (h >= group) continue;
         float mm = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, lds_m[w][h]);
+        for (int w = w0; w < w0 + kPW; ++w) mm = fmaxf(mm, lds_m[w][h]);
         float ll = 0.0f;
         float oo = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = w0; w < w0 + kPW; ++w) {
             const float cw = lds_m[w][h] == -INFINITY ? 0.0f : __expf(lds_m[w][h] - mm);
             ll = fmaf(lds_l[w][h], cw, ll);
             oo = fmaf(macc[(w * kMfmaHeads + h) * kD + d], cw, oo);
@@ -1178,18 +1185,33 @@ void launch_typed(const PagedArgs& args, const Plan& plan, int64_t sequences, hi
     }
     if constexpr (!std::is_same<T, float>::value) {
       if (plan.lanes == kMfmaPlan) {
-        const dim3 grid(static_cast<unsigned>(workgroups));
+        // Two waves per (sequence, KV head, split) for GQA when one round of
+        // two workgroups per CU holds them all: each wave then takes twice the
+        // tokens and the grid halves (bf16 D = 128, 64 x 1024 tokens: group 4
+        // 63.8 -> 68.1% of HBM peak, group 8 63.4 -> 66.5%). With two rounds
+        // (128 x 256 tokens, 54.2 -> 52.8%) and for MHA (16 x 512 tokens, 58.8
+        // -> 57.5%) it was slower.
+        const bool pair_waves = args.heads > args.kv_heads && workgroups % 2 == 0 &&
+                                workgroups <= 2 * static_cast<int64_t>(cu_count());
+        const dim3 grid(static_cast<unsigned>(pair_waves ? workgroups / 2 : workgroups));
         // Two sub-chunks per step up to D = 128 (64 KiB of LDS), one above.
         constexpr int kSubsSmall = 2;
+        auto go = [&](auto k4, auto k2) {
+            if (pair_waves) {
+                launch(k2, grid, dim3(kThreads), 0, stream, args);
+            } else {
+                launch(k4, grid, dim3(kThreads), 0, stream, args);
+            }
+        };
         switch (args.head_dim / 32) {
-            case 1: launch(paged_mfma_kernel<32, kSubsSmall>, grid, dim3(kThreads), 0, stream, args); break;
-            case 2: launch(paged_mfma_kernel<64, kSubsSmall>, grid, dim3(kThreads), 0, stream, args); break;
-            case 3: launch(paged_mfma_kernel<96, kSubsSmall>, grid, dim3(kThreads), 0, stream, args); break;
-            case 4: launch(paged_mfma_kernel<128, kSubsSmall>, grid, dim3(kThreads), 0, stream, args); break;
-            case 5: launch(paged_mfma_kernel<160, 1>, grid, dim3(kThreads), 0, stream, args); break;
-            case 6: launch(paged_mfma_kernel<192, 1>, grid, dim3(kThreads), 0, stream, args); break;
-            case 7: launch(paged_mfma_kernel<224, 1>, grid, dim3(kThreads), 0, stream, args); break;
-            default: launch(paged_mfma_kernel<256, 1>, grid, dim3(kThreads), 0, stream, args); break;
+            case 1: go(paged_mfma_kernel<32, kSubsSmall, 4>, paged_mfma_kernel<32, kSubsSmall, 2>); break;
+            case 2: go(paged_mfma_kernel<64, kSubsSmall, 4>, paged_mfma_kernel<64, kSubsSmall, 2>); break;
+            case 3: go(paged_mfma_kernel<96, kSubsSmall, 4>, paged_mfma_kernel<96, kSubsSmall, 2>); break;
+            case 4: go(paged_mfma_kernel<128, kSubsSmall, 4>, paged_mfma_kernel<128, kSubsSmall, 2>); break;
+            case 5: go(paged_mfma_kernel<160, 1, 4>, paged_mfma_kernel<160, 1, 2>); break;
+            case 6: go(paged_mfma_kernel<192, 1, 4>, paged_mfma_kernel<192, 1, 2>); break;
+            case 7: go(paged_mfma_kernel<224, 1, 4>, paged_mfma_kernel<224, 1, 2>); break;
+            default: go(paged_mfma_kernel<256, 1, 4>, paged_mfma_kernel<256, 1, 2>); break;
         }
         if (plan.splits > 1) {
             launch(paged_combine_kernel<T>, dim3(static_cast<unsigned>(sequences * args.heads)), dim3(kWaveSize), 0,
