@@ -26,6 +26,13 @@ profiles/ (null when absent). `cpu_baseline` times the reference's own CPU
 operators (oracle/_ref, built from the reference source) on the same step,
 each op for about --cpu-seconds of CPU work, on this host's cores.
 
+The stdout line stays under 4 KB: besides the contract's fields it carries
+`configs`, a few figures per configuration (C1 quantise/dequantise GB/s, C2
+RMSNorm GB/s and the softmax's microseconds, C3 fused LoRA TFLOP/s with
+hipBLASLt's plain GEMM beside it and the adapter backward GB/s, C4 tokens/s,
+C5 aggregate GB/s). The full breakdown goes to the `--detail` file
+(gpurun_out/bench_detail.json by default) and nowhere else.
+
 `breakdown` reports every other configuration (`--configs` selects them):
 median over 5 batches of back-to-back launches timed by HIP events, after at
 least 0.3 s of warm-up, with cache-cold rotation (`median_ms`: launch-to-launch
@@ -704,8 +711,10 @@ def bench_lora(torch, cf, warmup: int, runs: int) -> dict:
             gb.data_ptr(), cf._lib.CF_BF16, m, k, n, r, 2.0, ws.data_ptr(), nbytes,
             torch.cuda.current_stream().cuda_stream))
 
-    bw = summary(time_launches(torch, [backward(s) for s in sets], warmup, runs))
+    bw_launches = [backward(s) for s in sets]
+    bw = summary(time_launches(torch, bw_launches, warmup, runs))
     bw_bytes = m * k * 2 + m * n * 2 + m * r * 4 + r * n * 2 + k * r * 2 + r * n * 2
+    with_kernel_time(torch, cf, bw, bw_launches, nbytes=bw_bytes)
     out["lora_backward_bf16_8192x4096x4096_r16"] = {**bw, "bytes": bw_bytes, "buffer_sets": len(sets),
                                                     "GB/s": gbs(bw_bytes, bw["median_ms"]),
                                                     "frac_hbm": gbs(bw_bytes, bw["median_ms"]) / PEAK_HBM_GBS}
@@ -986,6 +995,56 @@ def cpu_baseline(seconds: float) -> dict | None:
     }
 
 
+def _sig(v, digits: int = 4):
+    """A float rounded to `digits` significant digits (keeps the stdout line short)."""
+    if isinstance(v, float):
+        return float(f"{v:.{digits}g}")
+    return v
+
+
+# Summary fields of the stdout line: (config, field) -> (breakdown key, entry field).
+# Kernel-timestamp medians where the entry has them, else launch-to-launch medians.
+SUMMARY_FIELDS = {
+    "c1": {"quantize_GB/s": ("quantize_f32_4096x4096", "kernel_GB/s"),
+           "quantize_frac_hbm": ("quantize_f32_4096x4096", "kernel_frac_hbm"),
+           "dequantize_GB/s": ("dequantize_f32_4096x4096", "kernel_GB/s"),
+           "dequantize_frac_hbm": ("dequantize_f32_4096x4096", "kernel_frac_hbm")},
+    "c2": {"rmsnorm_GB/s": ("rmsnorm_bf16_16384x4096", "kernel_GB/s"),
+           "rmsnorm_frac_hbm": ("rmsnorm_bf16_16384x4096", "kernel_frac_hbm"),
+           "softmax_us": ("softmax_bf16_causal_1024x2048", "kernel_median_ms")},
+    "c3": {"fused_TFLOP/s": ("lora_bf16_8192x4096x4096_r16", "kernel_TFLOP/s"),
+           "fused_frac_mfma": ("lora_bf16_8192x4096x4096_r16", "kernel_frac_peak"),
+           "hipblaslt_gemm_TFLOP/s": ("hipblaslt_gemm_bf16_8192x4096x4096_context", "TFLOP/s"),
+           "backward_GB/s": ("lora_backward_bf16_8192x4096x4096_r16", "kernel_GB/s"),
+           "backward_frac_hbm": ("lora_backward_bf16_8192x4096x4096_r16", "kernel_frac_hbm")},
+    "c4": {"tokens/s": ("block_c4_bf16_8x512_h4096", "tokens/s")},
+    "c5": {"quantize_GB/s": ("bulk_7b_quantize_bf16", "GB/s"),
+           "quantize_frac_hbm": ("bulk_7b_quantize_bf16", "frac_hbm"),
+           "dequantize_GB/s": ("bulk_7b_dequantize_bf16", "GB/s"),
+           "dequantize_frac_hbm": ("bulk_7b_dequantize_bf16", "frac_hbm")},
+}
+
+
+def config_summary(breakdown: dict) -> dict:
+    """One or a few numbers per configuration, picked from the full breakdown."""
+    out = {}
+    for config, fields in SUMMARY_FIELDS.items():
+        picked = {}
+        for name, (key, field) in fields.items():
+            value = breakdown.get(key, {}).get(field)
+            if value is None:
+                continue
+            if name.endswith("_us"):
+                value = value * 1e3
+            picked[name] = _sig(value)
+        if picked:
+            out[config] = picked
+    return out
+
+
+STDOUT_LINE_LIMIT = 4000  # bytes; the driver parses the last stdout line
+
+
 def profiled_traffic() -> float | None:
     """HBM bytes per RMSNorm launch from the committed rocprofv3 counter summary."""
     path = ROOT / "profiles" / "rmsnorm_bf16_c2_traffic.md"
@@ -1007,7 +1066,8 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--configs", default="1,ceiling,reference,2,reduce,3,4,5,paged,tensorcore,fp8",
                         help="breakdown configs to run (comma-separated: 1-5, ceiling, reference, "
                              "reduce, paged, tensorcore, fp8)")
-    parser.add_argument("--detail", default="", help="also write the full result JSON here")
+    parser.add_argument("--detail", default=str(ROOT / "gpurun_out" / "bench_detail.json"),
+                        help="write the full result JSON, with every breakdown entry, here ('' for none)")
     args = parser.parse_args(argv)
 
     if args.gpus != 1:
@@ -1089,12 +1149,24 @@ def main(argv: list[str] | None = None) -> int:
             "traffic": profiled_traffic(),
         },
         "cpu_baseline": baseline,
-        "breakdown": breakdown,
+        "configs": config_summary(breakdown),
     }
     if args.detail:
-        Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
-        Path(args.detail).write_text(json.dumps(line, indent=2) + "\n", encoding="utf-8")
-    print(json.dumps(line), flush=True)
+        try:
+            Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
+            Path(args.detail).write_text(json.dumps({**line, "breakdown": breakdown}, indent=2) + "\n",
+                                         encoding="utf-8")
+            log(f"full breakdown written to {args.detail}")
+        except OSError as exc:
+            log(f"could not write {args.detail}: {exc}")
+    for config, figures in line["configs"].items():
+        log(f"{config}: {json.dumps(figures)}")
+    text = json.dumps(line, separators=(",", ":"))
+    if len(text) > STDOUT_LINE_LIMIT:
+        log(f"summary line is {len(text)} bytes; dropping the per-config figures from it")
+        line["configs"] = None
+        text = json.dumps(line, separators=(",", ":"))
+    print(text, flush=True)
     return 0
 
 

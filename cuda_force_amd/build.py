@@ -59,12 +59,15 @@ OFFLOAD_ARCH = "gfx950"
 # -packed-fp32-ops keeps the compiler from emitting packed fp32 VALU ops
 # (v_pk_add/mul/fma_f32), which this hardware pool has miscomputed
 # intermittently. No -ffast-math: the quantiser relies on IEEE division and
-# the default correctly-rounded sqrt.
+# the default correctly-rounded sqrt. -fvisibility=hidden: only the C ABI
+# (declared default-visible in include/cudaforge_hip.h) is exported.
 HIPCC_FLAGS = (
     f"--offload-arch={OFFLOAD_ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
+    "-fvisibility=hidden",
+    "-fvisibility-inlines-hidden",
     "-Wall",
     "-Xclang",
     "-target-feature",

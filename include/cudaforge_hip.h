@@ -36,6 +36,11 @@
 #include <stddef.h>
 #include <stdint.h>
 
+/* The library is built with -fvisibility=hidden: the entry points below are
+ * its only exported symbols, so two builds loaded into one process share no
+ * internal C++ symbol. */
+#pragma GCC visibility push(default)
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -621,5 +626,7 @@ const char* cf_pool_backend_name(cf_pool_backend backend);
 #ifdef __cplusplus
 }
 #endif
+
+#pragma GCC visibility pop
 
 #endif /* CUDAFORGE_HIP_H */

@@ -40,8 +40,36 @@ def to_host(tensor: torch.Tensor) -> np.ndarray:
     return t.numpy()
 
 
+def poison_(t: torch.Tensor) -> torch.Tensor:
+    """Fill a buffer in place with a bit pattern no kernel stores, so that an
+    element a kernel leaves unwritten fails the comparison that follows
+    (the reference's kernel tests zero-fill outputs for the same reason,
+    tests/cuda/cuda_test_utils.cuh:93-111):
+
+    * floats: every bit set - a negative NaN with a full payload, never the
+      canonical NaN (bf16 0x7FC0, fp16 0x7E00/0xFE00, fp32 0x7FC00000) that
+      a kernel writes, and NaN fails every tolerance check;
+    * int8: -128, outside the quantiser's code range [-127, 127];
+    * other integer buffers (workspaces): 0xA5 bytes."""
+    if t.numel() == 0:
+        return t
+    if t.dtype == torch.int8:
+        t.fill_(-128)
+    elif t.dtype.is_floating_point:
+        ints = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[t.element_size()]
+        t.view(ints).fill_(-1 if ints is not torch.uint8 else 0xFF)
+    else:
+        t.view(torch.uint8).fill_(0xA5)
+    return t
+
+
 def empty(shape, dtype: torch.dtype) -> torch.Tensor:
-    return torch.empty(shape, dtype=dtype, device=DEVICE)
+    """A poisoned device buffer (see poison_)."""
+    return poison_(torch.empty(shape, dtype=dtype, device=DEVICE))
+
+
+def poison_like(t: torch.Tensor) -> torch.Tensor:
+    return poison_(torch.empty_like(t))
 
 
 def cf(dtype: str) -> int:

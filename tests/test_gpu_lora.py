@@ -27,7 +27,7 @@ def assert_gemm_close(got_stored: np.ndarray, exact: np.ndarray, dtype: str, wha
     rel, floor = (1e-4, 1e-4) if dtype == "f32" else (1e-2, 1e-3)
     scale = np.max(np.abs(exact)) if exact.size else 0.0
     err = np.abs(got - exact)
-    bad = np.flatnonzero((err > rel * np.abs(exact) + floor * scale).reshape(-1))
+    bad = np.flatnonzero(~(err <= rel * np.abs(exact) + floor * scale).reshape(-1))  # NaN fails
     assert bad.size == 0, f"{what}: {bad.size} out of tolerance, max err {err.max():.3e} (scale {scale:.3e})"
 
 
@@ -223,7 +223,7 @@ def test_fused_bf16_non_power_of_two_scale(shape, scale):
     exact = scale * (xa_bf16 @ bv.astype(np.float64))
     arithmetic = abs(scale) * (np.abs(xa_bf16) @ np.abs(bv.astype(np.float64)))
     err = np.abs(g.host_values(y0, "bf16").astype(np.float64) - exact)
-    bad = err > 2.0**-8 * np.abs(exact) + 2.0**-14 * arithmetic
+    bad = ~(err <= 2.0**-8 * np.abs(exact) + 2.0**-14 * arithmetic)  # NaN fails
     assert not bad.any(), f"{bad.sum()} outputs off by more than one bf16 rounding, max err {err.max():.3e}"
 
 

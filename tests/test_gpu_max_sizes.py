@@ -37,11 +37,11 @@ def bf16_bits(t: torch.Tensor) -> np.ndarray:
 def test_quantize_round_trip_past_2_31_elements():
     g.announce(f"quantize/dequantize bf16, {N_BIG} elements")
     x = torch.randn(N_BIG, device="cuda", dtype=torch.bfloat16)
-    q = torch.empty(N_BIG, device="cuda", dtype=torch.int8)
+    q = g.empty(N_BIG, torch.int8)
     nscales = (N_BIG + 63) // 64
-    s = torch.empty(nscales, device="cuda")
+    s = g.empty(nscales, torch.float32)
     g.call("cf_quantize_int8", x.data_ptr(), g.cf("bf16"), q.data_ptr(), s.data_ptr(), N_BIG, g.stream())
-    y = torch.empty_like(x)
+    y = g.poison_like(x)
     g.call("cf_dequantize_int8", q.data_ptr(), s.data_ptr(), y.data_ptr(), g.cf("bf16"), N_BIG, g.stream())
     torch.cuda.synchronize()
     assert int((q == -128).sum()) == 0
@@ -68,7 +68,7 @@ def test_row_ops_past_2_31_elements(op):
     rows = (1 << 31) // cols + 3
     g.announce(f"{op} bf16 [{rows}, {cols}] = {rows * cols} elements")
     x = torch.randn(rows, cols, device="cuda", dtype=torch.bfloat16)
-    y = torch.empty_like(x)
+    y = g.poison_like(x)
     if op == "rmsnorm":
         w = torch.ones(cols, device="cuda", dtype=torch.bfloat16)
         g.call("cf_rmsnorm", x.data_ptr(), w.data_ptr(), y.data_ptr(), g.cf("bf16"), rows, cols, 1e-6, g.stream())
@@ -95,10 +95,10 @@ def test_sum_past_2_31_elements():
     n = (1 << 31) + 77
     g.announce(f"sum fp32 of {n} ones")
     x = torch.ones(n, device="cuda")
-    out = torch.empty(1, device="cuda")
+    out = g.empty(1, torch.float32)
     lib = g.lib()
     nbytes = lib.cf_reduce_sum_workspace_bytes(n)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    ws = g.empty(nbytes, torch.uint8)
     g.call("cf_reduce_sum", x.data_ptr(), g.cf("f32"), out.data_ptr(), n, ws.data_ptr(), nbytes, 0, g.stream())
     torch.cuda.synchronize()
     # fp32 partial sums of ones are exact below 2^24 per partial; the final

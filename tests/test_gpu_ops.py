@@ -29,8 +29,8 @@ def test_the_backend_report_names_the_hip_kernels():
 def test_dispatcher_quantise_equals_the_c_abi():
     x = torch.randn(4096, 333, device=g.DEVICE)
     q, s = torch.ops.cudaforge.quantize_int8(x)
-    q2 = torch.empty(x.numel(), dtype=torch.int8, device=g.DEVICE)
-    s2 = torch.empty_like(s)
+    q2 = g.empty(x.numel(), torch.int8)
+    s2 = g.poison_like(s)
     g.call("cf_quantize_int8", x.data_ptr(), g.cf("f32"), q2.data_ptr(), s2.data_ptr(), x.numel(), g.stream())
     torch.cuda.synchronize()
     assert q.shape == x.shape and s.shape == ((x.numel() + 63) // 64,)

@@ -19,6 +19,7 @@ import torch
 import oracle
 from cuda_force_amd import _lib
 
+from . import gpu_util as g
 from .gpu_util import announce
 from .paged_util import REFERENCE_CASES, make_case
 
@@ -39,7 +40,7 @@ def run_gpu(case, dtype="f32", workspace=True):
     out = torch.full_like(q, float("nan"))
     lib = _lib.load()
     nbytes = lib.cf_paged_attention_workspace_bytes(s, h, kvh, d, bs, mb) if workspace else 0
-    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    ws = g.empty(max(nbytes, 1), torch.uint8)
     code = _lib.CF_F32 if dtype == "f32" else _lib.CF_BF16
     _lib.check(lib.cf_paged_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), tables.data_ptr(),
                                       ctx.data_ptr(), out.data_ptr(), code, s, h, kvh, d, bs, mb,

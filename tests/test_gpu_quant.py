@@ -181,7 +181,7 @@ def test_fake_quantisation_is_bit_exact(dtype):
     n = 70_001
     x = g.storage_bits((rng(17).standard_normal(n) * 3).astype(np.float32), dtype)
     xg = g.to_gpu(x, dtype)
-    y = torch.empty_like(xg)
+    y = g.poison_like(xg)
     g.call("cf_quantize_dequantize", xg.data_ptr(), y.data_ptr(), g.cf(dtype), n, g.stream())
     torch.cuda.synchronize()
     assert_bits_equal(g.to_host(y), oracle.quantize_dequantize(x, dtype))

@@ -42,14 +42,18 @@ def member_inputs(seed: int, dtype: str):
     return members
 
 
-def carve(members, elem_bytes: int, torch_dtype):
+def carve(members, elem_bytes: int, torch_dtype, poison: bool = False):
     """One device buffer holding every member at 256-byte aligned slots (plus
-    one element for misaligned members); returns the buffer and offsets."""
+    one element for misaligned members); returns the buffer and offsets.
+    Input buffers start zeroed; output buffers (poison=True) start poisoned,
+    so an element no kernel writes fails the comparison."""
     offsets, cursor = [], 0
     for n, _, misaligned in members:
         start = cursor + (elem_bytes if misaligned else 0)
         offsets.append(start)
         cursor = (start + max(n, 1) * elem_bytes + 255) // 256 * 256
+    if poison:
+        return g.empty(cursor // elem_bytes + 64, torch_dtype), offsets
     buf = torch.zeros(cursor // elem_bytes + 64, dtype=torch_dtype, device="cuda")
     return buf, offsets
 
@@ -65,8 +69,8 @@ def test_group_members_match_the_oracle_bit_for_bit(dtype):
         if n:
             host = torch.from_numpy(np.ascontiguousarray(x).view(np.uint8).copy())
             xbytes[off:off + host.numel()].copy_(host.to("cuda"))
-    qbuf, qoff = carve(members, 1, torch.int8)
-    sbuf = torch.zeros(sum((n + 63) // 64 + 64 for n, _, _ in members), dtype=torch.float32, device="cuda")
+    qbuf, qoff = carve(members, 1, torch.int8, poison=True)
+    sbuf = g.empty(sum((n + 63) // 64 + 64 for n, _, _ in members), torch.float32)
     soff, cursor = [], 0
     for n, _, _ in members:
         soff.append(cursor)
@@ -81,7 +85,7 @@ def test_group_members_match_the_oracle_bit_for_bit(dtype):
     outs = {}
     for out_dtype in ("f32", "bf16", "f16"):
         oelem = 4 if out_dtype == "f32" else 2
-        ybuf, yoff = carve(members, oelem, g.torch_dtype(out_dtype))
+        ybuf, yoff = carve(members, oelem, g.torch_dtype(out_dtype), poison=True)
         y_ptrs = [ybuf.data_ptr() + off for off in yoff]
         g.call("cf_dequantize_int8_group", _lib.pointer_array(q_ptrs), _lib.pointer_array(s_ptrs),
                _lib.pointer_array(y_ptrs), g.cf(out_dtype), _lib.int64_array(counts), len(members), g.stream())
@@ -102,11 +106,49 @@ def test_group_members_match_the_oracle_bit_for_bit(dtype):
             assert bad.size == 0, (f"member {i} (n={n}) dequantised to {out_dtype}: {bad.size} differ, "
                                    f"first {bad[:4]}: got {[hex(v) for v in got.view(view)[bad[:4]]]} "
                                    f"want {[hex(v) for v in want.view(view)[bad[:4]]]}")
-    # The slots between members were never written.
+    # The slots between members were never written: they still hold the poison (-128).
     for i, (n, _, _) in enumerate(members):
         end = qoff[i] + n
         gap_end = qoff[i + 1] if i + 1 < len(members) else qhost.size
-        assert not qhost[end:min(gap_end, end + 64)].any(), f"write past member {i}"
+        assert (qhost[end:min(gap_end, end + 64)] == -128).all(), f"write past member {i}"
+
+
+SHAPES_7B = [(4096, 4096), (11008, 4096), (4096, 11008)]
+
+
+def test_group_at_the_7b_shapes_matches_the_oracle():
+    """One member of each 7B layer shape (config 5: bf16 ~N(0, 0.02) with 0.1%
+    outliers x50) through the grouped quantiser, then the grouped dequantiser
+    to bf16 - the bench's aggregate kernels - every code, scale and output
+    bit against the oracle."""
+    print("case: grouped bf16 quantise/dequantise at the 7B shapes vs the oracle", flush=True)
+    gen = rng(7007)
+    hosts = []
+    for rows, cols in SHAPES_7B:
+        n = rows * cols
+        x = (0.02 * gen.standard_normal(n, dtype=np.float32))
+        x[gen.choice(n, n // 1000, replace=False)] *= 50.0
+        hosts.append(oracle.f32_to_bf16_bits(x))
+    xs = [g.to_gpu(h, "bf16") for h in hosts]
+    qs = [g.empty(x.numel(), torch.int8) for x in xs]
+    ss = [g.empty(x.numel() // 64, torch.float32) for x in xs]
+    ys = [g.poison_like(x) for x in xs]
+    g.call("cf_quantize_int8_group", _lib.pointer_array([x.data_ptr() for x in xs]), _lib.CF_BF16,
+           _lib.pointer_array([q.data_ptr() for q in qs]), _lib.pointer_array([s.data_ptr() for s in ss]),
+           _lib.int64_array([x.numel() for x in xs]), len(xs), g.stream())
+    g.call("cf_dequantize_int8_group", _lib.pointer_array([q.data_ptr() for q in qs]),
+           _lib.pointer_array([s.data_ptr() for s in ss]), _lib.pointer_array([y.data_ptr() for y in ys]),
+           _lib.CF_BF16, _lib.int64_array([x.numel() for x in xs]), len(xs), g.stream())
+    torch.cuda.synchronize()
+    for shape, h, q, s, y in zip(SHAPES_7B, hosts, qs, ss, ys):
+        q_ref, s_ref = oracle.quantize_int8(h, "bf16")
+        bad = np.flatnonzero(g.to_host(q).view(np.int8) != q_ref.reshape(-1))
+        assert bad.size == 0, f"{shape}: {bad.size} codes differ, first at {bad[:4]}"
+        assert np.array_equal(g.to_host(s).view(np.uint32), s_ref.view(np.uint32)), f"{shape}: scales differ"
+        want = oracle.dequantize_int8(q_ref, s_ref, "bf16").reshape(-1)
+        bad = np.flatnonzero(g.to_host(y) != want.view(np.uint16))
+        assert bad.size == 0, f"{shape}: {bad.size} dequantised values differ, first at {bad[:4]}"
+        del q_ref, s_ref, want
 
 
 def test_group_equals_single_calls_at_the_7b_shapes():
@@ -114,14 +156,14 @@ def test_group_equals_single_calls_at_the_7b_shapes():
     gen = torch.Generator(device="cuda").manual_seed(5)
     shapes = [(4096, 4096)] * 4 + [(11008, 4096)] * 2 + [(4096, 11008)]
     xs = [(0.02 * torch.randn(*s, generator=gen, device="cuda")).to(torch.bfloat16) for s in shapes * 8]
-    qs = [torch.empty(x.numel(), dtype=torch.int8, device="cuda") for x in xs]
-    ss = [torch.empty(x.numel() // 64, device="cuda") for x in xs]
+    qs = [g.empty(x.numel(), torch.int8) for x in xs]
+    ss = [g.empty(x.numel() // 64, torch.float32) for x in xs]
     g.call("cf_quantize_int8_group", _lib.pointer_array([x.data_ptr() for x in xs]), _lib.CF_BF16,
            _lib.pointer_array([q.data_ptr() for q in qs]), _lib.pointer_array([s.data_ptr() for s in ss]),
            _lib.int64_array([x.numel() for x in xs]), len(xs), g.stream())
     for x, q, s in zip(xs, qs, ss):
-        q1 = torch.empty_like(q)
-        s1 = torch.empty_like(s)
+        q1 = g.poison_like(q)
+        s1 = g.poison_like(s)
         g.call("cf_quantize_int8", x.data_ptr(), _lib.CF_BF16, q1.data_ptr(), s1.data_ptr(), x.numel(), g.stream())
         assert torch.equal(q, q1) and torch.equal(s.view(torch.int32), s1.view(torch.int32))
     assert len(xs) > GROUP_MAX

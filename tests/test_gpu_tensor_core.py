@@ -19,6 +19,7 @@ import torch
 
 from cuda_force_amd import _lib
 
+from . import gpu_util as g
 from .gpu_util import announce
 
 pytestmark = pytest.mark.gpu
@@ -30,7 +31,7 @@ def tensor_core(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     n = b.shape[1]
     c = torch.full((m, n), float("nan"), device=a.device)
     nbytes = lib.cf_matmul_tensor_core_workspace_bytes(m, n, k)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device)
+    ws = g.empty(nbytes, torch.uint8)
     _lib.check(lib.cf_matmul_tensor_core(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, ws.data_ptr(),
                                          nbytes, torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()

@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from cuda_force_amd import _lib
+from tests import gpu_util as g
 from tests.gpu_util import call, stream
 
 pytestmark = pytest.mark.gpu
@@ -25,8 +26,8 @@ def test_timed_launch_matches_untimed_and_is_the_kernel_time():
     gen = torch.Generator(device="cuda").manual_seed(11)
     x = torch.randn(4096, 4096, generator=gen, device="cuda").to(torch.bfloat16)
     w = (1 + 0.02 * torch.randn(4096, generator=gen, device="cuda")).to(torch.bfloat16)
-    plain = torch.empty_like(x)
-    timed = torch.empty_like(x)
+    plain = g.poison_like(x)
+    timed = g.poison_like(x)
     for _ in range(3):
         _rmsnorm(x, w, plain)
     torch.cuda.synchronize()
@@ -82,7 +83,7 @@ def test_only_the_next_launch_is_timed():
     print("case: dispatch timer armed once, two launches", flush=True)
     x = torch.ones(256, 1024, device="cuda", dtype=torch.bfloat16)
     w = torch.ones(1024, device="cuda", dtype=torch.bfloat16)
-    y = torch.empty_like(x)
+    y = g.poison_like(x)
     timer = _lib.DispatchTimer()
     timer.arm()
     _rmsnorm(x, w, y)
