@@ -22,6 +22,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <tuple>
+#include <type_traits>
 #include <utility>
 
 #include "../../include/cudaforge_hip.h"
@@ -151,6 +152,24 @@ __device__ __forceinline__ float block_reduce_f32(float v, float* slot) {
     }
 }
 
+/// Workgroup-wide OR of a per-thread predicate, the same result on every
+/// thread, through kWaves int slots of LDS that no other code reads or
+/// writes between the call's two barriers (__syncthreads_or would add LDS of
+/// its own, which costs kernels sized to the CU's 160 KiB a workgroup).
+/// Every thread of the workgroup must call it.
+template <int kWaves>
+__device__ __forceinline__ bool workgroup_any(bool pred, int* slots) {
+    const int wave = static_cast<int>(threadIdx.x) / kWaveSize;
+    const bool any = __builtin_amdgcn_ballot_w64(pred) != 0;
+    if ((threadIdx.x & (kWaveSize - 1)) == 0) slots[wave] = any ? 1 : 0;
+    __syncthreads();
+    int total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) total |= slots[w];
+    __syncthreads();  // every wave has read the slots before they are reused
+    return total != 0;
+}
+
 /// Workgroup barrier after LDS writes that does not wait for global loads:
 /// s_waitcnt lgkmcnt(0) (this wave's LDS writes are done), then s_barrier.
 /// __syncthreads() would also wait for every outstanding global load
@@ -217,9 +236,64 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2_canon(float lo, float hi) {
 /// nothing downstream (a NaN element gives NaN products either way). One
 /// conversion per two values instead of the software rounding's several
 /// instructions per value: these kernels spend their VALU time on the split.
-__device__ __forceinline__ void split_pk(float v0, float v1, uint32_t& hi, uint32_t& lo) {
-    hi = f32x2_to_bf16x2_bits(v0, v1);
+///
+/// Values outside bf16's finite range (|v| above 0x7F7F, +-inf) take another
+/// split, so that the three products follow fp32 arithmetic (inf * w = +-inf
+/// for w != 0, inf * 0 = NaN, a finite huge v times w finite):
+///   * finite |v| > 0x7F7F: hi = +-0x7F7F, lo = bf16(v - hi), the finite
+///     remainder (plain rounding would give hi = inf, lo = -inf);
+///   * v = +-inf: hi = +-1, lo = +-inf (with hi = +-0x7F7F the other
+///     operand's lo times it could overflow to an infinity of the wrong sign).
+/// A NaN keeps the plain split (lo = NaN).
+///
+/// split_pk_as<false> is the plain split, exact for |v| within bf16's range;
+/// split_pk_as<true> handles every value. Kernels pick one per wave: the
+/// staging loops fold |v| of a whole K-step into abs_max3 and branch once on
+/// wave_outside_bf16 (ordinary inputs pay half an instruction per value);
+/// split_pk and split_pk4 make the same choice per call.
+__device__ __forceinline__ float split_hi_special(float v) {
+    const float big = __uint_as_float(0x7F7F0000u);
+    return __builtin_isinf(v) ? __builtin_copysignf(1.0f, v) : __builtin_fminf(__builtin_fmaxf(v, -big), big);
+}
+
+/// max(m, |a|, |b|), one v_max3_f32; a NaN is ignored.
+__device__ __forceinline__ float abs_max3(float m, float a, float b) {
+    return __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fabsf(a), __builtin_fabsf(b)));
+}
+
+/// True on every lane when some lane's m lies above bf16's finite range
+/// (|v| > 0x7F7F or an infinity folded into m).
+__device__ __forceinline__ bool wave_outside_bf16(float m) {
+    return __builtin_amdgcn_ballot_w64(m > __uint_as_float(0x7F7F0000u)) != 0;
+}
+
+template <bool kWide>
+__device__ __forceinline__ void split_pk_as(float v0, float v1, uint32_t& hi, uint32_t& lo) {
+    if constexpr (kWide) {
+        hi = f32x2_to_bf16x2_bits(split_hi_special(v0), split_hi_special(v1));
+    } else {
+        hi = f32x2_to_bf16x2_bits(v0, v1);
+    }
     lo = f32x2_to_bf16x2_bits(v0 - __uint_as_float(hi << 16), v1 - __uint_as_float(hi & 0xFFFF0000u));
+}
+
+__device__ __forceinline__ void split_pk(float v0, float v1, uint32_t& hi, uint32_t& lo) {
+    if (wave_outside_bf16(abs_max3(0.0f, v0, v1))) {
+        split_pk_as<true>(v0, v1, hi, lo);
+    } else {
+        split_pk_as<false>(v0, v1, hi, lo);
+    }
+}
+
+/// Four values (x, y into hi.x / lo.x; z, w into hi.y / lo.y), one choice.
+__device__ __forceinline__ void split_pk4(float v0, float v1, float v2, float v3, uint2& hi, uint2& lo) {
+    if (wave_outside_bf16(abs_max3(abs_max3(0.0f, v0, v1), v2, v3))) {
+        split_pk_as<true>(v0, v1, hi.x, lo.x);
+        split_pk_as<true>(v2, v3, hi.y, lo.y);
+    } else {
+        split_pk_as<false>(v0, v1, hi.x, lo.x);
+        split_pk_as<false>(v2, v3, hi.y, lo.y);
+    }
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {

@@ -187,8 +187,8 @@ __global__ __launch_bounds__(kThreads) void lora_f32_kernel(F32Args args) {
             const int k = 4 * (idx & 7);
             uint2 hi;
             uint2 lo;
-            split_pk(st.x[i].x, st.x[i].y, hi.x, lo.x);
-            split_pk(st.x[i].z, st.x[i].w, hi.y, lo.y);
+            split_pk_as<false>(st.x[i].x, st.x[i].y, hi.x, lo.x);
+            split_pk_as<false>(st.x[i].z, st.x[i].w, hi.y, lo.y);
             const int off = x_offset(row, k);
             *reinterpret_cast<uint2*>(base + kOffXHi + off) = hi;
             *reinterpret_cast<uint2*>(base + kOffXLo + off) = lo;
@@ -200,15 +200,15 @@ __global__ __launch_bounds__(kThreads) void lora_f32_kernel(F32Args args) {
             const int col = 4 * (idx & 15);
             uint2 hi;
             uint2 lo;
-            split_pk(st.w[i].x, st.w[i].y, hi.x, lo.x);
-            split_pk(st.w[i].z, st.w[i].w, hi.y, lo.y);
+            split_pk_as<false>(st.w[i].x, st.w[i].y, hi.x, lo.x);
+            split_pk_as<false>(st.w[i].z, st.w[i].w, hi.y, lo.y);
             const int off = krow * (kTN * 2) + col * 2;
             *reinterpret_cast<uint2*>(base + kOffWHi + off) = hi;
             *reinterpret_cast<uint2*>(base + kOffWLo + off) = lo;
         }
         uint32_t ahi;
         uint32_t alo;
-        split_pk(st.a[0], st.a[1], ahi, alo);
+        split_pk_as<false>(st.a[0], st.a[1], ahi, alo);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 256 * i;
@@ -217,6 +217,7 @@ __global__ __launch_bounds__(kThreads) void lora_f32_kernel(F32Args args) {
             *reinterpret_cast<uint16_t*>(base + kOffALo + off) = static_cast<uint16_t>(alo >> (16 * i));
         }
     };
+
 
     // Fragment roles (16x16x32 MFMA, C^T = w^T x^T):
     //   B (x^T): lane holds x[16 wave + jl][k 8 g .. +7], one ds_read_b128;
@@ -261,6 +262,8 @@ __global__ __launch_bounds__(kThreads) void lora_f32_kernel(F32Args args) {
 
     // Stage j % 2 is written at the top of step j: every wave finished
     // reading it in step j - 2, before the barrier of step j - 1.
+    // Stage j % 2 is written at the top of step j: every wave finished
+    // reading it in step j - 2, before the barrier of step j - 1.
     Staged st;
     load(st, k_begin);
     for (int j = 0; j < args.steps; ++j) {
@@ -268,6 +271,45 @@ __global__ __launch_bounds__(kThreads) void lora_f32_kernel(F32Args args) {
         __syncthreads();
         if (j + 1 < args.steps) load(st, k_begin + static_cast<int64_t>(j + 1) * kTK);
         compute(j & 1);
+    }
+
+    // The split above is exact for values within bf16's range. A value
+    // outside it (inf, NaN, |v| > 0x7F7F) in this tile's x, w or a always
+    // leaves some accumulator of the tile (or of x @ a) non-finite under that
+    // split, and so does an fp32 overflow. Such a tile (a rare one; the vote
+    // costs two barriers and uses the b planes, idle until the epilogue) is
+    // summed again in plain fp32 arithmetic, the reference's own, from global
+    // memory: slow, and exact in its inf / NaN / overflow behaviour.
+    {
+        float probe = (xacc[0] + xacc[1]) + (xacc[2] + xacc[3]);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) probe += (acc[jb][0] + acc[jb][1]) + (acc[jb][2] + acc[jb][3]);
+        if (workgroup_any<kThreads / 64>(!__builtin_isfinite(probe), reinterpret_cast<int*>(lds + kOffBHi))) {
+            const int64_t row = m0 + 16 * wave + jl;
+            const int64_t k_end = k_begin + static_cast<int64_t>(args.steps) * kTK < K
+                                      ? k_begin + static_cast<int64_t>(args.steps) * kTK
+                                      : K;
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) acc[jb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            xacc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            if (row < M) {
+                for (int64_t k = k_begin; k < k_end; ++k) {
+                    const float xv = args.x[row * K + k];
+#pragma unroll
+                    for (int jb = 0; jb < 4; ++jb) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int64_t col = n0 + 16 * jb + 4 * g + e;
+                            if (col < N) acc[jb][e] = __builtin_fmaf(xv, args.w[k * N + col], acc[jb][e]);
+                        }
+                    }
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        if (4 * g + t < rank) xacc[t] = __builtin_fmaf(xv, args.a[k * rank + 4 * g + t], xacc[t]);
+                    }
+                }
+            }
+        }
     }
 
     // Epilogue: b's tile split into planes, then acc += u b with
@@ -282,17 +324,22 @@ __global__ __launch_bounds__(kThreads) void lora_f32_kernel(F32Args args) {
         const uint4 v = buffer_load16(bbuf, ok ? static_cast<uint32_t>((j * N + col) * 4) : 0x80000000u, 0);
         uint2 hi;
         uint2 lo;
-        split_pk(__uint_as_float(v.x), __uint_as_float(v.y), hi.x, lo.x);
-        split_pk(__uint_as_float(v.z), __uint_as_float(v.w), hi.y, lo.y);
+        split_pk4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w), hi, lo);
         const int off = j * (kTN * 2) + 8 * (tid & 15);
         *reinterpret_cast<uint2*>(lds + kOffBHi + off) = hi;
         *reinterpret_cast<uint2*>(lds + kOffBLo + off) = lo;
     }
     __syncthreads();
+    // Adapter columns past the rank are padding (a reads zero there): an
+    // infinite x makes them inf * 0 = NaN, which must not reach y through
+    // b's zero rows.
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        if (4 * g + t >= rank) xacc[t] = 0.0f;
+    }
     uint2 uhw;
     uint2 ulw;
-    split_pk(args.scale * xacc[0], args.scale * xacc[1], uhw.x, ulw.x);
-    split_pk(args.scale * xacc[2], args.scale * xacc[3], uhw.y, ulw.y);
+    split_pk4(args.scale * xacc[0], args.scale * xacc[1], args.scale * xacc[2], args.scale * xacc[3], uhw, ulw);
     const s16x4_t uh = __builtin_bit_cast(s16x4_t, uhw);
     const s16x4_t ul = __builtin_bit_cast(s16x4_t, ulw);
 #pragma unroll

@@ -169,9 +169,15 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int rb = wm * 4 + wn * 2 + t;
+            // Columns past the rank are padding (a reads zero there); an
+            // infinite x makes them inf * 0 = NaN, kept out of the product
+            // with b's zero rows.
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = 4 * g + e < rank ? xacc[t][e] : 0.0f;
             uint2 packed;
-            packed.x = f32x2_to_bf16x2_canon(xacc[t][0], xacc[t][1]);
-            packed.y = f32x2_to_bf16x2_canon(xacc[t][2], xacc[t][3]);
+            packed.x = f32x2_to_bf16x2_canon(v[0], v[1]);
+            packed.y = f32x2_to_bf16x2_canon(v[2], v[3]);
             xa_lds[rb * 64 + lane] = packed;
             const int64_t row = m0 + rb * 16 + jl;
             if (write_xa && row < M) {
@@ -204,6 +210,18 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
         // Two passes (high parts, then low parts) keep one b fragment live.
 #pragma unroll
         for (int part = 0; part < 2; ++part) {
+            if (part == 1) {
+                // An infinite x @ a meets only the high part of scale * b:
+                // inf * lo would add NaN (lo = 0) or an infinity of the
+                // other sign, where the fp32 product inf * b is +-inf.
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if ((xa_frag[i][e] & 0x7FFF) == 0x7F80) xa_frag[i][e] = 0;
+                    }
+                }
+            }
 #pragma unroll
             for (int jb = 0; jb < 8; ++jb) {
                 const int row = 4 * g + (jl >> 2);

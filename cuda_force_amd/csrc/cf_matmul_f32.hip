@@ -90,11 +90,12 @@ __device__ __forceinline__ bf16x8_t concat(s16x4_t lo, s16x4_t hi) {
 }
 
 /// The four values' bf16 high parts (returned) and low parts (lo_out),
-/// packed two per word.
+/// packed two per word: the plain split, exact for values within bf16's
+/// range (the kernel recomputes a tile that holds others).
 __device__ __forceinline__ uint2 pack_hi_lo(const float4& v, uint2& lo_out) {
     uint2 hi;
-    split_pk(v.x, v.y, hi.x, lo_out.x);
-    split_pk(v.z, v.w, hi.y, lo_out.y);
+    split_pk_as<false>(v.x, v.y, hi.x, lo_out.x);
+    split_pk_as<false>(v.z, v.w, hi.y, lo_out.y);
     return hi;
 }
 
@@ -171,6 +172,7 @@ __global__ __launch_bounds__(kThreads) void matmul_f32_kernel(Args args) {
         }
     };
 
+
     // Fragment roles (16x16x32 MFMA, C^T = b^T a^T):
     //   B (a^T) of row block rb: lane holds a[64 wm + 16 rb + jl][k 8 g .. +7]
     //     (one ds_read_b128);
@@ -225,6 +227,51 @@ __global__ __launch_bounds__(kThreads) void matmul_f32_kernel(Args args) {
         __syncthreads();
         if (j + 1 < args.steps) load(k_begin + static_cast<int64_t>(j + 1) * kTK);
         compute(j & 1);
+    }
+
+    // The split above is exact for values within bf16's range. A value
+    // outside it (inf, NaN, |v| > 0x7F7F) in this tile's operands always
+    // leaves some accumulator non-finite under that split, and so does an
+    // fp32 overflow. Such a tile (a rare one; the vote costs two barriers and
+    // uses stage steps % 2, which no wave reads after the barrier of the last
+    // step) is summed again in plain fp32 arithmetic from global memory:
+    // slow, and exact in its inf / NaN / overflow behaviour.
+    {
+        float probe = 0.0f;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                probe += (acc[rb][cb][0] + acc[rb][cb][1]) + (acc[rb][cb][2] + acc[rb][cb][3]);
+            }
+        }
+        int* slots = reinterpret_cast<int*>(lds + (args.steps & 1) * kStageBytes);
+        if (workgroup_any<kThreads / 64>(!__builtin_isfinite(probe), slots)) {
+            const int64_t k_end = k_begin + static_cast<int64_t>(args.steps) * kTK < K
+                                      ? k_begin + static_cast<int64_t>(args.steps) * kTK
+                                      : K;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            for (int64_t k = k_begin; k < k_end; ++k) {
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    const int64_t row = m0 + 64 * wm + 16 * rb + jl;
+                    if (row >= M) continue;
+                    const float av = args.a[row * K + k];
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int64_t col = n0 + 64 * wn + 16 * cb + 4 * g + e;
+                            if (col < N) acc[rb][cb][e] = __builtin_fmaf(av, args.b[k * N + col], acc[rb][cb][e]);
+                        }
+                    }
+                }
+            }
+        }
     }
 
     // acc[rb][cb] lane holds c[m0 + 64 wm + 16 rb + jl][n0 + 64 wn + 16 cb + 4 g .. +3];

@@ -102,8 +102,7 @@ __device__ __forceinline__ void split_row_quad(const float* __restrict__ a, uint
     for (int e = 0; e < 4; ++e) v[e] = j + e < k ? a[row * k + j + e] : 0.0f;
     uint2 hi;
     uint2 lo;
-    split_pk(v[0], v[1], hi.x, lo.x);
-    split_pk(v[2], v[3], hi.y, lo.y);
+    split_pk4(v[0], v[1], v[2], v[3], hi, lo);
     *reinterpret_cast<uint2*>(out + row * 3 * kp + col) = part == 2 ? lo : hi;
 }
 
@@ -119,8 +118,7 @@ __device__ __forceinline__ void split_col_quad(const float* __restrict__ b, uint
     if (j < k) v = *reinterpret_cast<const float4*>(b + j * n + col);
     uint2 hi;
     uint2 lo;
-    split_pk(v.x, v.y, hi.x, lo.x);
-    split_pk(v.z, v.w, hi.y, lo.y);
+    split_pk4(v.x, v.y, v.z, v.w, hi, lo);
     *reinterpret_cast<uint2*>(out + row * n + col) = part == 1 ? lo : hi;
 }
 

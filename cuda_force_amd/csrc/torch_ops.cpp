@@ -143,6 +143,8 @@ void check_attention(const torch::Tensor& rows, int64_t heads, const char* name)
 torch::Tensor attention_scores_causal_hip(const torch::Tensor& q, const torch::Tensor& k, int64_t heads) {
     check_attention(q, heads, "q");
     TORCH_CHECK(k.sizes() == q.sizes(), "q and k differ in shape");
+    TORCH_CHECK(k.scalar_type() == q.scalar_type(), "q and k differ in dtype");
+    check_same_device(q, k, "k");
     check_contiguous(q, "q");
     check_contiguous(k, "k");
     const at::DeviceGuard guard(q.device());
@@ -160,6 +162,7 @@ torch::Tensor attention_pv_causal_hip(const torch::Tensor& probs, const torch::T
                     probs.size(3) == seq,
                 "probs must be [batch, heads, seq, seq] = [", batch, ", ", heads, ", ", seq, ", ", seq, "]");
     TORCH_CHECK(probs.scalar_type() == v.scalar_type(), "probs and v differ in dtype");
+    check_same_device(v, probs, "probs");
     check_contiguous(probs, "probs");
     check_contiguous(v, "v");
     const at::DeviceGuard guard(v.device());

@@ -336,7 +336,11 @@ def attention_scores_causal(q: torch.Tensor, k: torch.Tensor, heads: int) -> tor
     if k.shape != q.shape:
         raise ValueError(f"q and k differ in shape: {tuple(q.shape)} and {tuple(k.shape)}")
     q, k = q.contiguous(), k.contiguous()
-    if _dispatch_available("attention_scores_causal", q, k) and (not q.is_cuda or _attention_kernel_shape(q, heads, k)):
+    if (
+        _dispatch_available("attention_scores_causal", q, k)
+        and _same_dtype(q, k)
+        and (not q.is_cuda or _attention_kernel_shape(q, heads, k))
+    ):
         return torch.ops.cudaforge.attention_scores_causal(q, k, int(heads))
     _refuse_gpu_fallback("attention_scores_causal", q, k)
     batch, seq, hidden = q.shape

@@ -142,3 +142,20 @@ def test_strict_mode_refuses_a_gpu_fallback():
     x = torch.randn(8, 8, device=g.DEVICE, dtype=torch.float64)
     with pytest.raises(NotImplementedError, match="no HIP kernel"):
         ops.softmax(x)
+
+
+def test_attention_products_reject_mixed_devices_and_dtypes():
+    """The dispatcher ops check devices and dtypes before any launch: a CPU k or
+    v beside a GPU q or probs, and a k whose dtype differs from q's, raise
+    RuntimeError (nothing is launched)."""
+    q = torch.zeros(1, 8, 64, dtype=torch.bfloat16, device=g.DEVICE)
+    probs = torch.zeros(1, 2, 8, 8, dtype=torch.bfloat16, device=g.DEVICE)
+    with pytest.raises(RuntimeError, match="is on"):
+        torch.ops.cudaforge.attention_scores_causal(q, q.cpu(), 2)
+    with pytest.raises(RuntimeError, match="dtype"):
+        torch.ops.cudaforge.attention_scores_causal(q, q.half(), 2)
+    with pytest.raises(RuntimeError, match="is on"):
+        torch.ops.cudaforge.attention_pv_causal(probs, q.cpu(), 2)
+    with pytest.raises(RuntimeError, match="dtype"):
+        torch.ops.cudaforge.attention_pv_causal(probs, q.half(), 2)
+    torch.cuda.synchronize()
