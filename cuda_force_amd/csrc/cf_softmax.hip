@@ -476,6 +476,10 @@ cf_status cf_softmax_scaled(const void* x, cf_dtype x_dtype, void* y, cf_dtype y
                "cf_softmax_scaled: input and output may alias only when their dtypes match");
     CF_REQUIRE(causal_period >= 0, "cf_softmax_scaled: negative causal period %lld",
                static_cast<long long>(causal_period));
+    // A period of rows or more gives row % period == row for every row, as
+    // rows does: clamping keeps the mask and lets the wave kernel take the
+    // period as a 32-bit value (it runs only for rows below 2^31).
+    if (causal_period > rows) causal_period = rows;
     return cf::dispatch_in<true>(x, x_dtype, y, y_dtype, rows, cols,
                                  cf::Masking{scale, causal_period}, static_cast<hipStream_t>(stream));
 }

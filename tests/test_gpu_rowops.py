@@ -378,6 +378,20 @@ def test_softmax_scaled_causal_matches_the_oracle(dtype, shape, period):
     assert_close(run_softmax_scaled(x, dtype, dtype, scale, period, in_place=True), exact, dtype, "in place")
 
 
+@pytest.mark.parametrize("period", [(1 << 32) + 1, 1 << 32, (1 << 31) + 5, 1 << 40], ids=str)
+def test_softmax_scaled_periods_past_32_bits(period):
+    """A period of rows or more masks column c of row r when c > r, whatever
+    its size: 2^32 + 1 must not act as 1 (a 32-bit truncation). Checked
+    against the oracle and bit for bit against period = rows."""
+    rows, cols = 512, 512  # the one-wave-per-row kernel
+    g.announce(f"softmax_scaled bf16 period {period}")
+    x = g.storage_bits((rng(period % 997).standard_normal((rows, cols)) * 4).astype(np.float32), "bf16")
+    y = run_softmax_scaled(x, "bf16", "bf16", 0.5, period)
+    exact = oracle.softmax(masked_logits(g.host_values(x, "bf16"), 0.5, rows))
+    assert_close(y, exact, "bf16", f"period {period}")
+    np.testing.assert_array_equal(y, run_softmax_scaled(x, "bf16", "bf16", 0.5, rows))
+
+
 def test_softmax_scaled_misaligned_and_scale_only():
     x = (rng(21).standard_normal((37, 512)) * 3).astype(np.float32)
     exact = oracle.softmax(masked_logits(x, 0.25, 512))

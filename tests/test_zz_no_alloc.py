@@ -40,9 +40,14 @@ def sum_noalloc(xg: torch.Tensor, dtype: str, n: int, start: float, accumulate: 
 
 
 def test_noalloc_sum_matches_the_workspace_sum_on_consecutive_calls():
-    # Largest first: 40M elements use all 4096 partials; the next calls use
-    # 367, 13 and 1, so a stage 2 that read stale partials would be caught.
-    cases = [(40_000_003, "f32"), (3_000_001, "f32"), (100_003, "bf16"), (1000, "f16"), (40_000_003, "f32")]
+    # Largest first: 40M elements use all 4096 partials (ceil(n / 4096),
+    # at most 4096, for inputs above 256 KiB); the next tree-path calls use
+    # 18 (f32 70,000), 733 (f32 3,000,001) and 74 (bf16 300,001) and leave
+    # the 4096-partial call's values in the slots past theirs, so a stage 2
+    # that read stale partials would be caught. bf16 100,003 and f16 1000 fit
+    # 256 KiB and take the one-launch path (no scratch).
+    cases = [(40_000_003, "f32"), (70_000, "f32"), (3_000_001, "f32"), (300_001, "bf16"), (100_003, "bf16"),
+             (1000, "f16"), (40_000_003, "f32")]
     for n, dtype in cases:
         g.announce(f"noalloc sum {dtype} n={n}")
         values = rng(n).standard_normal(n).astype(np.float32)
