@@ -70,6 +70,42 @@ __device__ __forceinline__ BlockScale block_scale(uint32_t absmax_bits) {
     return b;
 }
 
+/// The scales of kU blocks whose absmax bit patterns every lane holds in
+/// mx[0 .. kU) (kU a multiple of 4). Each block's two IEEE divides (absmax /
+/// 127 and 1 / s) are the bulk of the quantiser's arithmetic, and the lanes
+/// of a block compute them alike; here lane l of each quad divides for block
+/// c + l % 4 and quad-permute DPP moves hand the four results to every lane
+/// of the quad: one divide sequence per four blocks instead of one per
+/// block, the same values (block_scale on the same bits). All 64 lanes must
+/// be active.
+template <int kU>
+__device__ __forceinline__ void block_scales(const uint32_t (&mx)[kU], BlockScale (&bs)[kU]) {
+    static_assert(kU % 4 == 0, "blocks are taken four at a time");
+    // Lane bits 0 and 1 as all-ones masks. The pick is written as masked xors:
+    // a chain of selects is turned into an indexed load from a stack copy.
+    const uint32_t b0 = 0u - (threadIdx.x & 1u);
+    const uint32_t b1 = 0u - ((threadIdx.x >> 1) & 1u);
+#pragma unroll
+    for (int c = 0; c < kU; c += 4) {
+        const uint32_t a01 = mx[c] ^ ((mx[c] ^ mx[c + 1]) & b0);
+        const uint32_t a23 = mx[c + 2] ^ ((mx[c + 2] ^ mx[c + 3]) & b0);
+        const uint32_t mine = a01 ^ ((a01 ^ a23) & b1);
+        const BlockScale b = block_scale(mine);
+        auto take = [&](auto kk) {
+            constexpr int k = decltype(kk)::value;
+            constexpr int kCtrl = k | (k << 2) | (k << 4) | (k << 6);  // quad_perm [k, k, k, k]
+            BlockScale& out = bs[c + k];
+            out.s = dpp_f32<kCtrl>(b.s);
+            out.inv = dpp_f32<kCtrl>(b.inv);
+            out.exact = !(out.s >= kMinFastScale);
+        };
+        take(std::integral_constant<int, 0>{});
+        take(std::integral_constant<int, 1>{});
+        take(std::integral_constant<int, 2>{});
+        take(std::integral_constant<int, 3>{});
+    }
+}
+
 /// A rounded quotient clamped to [-127, 127]; NaN gives 0 (what ATen's
 /// float->int8 conversion of a NaN yields after torch.clamp propagates it).
 __device__ __forceinline__ int clamp_code(float r) {
@@ -124,14 +160,31 @@ __device__ __forceinline__ void load_lane(const T* __restrict__ x, int64_t e, in
     }
 }
 
-/// Shared body of quantise and fake-quantise. kMode 0 writes codes + scales,
-/// kMode 1 writes q * s in T. kFull: every element of this wave's blocks is
-/// inside `count` and the pointers are vector-aligned (all waves but the
-/// last), so loads and stores need no bounds tests.
-template <typename T, bool kVec, int kMode, bool kFull, int kU = kUnroll>
-__device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __restrict__ q,
-                                           float* __restrict__ scales, T* __restrict__ y,
-                                           int64_t count, int64_t wave) {
+/// The loads of one step of quant_body: this lane's kPer elements of each of
+/// the kU block groups of step `wave` (zeros past `count`).
+template <typename T, bool kVec, bool kFull, int kU>
+__device__ __forceinline__ void quant_load(const T* __restrict__ x, int64_t count, int64_t wave,
+                                           float (&v)[kU][Storage<T>::kPerVec]) {
+    constexpr int kPer = Storage<T>::kPerVec;
+    constexpr int kLanesPerBlock = kQuantBlockSize / kPer;
+    constexpr int kBlocksPerStep = kWaveSize / kLanesPerBlock;
+    const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
+    const int64_t base_block = wave * (kBlocksPerStep * kU);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        const int64_t block = base_block + u * kBlocksPerStep + lane / kLanesPerBlock;
+        load_lane<T, kVec, kFull>(x, block * kQuantBlockSize + (lane % kLanesPerBlock) * kPer, count, v[u]);
+    }
+}
+
+/// Quantise (kMode 0: codes + scales) or fake-quantise (kMode 1: q * s in T)
+/// the elements quant_load brought in for step `wave`. kFull: every element
+/// of the step is inside `count` and the pointers are vector-aligned, so
+/// stores need no bounds tests. Every lane of the wave must be active.
+template <typename T, bool kVec, int kMode, bool kFull, int kU>
+__device__ __forceinline__ void quant_process(float (&v)[kU][Storage<T>::kPerVec], int8_t* __restrict__ q,
+                                              float* __restrict__ scales, T* __restrict__ y, int64_t count,
+                                              int64_t wave) {
     constexpr int kPer = Storage<T>::kPerVec;                  // 4 (fp32) or 8 (16-bit)
     constexpr int kLanesPerBlock = kQuantBlockSize / kPer;     // 16 or 8
     constexpr int kBlocksPerStep = kWaveSize / kLanesPerBlock; // 4 or 8
@@ -141,16 +194,7 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
     const int sub = lane / kLanesPerBlock;
     const int part = lane % kLanesPerBlock;
 
-    float v[kU][kPer];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-        const int64_t block = base_block + u * kBlocksPerStep + sub;
-        load_lane<T, kVec, kFull>(x, block * kQuantBlockSize + part * kPer, count, v[u]);
-    }
-    // Keep every load of the step ahead of the first use: without this the
-    // scheduler starts on block 0 after two of the four loads.
-    __builtin_amdgcn_sched_barrier(0);
-
+    uint32_t mx[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
         uint32_t m = 0;
@@ -159,8 +203,15 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
             const uint32_t a = abs_bits(v[u][i]);
             m = a > m ? a : m;
         }
-        m = group_reduce_u32<kLanesPerBlock, MaxU32>(m);
-        const BlockScale b = block_scale(m);
+        mx[u] = group_reduce_u32<kLanesPerBlock, MaxU32>(m);
+    }
+    BlockScale bs[kU];
+    block_scales<kU>(mx, bs);
+
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        const uint32_t m = mx[u];
+        const BlockScale& b = bs[u];
 
         const int64_t block = base_block + u * kBlocksPerStep + sub;
         const int64_t e = block * kQuantBlockSize + part * kPer;
@@ -228,6 +279,21 @@ __device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __re
             }
         }
     }
+}
+
+/// One step of quantise / fake-quantise: the loads, then the arithmetic and
+/// stores. kFull: every element of step `wave` is inside `count` and the
+/// pointers are vector-aligned (all waves but the last).
+template <typename T, bool kVec, int kMode, bool kFull, int kU = kUnroll>
+__device__ __forceinline__ void quant_body(const T* __restrict__ x, int8_t* __restrict__ q,
+                                           float* __restrict__ scales, T* __restrict__ y,
+                                           int64_t count, int64_t wave) {
+    float v[kU][Storage<T>::kPerVec];
+    quant_load<T, kVec, kFull, kU>(x, count, wave, v);
+    // Keep every load of the step ahead of the first use: without this the
+    // scheduler starts on block 0 after two of the four loads.
+    __builtin_amdgcn_sched_barrier(0);
+    quant_process<T, kVec, kMode, kFull, kU>(v, q, scales, y, count, wave);
 }
 
 /// Index of the calling wave in the grid (wave-uniform).
