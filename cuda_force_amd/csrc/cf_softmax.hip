@@ -215,17 +215,21 @@ __global__ __launch_bounds__(kDefaultBlockSize) void softmax_wave_kernel(const T
     }
 }
 
-/// One workgroup of kRowThreads threads per row (grid-stride over rows), the
-/// row in registers: thread t holds vectors t, t + kRowThreads, ... of it.
+/// One workgroup of kThreads threads per row (grid-stride over rows), the
+/// row in registers: thread t holds vectors t, t + kThreads, ... of it.
 /// Every thread reads its vectors before the first reduction's barrier, so
-/// x and y may alias.
+/// x and y may alias. Rows wider than a wave's registers take 1024 threads;
+/// latency-bound shapes (no more rows than SIMDs, 257-1024 vectors a row)
+/// take 512 or 1024 threads of one vector each, so the row's serial
+/// arithmetic (unpack, exp, scale, pack) is spread over more lanes, for two
+/// cross-wave reductions through LDS.
 constexpr int kRowThreads = 1024;
 
-template <typename Tin, typename Tout, int kVecs, bool kFullCols, bool kMasked>
-__global__ __launch_bounds__(kRowThreads) void softmax_row_kernel(const Tin* x, Tout* y, int64_t rows,
-                                                                  int64_t cols, Masking mask) {
+template <typename Tin, typename Tout, int kVecs, bool kFullCols, bool kMasked, int kThreads = kRowThreads>
+__global__ __launch_bounds__(kThreads) void softmax_row_kernel(const Tin* x, Tout* y, int64_t rows,
+                                                               int64_t cols, Masking mask) {
     constexpr int kPer = Storage<Tin>::kPerVec;
-    __shared__ float slot[kRowThreads / kWaveSize];
+    __shared__ float slot[kThreads / kWaveSize];
     const int tid = static_cast<int>(threadIdx.x);
     const int64_t vec_cols = cols / kPer;
     const float neg_inf = -__builtin_inff();
@@ -237,7 +241,7 @@ __global__ __launch_bounds__(kRowThreads) void softmax_row_kernel(const Tin* x, 
         uint4 raw[kVecs];
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
-            const int64_t idx = static_cast<int64_t>(j) * kRowThreads + tid;
+            const int64_t idx = static_cast<int64_t>(j) * kThreads + tid;
             const int64_t ic = kFullCols || idx < vec_cols ? idx : vec_cols - 1;
             if constexpr (kMasked) {
                 const bool read = static_cast<int>(ic) * kPer <= visible;
@@ -250,7 +254,7 @@ __global__ __launch_bounds__(kRowThreads) void softmax_row_kernel(const Tin* x, 
         float v[kVecs][kPer];
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
-            const int64_t idx = static_cast<int64_t>(j) * kRowThreads + tid;
+            const int64_t idx = static_cast<int64_t>(j) * kThreads + tid;
             if (kFullCols || idx < vec_cols) {
                 unpack16<Tin>(raw[j], v[j]);
                 if constexpr (kMasked) {
@@ -269,7 +273,7 @@ __global__ __launch_bounds__(kRowThreads) void softmax_row_kernel(const Tin* x, 
 #pragma unroll
             for (int i = 0; i < kPer; ++i) local_max = fmaxf(local_max, v[j][i]);
         }
-        const float row_max = block_reduce_f32<kRowThreads / kWaveSize, MaxF32>(local_max, slot);
+        const float row_max = block_reduce_f32<kThreads / kWaveSize, MaxF32>(local_max, slot);
         float partial[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
@@ -280,11 +284,11 @@ __global__ __launch_bounds__(kRowThreads) void softmax_row_kernel(const Tin* x, 
             }
         }
         const float inv_sum =
-            1.0f / block_reduce_f32<kRowThreads / kWaveSize, AddF32>(partial[0] + partial[1], slot);
+            1.0f / block_reduce_f32<kThreads / kWaveSize, AddF32>(partial[0] + partial[1], slot);
         const bool row_nan = inv_sum != inv_sum;
 #pragma unroll
         for (int j = 0; j < kVecs; ++j) {
-            const int64_t idx = static_cast<int64_t>(j) * kRowThreads + tid;
+            const int64_t idx = static_cast<int64_t>(j) * kThreads + tid;
             if (kFullCols || idx < vec_cols) {
 #pragma unroll
                 for (int i = 0; i < kPer; ++i) v[j][i] = v[j][i] * inv_sum;
@@ -294,18 +298,18 @@ __global__ __launch_bounds__(kRowThreads) void softmax_row_kernel(const Tin* x, 
     }
 }
 
-template <typename Tin, typename Tout, int kVecs, bool kMasked>
+template <typename Tin, typename Tout, int kVecs, bool kMasked, int kThreads = kRowThreads>
 void launch_row(const void* x, void* y, int64_t rows, int64_t cols, const Masking& mask, hipStream_t stream) {
-    const bool full = cols / Storage<Tin>::kPerVec == static_cast<int64_t>(kVecs) * kRowThreads;
+    const bool full = cols / Storage<Tin>::kPerVec == static_cast<int64_t>(kVecs) * kThreads;
     const unsigned grid = static_cast<unsigned>(rows < (1 << 20) ? rows : (1 << 20));
     const auto* xin = static_cast<const Tin*>(x);
     auto* out = static_cast<Tout*>(y);
     if (full) {
-        launch(softmax_row_kernel<Tin, Tout, kVecs, true, kMasked>, dim3(grid), dim3(kRowThreads), 0, stream, xin,
-               out, rows, cols, mask);
+        launch(softmax_row_kernel<Tin, Tout, kVecs, true, kMasked, kThreads>, dim3(grid), dim3(kThreads), 0, stream,
+               xin, out, rows, cols, mask);
     } else {
-        launch(softmax_row_kernel<Tin, Tout, kVecs, false, kMasked>, dim3(grid), dim3(kRowThreads), 0, stream, xin,
-               out, rows, cols, mask);
+        launch(softmax_row_kernel<Tin, Tout, kVecs, false, kMasked, kThreads>, dim3(grid), dim3(kThreads), 0, stream,
+               xin, out, rows, cols, mask);
     }
 }
 
@@ -391,7 +395,20 @@ cf_status dispatch(const void* x, void* y, int64_t rows, int64_t cols, const Mas
     const bool offsets_fit = !kMasked || rows * cols * static_cast<int64_t>(sizeof(Tin)) < (1LL << 31);
     const bool vec = cols % kPer == 0 && host_aligned(x, 16) && host_aligned(y, 16) && offsets_fit;
     const int64_t vectors_per_lane = ceil_div<int64_t>(cols / kPer, kWaveSize);
-    if (vec && vectors_per_lane <= 16) {
+    const int64_t simds = static_cast<int64_t>(cu_count()) * 4;
+    if (vec && rows <= simds && vectors_per_lane > 4 && vectors_per_lane <= 16) {
+        // At most one wave per SIMD with 5-16 vectors per lane: the one-wave
+        // form's per-lane arithmetic is the latency, so each row is spread
+        // over 64 threads per vector per lane ([256, 4096] bf16: 4.05 -> 3.4
+        // us by kernel trace). With 2-4 vectors per lane the two LDS
+        // reductions cost more than they save ([1024, 2048] bf16 3.7 -> 4.2
+        // us), and those shapes keep the one-wave form.
+        if (vectors_per_lane <= 8) {
+            launch_row<Tin, Tout, 1, kMasked, 512>(x, y, rows, cols, mask, stream);
+        } else {
+            launch_row<Tin, Tout, 1, kMasked, 1024>(x, y, rows, cols, mask, stream);
+        }
+    } else if (vec && vectors_per_lane <= 16) {
         if (vectors_per_lane <= 1) {
             launch_wave<Tin, Tout, 1, kMasked>(x, y, rows, cols, mask, stream);
         } else if (vectors_per_lane <= 2) {

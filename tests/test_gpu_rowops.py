@@ -445,6 +445,42 @@ def test_softmax_long_rows(in_dtype, out_dtype, shape):
                  f"causal period {period} {shape}")
 
 
+@pytest.mark.parametrize(
+    "in_dtype,out_dtype,shape",
+    [
+        ("bf16", "bf16", (256, 4096)),   # 512 vectors: 512 threads, full
+        ("bf16", "bf16", (128, 3000)),   # 375 vectors: 512 threads, ragged
+        ("f16", "f16", (7, 6000)),       # 750 vectors: 1024 threads, ragged
+        ("bf16", "bf16", (64, 8192)),    # 1024 vectors: 1024 threads, full
+        ("f32", "f32", (1024, 1028)),    # 257 vectors at 1024 rows: the shortest such row, the most rows
+        ("f32", "bf16", (100, 2048)),    # fp32 logits to bf16 probabilities
+        ("bf16", "f32", (33, 4104)),     # bf16 logits to fp32 probabilities, 513 vectors
+        ("f32", "f32", (1025, 1028)),    # one row more than SIMDs: the one-wave form
+    ],
+    ids=str,
+)
+def test_softmax_few_rows_spread_over_a_workgroup(in_dtype, out_dtype, shape):
+    """No more rows than SIMDs with 257-1024 16-byte vectors a row: a 512- or
+    1024-thread workgroup per row, one vector per thread. Plain, in place, and
+    causally masked with NaN in every masked input, against the float64
+    oracle; masked outputs are exactly 0."""
+    rows, cols = shape
+    g.announce(f"softmax few rows {in_dtype}->{out_dtype} {shape}")
+    x = g.storage_bits((rng(rows * 5 + cols).standard_normal(shape) * 4).astype(np.float32), in_dtype)
+    xv = g.host_values(x, in_dtype)
+    assert_close(run_softmax(x, in_dtype, out_dtype), oracle.softmax(xv), out_dtype, f"softmax {shape}")
+    if in_dtype == out_dtype:
+        assert_close(run_softmax_scaled(x, in_dtype, in_dtype, 1.0, 0, in_place=True), oracle.softmax(xv), in_dtype,
+                     f"in place {shape}")
+    for period in (max(rows // 2, 1), cols):
+        z = masked_logits(xv, 0.125, period)
+        poisoned = x.copy()
+        poisoned[np.isinf(z)] = {"f32": np.nan, "bf16": 0x7FC0, "f16": 0x7E00}[in_dtype]
+        y = run_softmax_scaled(poisoned, in_dtype, out_dtype, 0.125, period)
+        assert_close(y, oracle.softmax(z), out_dtype, f"causal period {period} {shape}")
+        assert (g.host_values(y, out_dtype)[np.isinf(z)] == 0).all()
+
+
 def test_softmax_in_place():
     x = rng(10).standard_normal((16, 1024)).astype(np.float32)
     xg = g.to_gpu(x)
