@@ -546,11 +546,15 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     // wave is past it once it is at this barrier), step kt + 1 is read into
     // registers while step kt is multiplied. x pair p goes out on step
     // 2p - 3 into the slot pair p - 2 left (its last K-step, 2p - 3, was read
-    // during step 2p - 4) and is first read on step 2p - 1. DMA completes in
-    // issue order, so the wait lets exactly the previous step's loads stay
-    // in flight: w (+ a) after an even step, w (+ a) and an x pair after an
-    // odd one. The last four steps are peeled so the loop body has no
-    // branches.
+    // during step 2p - 4) and is first read on step 2p - 1. Those reads of
+    // K-step 2p - 3 are only consumed in step 2p - 3 itself, after the
+    // barrier the overwriting DMA follows, so before the barrier of an odd
+    // step every wave also drains its LDS reads (lgkmcnt 0): the slot is
+    // then free by construction rather than by where the compiler happens
+    // to place its own waits. DMA completes in issue order, so the wait
+    // lets exactly the previous step's loads stay in flight: w (+ a) after
+    // an even step, w (+ a) and an x pair after an odd one. The last four
+    // steps are peeled so the loop body has no branches.
     using yes = std::true_type;
     using no = std::false_type;
     // Steps with f0 as the current fragments are even, with f1 odd.
@@ -560,7 +564,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
             if constexpr (decltype(wait_all)::value) {
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             } else if constexpr (decltype(odd)::value) {
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads) & ~(15 << 8));  // and lgkmcnt(0)
             } else {
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads + kXLoads));
             }

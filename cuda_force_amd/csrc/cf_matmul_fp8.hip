@@ -332,7 +332,7 @@ void matmul_fp8_kernel(Fp8Args args) {
         // barrier for everyone's). The loads for kt + 3 reuse the stage of
         // kt - 1, which every wave has finished reading once it is at this
         // barrier; x pair p goes out on step 2p - 3 into the slot pair p - 2
-        // left. DMA completes in issue order, so the wait leaves exactly the
+        // left, once every wave has drained its reads of K-step 2p - 3. DMA completes in issue order, so the wait leaves exactly the
         // previous step's loads in flight: w after an even step, w and an x
         // pair after an odd one. With w_t both operands' pair p goes out on
         // step 2p - 3 and even steps issue nothing, so an even step leaves
@@ -342,10 +342,16 @@ void matmul_fp8_kernel(Fp8Args args) {
         auto step = [&](int64_t kt, XFrags& cur, XFrags& nxt, auto issue, auto wait_all, auto read,
                         auto odd) {
             if constexpr (decltype(read)::value) {
-                if constexpr (decltype(wait_all)::value || (kWT && decltype(odd)::value)) {
+                // Odd steps also drain this wave's LDS reads (lgkmcnt 0):
+                // the x (and w_t) pair sent out after this barrier overwrites
+                // the slot whose last K-step was read in the step before and
+                // is consumed only in this one.
+                if constexpr (decltype(wait_all)::value) {
                     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                } else if constexpr (kWT && decltype(odd)::value) {
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));
                 } else if constexpr (decltype(odd)::value) {
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads) & ~(15 << 8));
                 } else {
                     __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads + kXLoads));
                 }
