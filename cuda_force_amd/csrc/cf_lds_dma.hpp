@@ -46,11 +46,15 @@ __device__ __forceinline__ i32x4_t uniform(i32x4_t v) {
 /// The LDS base travels as an M0 operand: the compiler writes M0 itself (one
 /// scalar instruction, often folded into the address add) and knows its
 /// value afterwards, so nothing is saved or restored around the copy. The
-/// s_nop covers the one wait state an M0 write needs before an LDS DMA
-/// reads it.
+/// s_nop 4 gives the five wait states a vector-memory instruction needs
+/// after a VALU instruction writes an SGPR it reads (v_readlane of a spilled
+/// SGPR, v_readfirstlane), and so also the one an M0 write needs: the
+/// compiler's hazard recognizer does not look inside inline assembly, and a
+/// kernel variant whose spill reloads fed the scalar offset one to four
+/// instructions before the copy read stale offsets (wrong rows, no fault).
 __device__ __forceinline__ void dma16_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
                                          uint32_t soffset) {
-    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                  :
                  : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_dst)
                  : "memory");
@@ -58,7 +62,7 @@ __device__ __forceinline__ void dma16_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_
 
 __device__ __forceinline__ void dma4_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
                                         uint32_t soffset) {
-    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds"
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds"
                  :
                  : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_dst)
                  : "memory");
