@@ -143,6 +143,46 @@ def test_fused_bf16_matches_the_oracle(shape):
     np.testing.assert_allclose(xa[:, :r], xv.astype(np.float64) @ av, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (256, 2048, 256, 16),   # one tile, 64 K-steps
+        (300, 2048, 264, 12),   # ragged M and N, rank 12
+        (513, 4096, 520, 2),    # rank 2, a row past a tile, columns past a tile
+        (1024, 6144, 768, 16),  # 96 K-tiles
+    ],
+    ids=str,
+)
+def test_fused_bf16_long_reductions(shape):
+    """Long reductions (64 to 192 K-steps of the fused kernel's pipeline,
+    ragged tiles, small ranks): every output and x @ a against the float64
+    oracle."""
+    m, k, n, r = shape
+    g.announce(f"fused bf16 LoRA, long reduction {shape}")
+    x, w, a, b = make_operands(m, k, n, r, "bf16", seed=m + k + n + r)
+    y, xa = run_lora(x, w, a, b, "bf16", 2.0)
+    xv, wv, av, bv = (g.host_values(t, "bf16") for t in (x, w, a, b))
+    assert_gemm_close(y, oracle.lora_linear(xv, wv, av, bv, 2.0, True), "bf16", f"bf16 {shape}")
+    np.testing.assert_allclose(xa[:, :r], xv.astype(np.float64) @ av, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("shape", [(256, 2048, 256), (300, 4096, 264), (1000, 2048, 1000)], ids=str)
+def test_matmul_bf16_long_reductions(shape):
+    """cf_matmul bf16 at K >= 2048 (the rank-0 form of the fused kernel):
+    every output against the float64 product."""
+    m, k, n = shape
+    g.announce(f"bf16 matmul, long reduction {shape}")
+    gen = rng(m + 3 * k + n)
+    a = g.storage_bits(gen.standard_normal((m, k)).astype(np.float32), "bf16")
+    b = g.storage_bits((0.05 * gen.standard_normal((k, n))).astype(np.float32), "bf16")
+    ag, bg = g.to_gpu(a, "bf16"), g.to_gpu(b, "bf16")
+    cg = g.empty((m, n), torch.bfloat16)
+    g.call("cf_matmul", ag.data_ptr(), bg.data_ptr(), cg.data_ptr(), g.cf("bf16"), m, n, k, g.stream())
+    torch.cuda.synchronize()
+    exact = g.host_values(a, "bf16").astype(np.float64) @ g.host_values(b, "bf16")
+    assert_gemm_close(g.to_host(cg), exact, "bf16", f"matmul bf16 {shape}")
+
+
 def test_bf16_golden_case():
     d = load_golden("lora.npz")["bf16_64x256x128r16"]
     y, _ = run_lora(d["x"], d["w"], d["a"], d["b"], "bf16", 2.0)

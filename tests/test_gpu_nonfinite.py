@@ -154,12 +154,14 @@ def bf16_operands(m: int, k: int, n: int, r: int, seed: int):
     return tuple(g.storage_bits(t, "bf16") for t in (x, w, a, b))
 
 
-@pytest.mark.parametrize("shape", [(256, 512, 256, 8), (256, 512, 256, 16)], ids=str)
+@pytest.mark.parametrize("shape", [(256, 512, 256, 8), (256, 512, 256, 16), (256, 2048, 256, 8),
+                                   (300, 2048, 264, 16)], ids=str)
 def test_fused_bf16_lora_follows_the_reference_off_the_finite_range(shape):
     """The reference's bf16 path: x @ w + scale * (bf16(x @ a) @ b). An
     infinite x @ a times scale * b must be +-inf (the kernel splits scale * b
     into two bf16 parts; the low part is 0 for scale 2), and the adapter
-    columns past the rank (rank 8) must not turn inf * 0 into NaN."""
+    columns past the rank (rank 8) must not turn inf * 0 into NaN; at short
+    and long reductions, with ragged tiles."""
     m, k, n, r = shape
     g.announce(f"bf16 fused LoRA with inf / NaN inputs {shape}")
     bits = bf16_operands(m, k, n, r, seed=sum(shape))
