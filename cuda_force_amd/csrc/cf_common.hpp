@@ -56,10 +56,15 @@ inline constexpr int kDppRowRor4 = 0x124;       // rotate by 4 within a 16-lane 
 inline constexpr int kDppRowRor8 = 0x128;       // rotate by 8 within a 16-lane row
 inline constexpr int kDppRowHalfMirror = 0x141; // reverse each 8-lane half row
 
+/// v from another lane of the same 16-lane row (the controls above never
+/// address a lane outside it). bound_ctrl is set because that lets the
+/// compiler fold the move into the reduction instruction that consumes it
+/// (v_max_u32_dpp, v_add_f32_dpp: one VALU instruction per step instead of
+/// two); with no out-of-row source it changes no value.
 template <int kCtrl>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
     return static_cast<uint32_t>(
-        __builtin_amdgcn_mov_dpp(static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+        __builtin_amdgcn_mov_dpp(static_cast<int>(v), kCtrl, 0xF, 0xF, true));
 }
 
 template <int kCtrl>
