@@ -47,7 +47,14 @@ namespace {
 // 48 bf16 tensors of config 5's shapes (4.25 GB per launch) 720 -> 694 us
 // (72.9% -> 75.7%) against 8, in a same-process A/B; 10 gave 74.4%, 14 76.1%.
 // 12 steps for the grouped quantiser were slower (70.8% -> 66.3%).
+// Fewer dequantising steps per wave, which a bare read-8-bytes /
+// write-16-bytes stream favours (one step: 84.6% against 73.4% with 12 at
+// 48 x 16M codes), lose here: the grouped kernel's per-wave tensor search and
+// scale loads then dominate (kernel trace, 48 x [4096, 4096] bf16: 12 steps
+// 407 us, 4 steps 466, 2 steps 722, 1 step 1101; fp32 [4096, 4096]: 4 steps
+// 15.1 us, 2 steps 15.3, 1 step 18.6; bit-identical).
 constexpr int kUnroll = 4;
+constexpr int kDequantUnroll = 4;
 constexpr int kGroupUnroll = 8;
 constexpr int kDequantGroupUnroll = 12;
 constexpr float kTieMargin = 6.0e-5f;
@@ -408,10 +415,10 @@ __global__ __launch_bounds__(kDefaultBlockSize) void dequantize_kernel(
     const int8_t* __restrict__ q, const float* __restrict__ scales, Tout* __restrict__ y,
     int64_t count) {
     const int64_t wave = grid_wave();
-    if (kVec && (wave + 1) * dequant_elements_per_wave<Tout>() <= count) {
-        dequantize_body<Tout, kVec, true>(q, scales, y, count, wave);
+    if (kVec && (wave + 1) * dequant_elements_per_wave<Tout, kDequantUnroll>() <= count) {
+        dequantize_body<Tout, kVec, true, kDequantUnroll>(q, scales, y, count, wave);
     } else {
-        dequantize_body<Tout, kVec, false>(q, scales, y, count, wave);
+        dequantize_body<Tout, kVec, false, kDequantUnroll>(q, scales, y, count, wave);
     }
 }
 
@@ -427,8 +434,7 @@ int64_t quant_grid(int64_t count) {
 
 template <typename T>
 int64_t dequant_grid(int64_t count) {
-    constexpr int64_t kPerWave = static_cast<int64_t>(kWaveSize) * Storage<T>::kPerVec * kUnroll;
-    const int64_t waves = ceil_div<int64_t>(count, kPerWave);
+    const int64_t waves = ceil_div<int64_t>(count, dequant_elements_per_wave<T, kDequantUnroll>());
     return ceil_div<int64_t>(waves, kDefaultBlockSize / kWaveSize);
 }
 
