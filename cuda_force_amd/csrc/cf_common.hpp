@@ -462,6 +462,19 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+/// Cache-policy operand of the buffer intrinsics on gfx950: bit 1 is the
+/// non-temporal (streaming) hint.
+inline constexpr int kCacheNonTemporal = 2;
+
+/// buffer_load16 with the non-temporal hint, for operands read exactly once
+/// (the LoRA backward's passes over dy and x: 37.9 -> 34.7 us at 8192 x 4096
+/// x 4096 against plain loads, bit-identical).
+__device__ __forceinline__ uint4 buffer_load16_stream(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset,
+                                                      uint32_t soffset) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, kCacheNonTemporal);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ uint16_t buffer_load2(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset,
                                                  uint32_t soffset) {
     return __builtin_amdgcn_raw_buffer_load_b16(rsrc, voffset, soffset, 0);

@@ -11,7 +11,8 @@
 // The work is two reductions over M of HBM-sized operands, so the design
 // reads dy once and x once (the HBM floor) and keeps everything else small:
 //   1. One pass over dy in 512-row x 256-column tiles (Mp = M rounded up to
-//      512), two 64-row chunks in flight per workgroup: each chunk goes
+//      512), two 64-row chunks in flight per workgroup, loaded with the
+//      non-temporal hint (every byte is read once): each chunk goes
 //      HBM -> registers -> LDS; G partial rows = chunk @
 //      b^T (16x16x32 MFMA, row fragments by ds_read_b128, b fragments held in
 //      registers) and grad_b partials += bf16(xa)^T-chunk @ chunk (16x16x32
@@ -159,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void column_mfma_kernel(ColumnArgs args) 
             const int64_t row = row0 + 8 * i + (tid >> 5);
             const uint32_t off =
                 col_ok ? static_cast<uint32_t>((row * C + piece_col) * 2) : kOutOfRange;
-            staged[slot][i] = buffer_load16(vbuf, off, 0);
+            staged[slot][i] = buffer_load16_stream(vbuf, off, 0);
         }
         if constexpr (kRowDot) {
             // Past the chunk's kChunkRows x rank elements (rank < 16), or past

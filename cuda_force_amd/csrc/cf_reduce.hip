@@ -67,7 +67,7 @@ __device__ __forceinline__ float range_sum(const T* __restrict__ x, int64_t begi
         for (; e + (kUnroll - 1) * step + kPer <= end; e += kUnroll * step) {
             uint4 raw[kUnroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) raw[u] = *reinterpret_cast<const uint4*>(x + e + u * step);
+            for (int u = 0; u < kUnroll; ++u) raw[u] = load_stream16(x + e + u * step);
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 float v[kPer];
@@ -78,7 +78,7 @@ __device__ __forceinline__ float range_sum(const T* __restrict__ x, int64_t begi
         }
         for (; e + kPer <= end; e += step) {
             float v[kPer];
-            unpack16<T>(*reinterpret_cast<const uint4*>(x + e), v);
+            unpack16<T>(load_stream16(x + e), v);
 #pragma unroll
             for (int i = 0; i < kPer; ++i) acc[i & 3] += v[i];
         }
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void row_sum_kernel(const T* __r
             for (; e + 3 * kStep < cols; e += 4 * kStep) {  // four loads in flight per lane
                 uint4 raw[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) raw[u] = *reinterpret_cast<const uint4*>(xr + e + u * kStep);
+                for (int u = 0; u < 4; ++u) raw[u] = load_stream16(xr + e + u * kStep);
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     float v[kPer];
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kDefaultBlockSize) void row_sum_kernel(const T* __r
             }
             for (; e < cols; e += kStep) {
                 float v[kPer];
-                unpack16<T>(*reinterpret_cast<const uint4*>(xr + e), v);
+                unpack16<T>(load_stream16(xr + e), v);
 #pragma unroll
                 for (int i = 0; i < kPer; ++i) acc[i & 3] += v[i];
             }
