@@ -356,13 +356,12 @@ __global__ __launch_bounds__(kDefaultBlockSize) void fake_quant_kernel(const T* 
 }
 
 /// y = float(q) * s, one multiply, rounded to Tout. Each lane owns kPer
-/// consecutive elements (always inside one block); a wave stores 1 KiB per
-/// step with 16-byte non-temporal stores. The codes are read with plain
-/// loads: config 1's dequantise (16 MiB of codes in, 64 MiB out) ran 71.7% ->
-/// 81.7% of HBM peak against non-temporal code loads, and device-scope (sc1)
-/// output stores instead of non-temporal ones took it to 62%. kFull: the
-/// wave's whole range is below `count` and aligned, so nothing is
-/// bounds-tested.
+/// consecutive elements (always inside one block); codes come in by
+/// non-temporal loads and a wave stores 1 KiB per step with 16-byte
+/// non-temporal stores. (Plain code loads measured 70% against 71% of HBM
+/// peak at config 1 once no launch could find its codes in the Infinity
+/// Cache; device-scope (sc1) output stores, 62%.) kFull: the wave's whole
+/// range is below `count` and aligned, so nothing is bounds-tested.
 template <typename Tout, bool kVec, bool kFull, int kU = kUnroll>
 __device__ __forceinline__ void dequantize_body(const int8_t* __restrict__ q,
                                                 const float* __restrict__ scales,
@@ -381,11 +380,11 @@ __device__ __forceinline__ void dequantize_body(const int8_t* __restrict__ q,
         scale[u] = (kFull || e < count) ? scales[e / kQuantBlockSize] : 0.0f;
         if (kFull || (kVec && e + kPer <= count)) {
             if constexpr (kPer == 4) {
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(q + e);
+                const uint32_t w = load_stream4(q + e);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) codes[u][i] = static_cast<int8_t>((w >> (8 * i)) & 0xFFu);
             } else {
-                const uint2 w = *reinterpret_cast<const uint2*>(q + e);
+                const uint2 w = load_stream8(q + e);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     codes[u][i] = static_cast<int8_t>((w.x >> (8 * i)) & 0xFFu);
