@@ -397,19 +397,19 @@ def bench_ceiling(torch, cf, warmup: int, runs: int) -> dict:
     """Config 1's kernels next to the streaming ceilings of their traffic, all
     under the same conditions: 32 rotating buffer sets (2.6 GB, so no launch
     finds its input in the 256 MB Infinity Cache), one untimed pass over them,
-    then two passes launched back to back straight through ctypes (a Python
-    launch loop with per-call overhead near these ~15 us kernels' duration
-    lets the queue run dry between them) and timed by one HIP event pair.
-    Kernels: quantise and dequantise fp32 [4096, 4096]; reading the 64 MiB
-    input alone; writing 16 MiB alone; reading 64 MiB and writing 16 MiB
-    with the quantiser's pattern (cf_stream_bytes divisors 0, -1 and 4); and a
-    64 MiB copy; and config 5's 2 : 1 read/write mix at the size of one
-    grouped launch. `median_ms` is the median over 3 rounds of the per-launch
+    then two passes captured into a HIP graph and replayed (dispatches back
+    to back, with no host launch loop, which kernels of a few microseconds
+    outrun), each replay timed by a HIP event pair. Kernels: quantise and
+    dequantise fp32 [4096, 4096]; reading the 64 MiB input alone; writing
+    16 MiB alone (four stores per lane, and one store per lane under each
+    cache policy: cf_stream_bytes divisors -1 .. -5); reading 64 MiB and
+    writing 16 MiB with the quantiser's pattern (divisors 0 and 4); a 64 MiB
+    copy; and config 5's 2 : 1 read/write mix at the size of one grouped
+    launch. `median_ms` is the median over 3 replays of the per-launch
     time."""
     gen = torch.Generator(device="cuda").manual_seed(11)
     n = 4096 * 4096
     lib = cf._lib.load()
-    st = torch.cuda.current_stream().cuda_stream
     nsets = 32
     xs = [with_outliers(torch, gen, torch.randn(n, generator=gen, device="cuda"), 0.01, 20.0)
           for _ in range(nsets)]
@@ -418,14 +418,27 @@ def bench_ceiling(torch, cf, warmup: int, runs: int) -> dict:
     ys = [torch.empty(n, device="cuda") for _ in range(nsets)]
     xp, qp, sp, yp = ([t.data_ptr() for t in ts] for ts in (xs, qs, ss, ys))
     f32 = cf._lib.CF_F32
+    # Each launch reads the current stream when it is made, so the same
+    # closures run eagerly and under graph capture.
+    def cur():
+        return torch.cuda.current_stream().cuda_stream
+
     kinds = {
-        "quantize_f32_4096x4096": (bytes_quant(n, 4), lambda i: lib.cf_quantize_int8(xp[i], f32, qp[i], sp[i], n, st)),
+        "quantize_f32_4096x4096": (bytes_quant(n, 4),
+                                   lambda i: lib.cf_quantize_int8(xp[i], f32, qp[i], sp[i], n, cur())),
         "dequantize_f32_4096x4096": (bytes_dequant(n, 4),
-                                     lambda i: lib.cf_dequantize_int8(qp[i], sp[i], yp[i], f32, n, st)),
-        "read_only_64MiB": (n * 4, lambda i: lib.cf_stream_bytes(xp[i], sp[i], n * 4, 0, st)),
-        "write_only_16MiB": (n, lambda i: lib.cf_stream_bytes(None, qp[i], n, -1, st)),
-        "read_64MiB_write_16MiB": (n * 5, lambda i: lib.cf_stream_bytes(xp[i], qp[i], n * 4, 4, st)),
-        "copy_64MiB": (n * 8, lambda i: lib.cf_copy_bytes(xp[i], yp[i], n * 4, st)),
+                                     lambda i: lib.cf_dequantize_int8(qp[i], sp[i], yp[i], f32, n, cur())),
+        "read_only_64MiB": (n * 4, lambda i: lib.cf_stream_bytes(xp[i], sp[i], n * 4, 0, cur())),
+        "write_only_16MiB": (n, lambda i: lib.cf_stream_bytes(None, qp[i], n, -1, cur())),
+        # The same 16 MiB written with one 16-byte store per lane, under each
+        # cache policy the stores can carry: the fastest of these is the best
+        # this box writes 16 MiB in one launch.
+        "write_only_16MiB_once_nt": (n, lambda i: lib.cf_stream_bytes(None, qp[i], n, -2, cur())),
+        "write_only_16MiB_once_device_scope": (n, lambda i: lib.cf_stream_bytes(None, qp[i], n, -3, cur())),
+        "write_only_16MiB_once_nt_device_scope": (n, lambda i: lib.cf_stream_bytes(None, qp[i], n, -4, cur())),
+        "write_only_16MiB_once_plain": (n, lambda i: lib.cf_stream_bytes(None, qp[i], n, -5, cur())),
+        "read_64MiB_write_16MiB": (n * 5, lambda i: lib.cf_stream_bytes(xp[i], qp[i], n * 4, 4, cur())),
+        "copy_64MiB": (n * 8, lambda i: lib.cf_copy_bytes(xp[i], yp[i], n * 4, cur())),
     }
     # Config 5's bulk bf16 quantiser moves 2 bytes in per byte out in launches
     # of up to 48 tensors (~2.3 GB each): its traffic mix at that scale, one
@@ -434,21 +447,17 @@ def bench_ceiling(torch, cf, warmup: int, runs: int) -> dict:
     big_in = torch.empty(big, dtype=torch.uint8, device="cuda")
     big_out = torch.empty(big // 2, dtype=torch.uint8, device="cuda")
     kinds["read_1536MiB_write_768MiB"] = (
-        big + big // 2, lambda i: lib.cf_stream_bytes(big_in.data_ptr(), big_out.data_ptr(), big, 2, st))
+        big + big // 2, lambda i: lib.cf_stream_bytes(big_in.data_ptr(), big_out.data_ptr(), big, 2, cur()))
     samples: dict[str, list[float]] = {}
-    for _ in range(3):
-        for label, (_, call) in kinds.items():
-            for i in range(nsets):  # untimed pass, statuses checked
-                cf._lib.check(call(i))
-            start = torch.cuda.Event(enable_timing=True)
-            stop = torch.cuda.Event(enable_timing=True)
-            start.record()
-            for _ in range(2):
-                for i in range(nsets):
-                    call(i)
-            stop.record()
-            torch.cuda.synchronize()
-            samples.setdefault(label, []).append(start.elapsed_time(stop) / (2 * nsets))
+    for label, (_, call) in kinds.items():
+        for i in range(nsets):  # untimed pass, statuses checked
+            cf._lib.check(call(i))
+        torch.cuda.synchronize()
+        # Two passes over the sets captured into one HIP graph (kernels only)
+        # and replayed: dispatches back to back, with no host launch loop that
+        # kernels of a few microseconds would outrun.
+        samples[label] = graph_times(torch, [lambda i=i, call=call: call(i) for i in range(nsets)],
+                                     runs=2 * nsets, batches=3)
     out = {}
     for label, (nbytes, _) in kinds.items():
         r = summary(samples[label])

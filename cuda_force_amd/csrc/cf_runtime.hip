@@ -185,6 +185,17 @@ __global__ __launch_bounds__(256) void write_stream_kernel(uint4* __restrict__ d
     }
 }
 
+/// Write only, one 16-byte store per lane (the grid covers the bytes once),
+/// with cache policy kPolicy on a buffer store: 2 non-temporal, 16
+/// device-scope (sc1), 18 both, 0 none.
+template <int kPolicy>
+__global__ __launch_bounds__(256) void write_once_kernel(uint8_t* __restrict__ dst, uint32_t bytes) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    const __amdgpu_buffer_rsrc_t out = make_buffer(dst, bytes);
+    const u32x4_t v = {i, ~i, i ^ 0x5bd1e995u, i + 1u};
+    __builtin_amdgcn_raw_buffer_store_b128(v, out, 16u * i, 0, kPolicy);
+}
+
 __global__ void copy_tail_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                  int64_t bytes) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -231,13 +242,16 @@ int cf_time_next_launch_armed(void) { return cf::launch_events_armed() ? 1 : 0; 
 cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int divisor, void* stream) {
     CF_ENTRY();
     if (read_bytes <= 0) return CF_OK;
-    CF_REQUIRE(dst != nullptr && (src != nullptr || divisor == -1), "cf_stream_bytes: null pointer");
-    CF_REQUIRE(divisor == 1 || divisor == 2 || divisor == 4 || divisor == 0 || divisor == -1,
-               "cf_stream_bytes: divisor %d is not 1, 2, 4, 0 or -1", divisor);
+    CF_REQUIRE(dst != nullptr && (src != nullptr || divisor < 0), "cf_stream_bytes: null pointer");
+    CF_REQUIRE(divisor == 1 || divisor == 2 || divisor == 4 || divisor == 0 ||
+                   (divisor <= -1 && divisor >= -5),
+               "cf_stream_bytes: divisor %d is not 1, 2, 4, 0 or -1 .. -5", divisor);
+    CF_REQUIRE(divisor >= -1 || read_bytes < (1LL << 32),
+               "cf_stream_bytes: the one-store-per-lane write streams take under 4 GiB");
     constexpr int64_t kChunk = 256 * cf::kCopyUnroll * 16;
     CF_REQUIRE(read_bytes % kChunk == 0, "cf_stream_bytes: %lld bytes are not a multiple of %lld",
                static_cast<long long>(read_bytes), static_cast<long long>(kChunk));
-    CF_REQUIRE((divisor == -1 || cf::host_aligned(src, 16)) && cf::host_aligned(dst, 16),
+    CF_REQUIRE((divisor < 0 || cf::host_aligned(src, 16)) && cf::host_aligned(dst, 16),
                "cf_stream_bytes: src and dst must be 16-byte aligned");
     const int64_t grid = read_bytes / kChunk;
     CF_REQUIRE(grid < (1LL << 31), "cf_stream_bytes: %lld bytes exceed the launch limit",
@@ -246,8 +260,18 @@ cf_status cf_stream_bytes(const void* src, void* dst, int64_t read_bytes, int di
     const dim3 g(static_cast<unsigned>(grid));
     const auto* in = static_cast<const uint4*>(src);
     auto* out = static_cast<uint8_t*>(dst);
+    const dim3 g_once(static_cast<unsigned>(grid * cf::kCopyUnroll));
+    const auto bytes32 = static_cast<uint32_t>(read_bytes);
     if (divisor == -1) {
         cf::launch(cf::write_stream_kernel, g, dim3(256), 0, s, static_cast<uint4*>(dst));
+    } else if (divisor == -2) {
+        cf::launch(cf::write_once_kernel<2>, g_once, dim3(256), 0, s, out, bytes32);
+    } else if (divisor == -3) {
+        cf::launch(cf::write_once_kernel<16>, g_once, dim3(256), 0, s, out, bytes32);
+    } else if (divisor == -4) {
+        cf::launch(cf::write_once_kernel<18>, g_once, dim3(256), 0, s, out, bytes32);
+    } else if (divisor == -5) {
+        cf::launch(cf::write_once_kernel<0>, g_once, dim3(256), 0, s, out, bytes32);
     } else if (divisor == 0) {
         cf::launch(cf::stream_kernel<0>, g, dim3(256), 0, s, in, out);
     } else if (divisor == 1) {

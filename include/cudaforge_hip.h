@@ -454,8 +454,11 @@ cf_status cf_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream)
  * access pattern (four 16-byte loads per lane, then the stores; one-shot
  * grid). Divisor 0 only reads (dst receives one 4-byte word per 16 KiB
  * read); divisor -1 only writes read_bytes bytes to dst with the same store
- * pattern (src unused, may be NULL). read_bytes must be a multiple of 16 KiB
- * and the pointers used 16-byte aligned. It has no counterpart in the
+ * pattern (src unused, may be NULL); divisors -2 .. -5 also only write, one
+ * 16-byte store per lane, with the non-temporal (-2), device-scope (-3),
+ * both (-4) or no (-5) cache-policy bits (read_bytes under 4 GiB).
+ * read_bytes must be a multiple of 16 KiB and the pointers used 16-byte
+ * aligned. It has no counterpart in the
  * reference: it measures the streaming ceiling of a traffic mix (divisor 4
  * is the fp32 quantiser's 4 : 1) and of its read and write halves next to
  * the kernels that move them. */

@@ -206,6 +206,9 @@ def test_stream_bytes_host_checks(lib):
     assert lib.cf_stream_bytes(null, fake, 16384, 0, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_stream_bytes(fake, fake, 1000, 4, null) == _lib.CF_ERR_INVALID_ARGUMENT
     assert lib.cf_stream_bytes(null, fake, 16384, 4, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_stream_bytes(null, null, 16384, -3, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_stream_bytes(null, fake, 16384, -6, null) == _lib.CF_ERR_INVALID_ARGUMENT
+    assert lib.cf_stream_bytes(null, fake, 1 << 32, -2, null) == _lib.CF_ERR_INVALID_ARGUMENT
 
 
 def test_attention_products_host_checks(lib):

@@ -135,3 +135,17 @@ def test_stream_bytes_read_only_and_write_only_modes():
     expect = torch.stack([i, ~i & 0xFFFFFFFF, i ^ 0x5BD1E995, i + 1], dim=1) & 0xFFFFFFFF
     got = out.view(-1, 4).to(torch.int64) & 0xFFFFFFFF
     assert torch.equal(got, expect)
+
+
+@pytest.mark.parametrize("divisor", [-2, -3, -4, -5])
+def test_stream_bytes_write_once_modes(divisor):
+    """Divisors -2 .. -5 write only, one 16-byte store per lane (vector i =
+    (i, ~i, i ^ 0x5bd1e995, i + 1)), whatever their cache-policy bits."""
+    print(f"case: cf_stream_bytes write-once divisor {divisor}", flush=True)
+    out = torch.zeros(1 << 14, dtype=torch.int32, device="cuda")  # 64 KiB
+    call("cf_stream_bytes", None, out.data_ptr(), out.numel() * 4, divisor, stream())
+    torch.cuda.synchronize()
+    i = torch.arange(1 << 12, dtype=torch.int64, device="cuda")
+    expect = torch.stack([i, ~i & 0xFFFFFFFF, i ^ 0x5BD1E995, i + 1], dim=1) & 0xFFFFFFFF
+    got = out.view(-1, 4).to(torch.int64) & 0xFFFFFFFF
+    assert torch.equal(got, expect)
