@@ -46,20 +46,21 @@ namespace {
 // (config 1's fp32 [4096, 4096] ran 15.6 us against 16.1 with 8), 8 for the
 // grouped launches of bulk quantisation (bf16 [4096, 4096] x 48 per launch:
 // quantise 68% -> 75.5%, dequantise 65.5% -> 74% of HBM peak against 4).
-// Grouped dequantisation reads 8 codes per lane and step and takes 12 steps:
-// 48 bf16 tensors of config 5's shapes (4.25 GB per launch) 720 -> 694 us
-// (72.9% -> 75.7%) against 8, in a same-process A/B; 10 gave 74.4%, 14 76.1%.
-// 12 steps for the grouped quantiser were slower (70.8% -> 66.3%).
-// Fewer dequantising steps per wave, which a bare read-8-bytes /
-// write-16-bytes stream favours (one step: 84.6% against 73.4% with 12 at
-// 48 x 16M codes), lose here: the grouped kernel's per-wave tensor search and
-// scale loads then dominate (kernel trace, 48 x [4096, 4096] bf16: 12 steps
-// 407 us, 4 steps 466, 2 steps 722, 1 step 1101; fp32 [4096, 4096]: 4 steps
-// 15.1 us, 2 steps 15.3, 1 step 18.6; bit-identical).
+// Grouped dequantisation reads 8 codes per lane and step and takes 2 steps,
+// finding its tensor with one ballot (group_member_ballot): config 5's
+// grouped dequantise 74.6-74.9% -> 77.5-77.7% of HBM peak against 12 steps
+// with a binary search, bit-identical. A bare read-8-bytes / write-16-bytes
+// stream favours few steps (one: 84.6%, twelve: 73.4% at 48 x 16M codes),
+// but with the binary search, six dependent loads of the kernel arguments
+// per wave, fewer steps lost (2 steps 43.6%); with the ballot 1 step gave
+// 62.5%, 4 steps 75.4%, 12 steps 71.5-71.9%. The grouped quantiser keeps the
+// binary search (75.6-75.9% with the ballot against 76.7-77.4%). Single
+// tensors: fp32 [4096, 4096] dequantise 4 steps 15.1 us, 2 steps 15.3,
+// 1 step 18.6.
 constexpr int kUnroll = 4;
 constexpr int kDequantUnroll = 4;
 constexpr int kGroupUnroll = 8;
-constexpr int kDequantGroupUnroll = 12;
+constexpr int kDequantGroupUnroll = 2;
 constexpr float kTieMargin = 6.0e-5f;
 constexpr float kMinFastScale = 7.88860905e-31f;  // 2^-100
 constexpr float kRoundShift = 12582912.0f;        // 3 * 2^22
@@ -455,9 +456,10 @@ constexpr int64_t kMaxGrid = 2147483647;
 // Grouped launches: up to CF_QUANT_GROUP_MAX tensors per kernel, described in
 // the kernel arguments (no device-side staging, nothing allocated). Tensor t
 // owns grid waves [first_wave[t], first_wave[t + 1]); each wave finds its
-// tensor by a binary search over first_wave (scalar loads from the kernel
-// argument segment) and then runs the single-tensor body with its index
-// inside that tensor. Every tensor of a group is vector-aligned.
+// tensor in first_wave (a binary search of scalar loads from the kernel
+// argument segment for quantisation, one ballot over a vector load for
+// dequantisation) and then runs the single-tensor body with its index inside
+// that tensor. Every tensor of a group is vector-aligned.
 // ---------------------------------------------------------------------------
 
 constexpr int kGroupMax = CF_QUANT_GROUP_MAX;
@@ -496,6 +498,16 @@ __device__ __forceinline__ int group_member(const int64_t* first_wave, int n, in
     return lo;
 }
 
+/// The same index t in one round trip: lane l reads tensor l's first wave
+/// (n <= 48 < 64 lanes) and a ballot counts the tensors that start at or
+/// before `wave` (first_wave is increasing and first_wave[0] = 0). Every lane
+/// of the wave must be active; the caller has checked wave < first_wave[n].
+__device__ __forceinline__ int group_member_ballot(const int64_t* first_wave, int n, int64_t wave) {
+    const int lane = static_cast<int>(threadIdx.x) & (kWaveSize - 1);
+    const int64_t fw = lane < n ? first_wave[lane] : INT64_MAX;
+    return __popcll(__ballot(fw <= wave)) - 1;
+}
+
 template <typename T>
 __global__ __launch_bounds__(kDefaultBlockSize) void quantize_group_kernel(QuantGroupArgs args) {
     const int64_t gw = grid_wave();
@@ -515,7 +527,7 @@ template <typename Tout>
 __global__ __launch_bounds__(kDefaultBlockSize) void dequantize_group_kernel(DequantGroupArgs args) {
     const int64_t gw = grid_wave();
     if (gw >= args.first_wave[args.n]) return;  // wave-uniform
-    const int t = group_member(args.first_wave, args.n, gw);
+    const int t = group_member_ballot(args.first_wave, args.n, gw);
     const int64_t wave = gw - args.first_wave[t];
     Tout* y = static_cast<Tout*>(args.y[t]);
     const int64_t count = args.count[t];
