@@ -47,6 +47,8 @@
 #include "cf_lora_fused.hpp"
 #include "cf_lds_dma.hpp"
 
+#include <cmath>
+
 #include <type_traits>
 
 namespace cf {
@@ -150,8 +152,10 @@ struct XFrags {
 /// xacc[t] holds (x @ a) for row block 2 wn + t of the wave's 64 rows. Every
 /// wave must have finished reading operands from LDS (the first barrier
 /// below, or the one before the staged stores, orders the reuse of the
-/// operand area).
-template <bool kAdapter, bool kOutF32>
+/// operand area). kSplitB false: scale * b is exact in bf16 (the host
+/// passes it for a scale of 0 or +-2^k, k >= 0), so its low part is zero and
+/// only the high pass runs.
+template <bool kAdapter, bool kOutF32, bool kSplitB = true>
 __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds, f32x4_t (&acc)[8][4],
                                             const f32x4_t (&xacc)[2], int wave, int lane, int tn,
                                             int64_t m0, int64_t n0) {
@@ -209,7 +213,7 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
         const uint8_t* tb = lds + kOffB;
         // Two passes (high parts, then low parts) keep one b fragment live.
 #pragma unroll
-        for (int part = 0; part < 2; ++part) {
+        for (int part = 0; part < (kSplitB ? 2 : 1); ++part) {
             if (part == 1) {
                 // An infinite x @ a meets only the high part of scale * b:
                 // inf * lo would add NaN (lo = 0) or an infinity of the
@@ -314,7 +318,7 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
     }
 }
 
-template <bool kAdapter, bool kOutF32>
+template <bool kAdapter, bool kOutF32, bool kSplitB = true>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lora_fused_bf16_kernel(FusedArgs args) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
@@ -592,7 +596,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         run(std::false_type{});
     }
 
-    finish_tile<kAdapter, kOutF32>(args, lds, acc, xacc, wave, lane, tn, m0, n0);
+    finish_tile<kAdapter, kOutF32, kSplitB>(args, lds, acc, xacc, wave, lane, tn, m0, n0);
 }
 
 }  // namespace
@@ -630,7 +634,18 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
     args.tiles_m = static_cast<int>(ceil_div<int64_t>(M, kBM));
     args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
     const int grid = args.tiles_m * args.tiles_n;
-    if (rank > 0) {
+    // scale * b is exact in bf16 for every bf16 b when the scale is 0 or
+    // +-2^k with k >= 0 (the exponent only moves up; an overflow gives the
+    // infinity the fp32 product has): the epilogue then skips the pass over
+    // the low parts, which would add zeros (config 3's scale of 2: 213.4 ->
+    // 211.7 and 219.3 -> 218.7 us in two same-process A/Bs, within their
+    // noise).
+    int exponent = 0;
+    const float mantissa = std::frexp(std::fabs(scale), &exponent);
+    const bool exact_b = scale == 0.0f || (mantissa == 0.5f && exponent >= 1);
+    if (rank > 0 && exact_b) {
+        launch(lora_fused_bf16_kernel<true, false, false>, dim3(grid), dim3(kThreads), 0, stream, args);
+    } else if (rank > 0) {
         launch(lora_fused_bf16_kernel<true, false>, dim3(grid), dim3(kThreads), 0, stream, args);
     } else {
         launch(lora_fused_bf16_kernel<false, false>, dim3(grid), dim3(kThreads), 0, stream, args);
