@@ -30,8 +30,9 @@ The stdout line stays under 4 KB: besides the contract's fields it carries
 `configs`, a few figures per configuration (C1 quantise/dequantise GB/s from
 back-to-back launches, C2 RMSNorm GB/s from the kernels' own timestamps and the
 softmax's microseconds per launch from a replayed HIP graph of back-to-back
-launches, C3 fused LoRA TFLOP/s with
-hipBLASLt's plain GEMM beside it and the adapter backward GB/s, C4 tokens/s,
+launches, C3 fused LoRA TFLOP/s from its kernels' timestamps, its and
+hipBLASLt's plain GEMM's microseconds per launch from back-to-back launches
+(the same method for both), and the adapter backward GB/s, C4 tokens/s,
 C5 aggregate GB/s). The full breakdown goes to the `--detail` file
 (gpurun_out/bench_detail.json by default) and nowhere else.
 
@@ -715,7 +716,9 @@ def bench_lora(torch, cf, warmup: int, runs: int) -> dict:
     """config 3: fused LoRA bf16 8192x4096x4096 r16, alpha 32; adapter backward.
     Operand sets (x, W, A, B, y, dY, x@A) rotate until they exceed 1 GiB, so the
     forward and the backward read their operands from HBM, not from the 256 MB
-    Infinity Cache; hipBLASLt's plain GEMM runs on the same sets."""
+    Infinity Cache; hipBLASLt's plain GEMM runs on the same sets. The forward
+    goes through cf_lora_linear_ws with the workspace it asks for (x @ a shared
+    between column tiles), the entry point the torch operator calls."""
     gen = torch.Generator(device="cuda").manual_seed(4)
     m, k, n, r = 8192, 4096, 4096, 16
     lib = cf._lib.load()
@@ -733,10 +736,14 @@ def bench_lora(torch, cf, warmup: int, runs: int) -> dict:
                      "xa": torch.empty(m, r, device="cuda")})
         del W, A, B
 
+    fwd_ws_bytes = lib.cf_lora_linear_ws_bytes(cf._lib.CF_BF16, m, k, n, r)
+    fwd_ws = torch.empty(max(fwd_ws_bytes, 1), dtype=torch.uint8, device="cuda")
+
     def fused(s, xa_out=None):
-        return lambda: cf._lib.check(lib.cf_lora_linear(
+        return lambda: cf._lib.check(lib.cf_lora_linear_ws(
             s["x"].data_ptr(), s["w"].data_ptr(), s["a"].data_ptr(), s["b"].data_ptr(), s["y"].data_ptr(),
-            xa_out, cf._lib.CF_BF16, m, k, n, r, 2.0, torch.cuda.current_stream().cuda_stream))
+            xa_out, cf._lib.CF_BF16, m, k, n, r, 2.0, fwd_ws.data_ptr() if fwd_ws_bytes else None,
+            fwd_ws_bytes, torch.cuda.current_stream().cuda_stream))
 
     launches = [fused(s) for s in sets]
     f = summary(time_launches(torch, launches, warmup, runs))
@@ -1069,6 +1076,8 @@ SUMMARY_FIELDS = {
            "softmax_us": ("softmax_bf16_causal_1024x2048", "graph_median_ms")},
     "c3": {"fused_TFLOP/s": ("lora_bf16_8192x4096x4096_r16", "kernel_TFLOP/s"),
            "fused_frac_mfma": ("lora_bf16_8192x4096x4096_r16", "kernel_frac_peak"),
+           "fused_us": ("lora_bf16_8192x4096x4096_r16", "median_ms"),
+           "hipblaslt_gemm_us": ("hipblaslt_gemm_bf16_8192x4096x4096_context", "median_ms"),
            "hipblaslt_gemm_TFLOP/s": ("hipblaslt_gemm_bf16_8192x4096x4096_context", "TFLOP/s"),
            "backward_GB/s": ("lora_backward_bf16_8192x4096x4096_r16", "kernel_GB/s"),
            "backward_frac_hbm": ("lora_backward_bf16_8192x4096x4096_r16", "kernel_frac_hbm")},

@@ -463,8 +463,11 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint
 }
 
 /// Cache-policy operand of the buffer intrinsics on gfx950: bit 1 is the
-/// non-temporal (streaming) hint.
+/// non-temporal (streaming) hint; bit 4 (sc1) gives the access device
+/// scope: a store is acknowledged once it is visible to every CU of the GPU
+/// (whichever XCD's L2 they sit behind), a load reads that level.
 inline constexpr int kCacheNonTemporal = 2;
+inline constexpr int kCacheDeviceScope = 16;
 
 /// buffer_load16 with the non-temporal hint, for operands read exactly once
 /// (the LoRA backward's passes over dy and x: 37.9 -> 34.7 us at 8192 x 4096

@@ -60,6 +60,16 @@ __device__ __forceinline__ void dma16_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_
                  : "memory");
 }
 
+/// dma16_m0 at device scope (sc1): reads what another workgroup published
+/// with device-scope stores, past this XCD's L2.
+__device__ __forceinline__ void dma16_device_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
+                                                uint32_t soffset) {
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen sc1 lds"
+                 :
+                 : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_dst)
+                 : "memory");
+}
+
 __device__ __forceinline__ void dma4_m0(i32x4_t rsrc, uint32_t lds_dst, uint32_t voffset,
                                         uint32_t soffset) {
     asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds"

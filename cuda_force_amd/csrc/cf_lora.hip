@@ -318,7 +318,7 @@ cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void
     if (dtype == CF_BF16 &&
         cf::lora_fused_eligible(x, w, a, b, batch, out_features, in_features, rank)) {
         return cf::launch_lora_fused(x, w, a, b, y, xa_out, batch, out_features, in_features, rank,
-                                scale, s);
+                                scale, nullptr, s);
     }
     if (dtype == CF_F32 &&
         cf::lora_f32_eligible(x, w, a, b, y, batch, out_features, in_features, rank)) {
@@ -340,6 +340,14 @@ cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void
 
 size_t cf_lora_linear_ws_bytes(cf_dtype dtype, int64_t batch, int64_t in_features,
                                int64_t out_features, int64_t rank) {
+    if (dtype == CF_BF16) {
+        // The fused kernel's shapes (its pointer checks aside): x @ a shared
+        // between the column tiles of a row tile.
+        const bool fused_shape = batch > 0 && out_features > 0 && in_features > 0 &&
+                                 in_features % 64 == 0 && out_features % 8 == 0 && rank > 0 &&
+                                 rank <= 16 && rank % 2 == 0;
+        return fused_shape ? cf::lora_fused_workspace_bytes(batch, rank) : 0;
+    }
     if (dtype != CF_F32 || batch <= 0 || in_features <= 0 || out_features <= 0 || rank < 0 ||
         rank > 16 || in_features % 4 != 0 || out_features % 4 != 0) {
         return 0;
@@ -356,7 +364,18 @@ cf_status cf_lora_linear_ws(const void* x, const void* w, const void* a, const v
     if (batch <= 0 || out_features <= 0) return CF_OK;
     CF_REQUIRE(in_features >= 0 && rank >= 0, "cf_lora_linear_ws: negative dimension");
     const size_t needed = cf_lora_linear_ws_bytes(dtype, batch, in_features, out_features, rank);
-    if (needed > 0 &&
+    if (needed > 0 && dtype == CF_BF16 &&
+        cf::lora_fused_eligible(x, w, a, b, batch, out_features, in_features, rank)) {
+        CF_REQUIRE(x != nullptr && w != nullptr && y != nullptr && a != nullptr && b != nullptr,
+                   "cf_lora_linear_ws: null pointer");
+        CF_REQUIRE(workspace != nullptr && workspace_bytes >= needed,
+                   "cf_lora_linear_ws: workspace of %zu bytes given, %zu needed", workspace_bytes,
+                   needed);
+        CF_REQUIRE(cf::host_aligned(workspace, 16), "cf_lora_linear_ws: workspace must be 16-byte aligned");
+        return cf::launch_lora_fused(x, w, a, b, y, xa_out, batch, out_features, in_features, rank,
+                                     scale, workspace, static_cast<hipStream_t>(stream));
+    }
+    if (needed > 0 && dtype == CF_F32 &&
         cf::lora_f32_eligible(x, w, a, b, y, batch, out_features, in_features, rank)) {
         CF_REQUIRE(x != nullptr && w != nullptr && y != nullptr && (rank == 0 || (a != nullptr && b != nullptr)),
                    "cf_lora_linear_ws: null pointer");
@@ -383,7 +402,7 @@ cf_status cf_matmul(const void* a, const void* b, void* c, cf_dtype dtype, int64
                cf::dtype_name(dtype));
     auto s = static_cast<hipStream_t>(stream);
     if (dtype == CF_BF16 && cf::lora_fused_eligible(a, b, nullptr, nullptr, m, n, k, 0)) {
-        return cf::launch_lora_fused(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, s);
+        return cf::launch_lora_fused(a, b, nullptr, nullptr, c, nullptr, m, n, k, 0, 0.0f, nullptr, s);
     }
     if (dtype == CF_F32 && cf::lora_f32_eligible(a, b, nullptr, nullptr, c, m, n, k, 0)) {
         return cf::launch_lora_f32(static_cast<const float*>(a), static_cast<const float*>(b), nullptr,

@@ -42,6 +42,12 @@
 //   * Workgroup ids are remapped so the tiles dispatched to one XCD (ids are
 //     dealt round-robin over the 8 XCDs) form a band of 4 row-tiles sharing x
 //     row-panels in that XCD's L2.
+//   * With a workspace, column tile 0 of each row tile publishes its bf16
+//     x @ a fragments (device-scope stores, then a flag set to a token of
+//     the dispatch), and workgroups that start after the first round find
+//     the flag set and skip the adapter MFMAs of their K-loop, copying the
+//     fragments instead. The flag is read once; nothing waits on it, so a
+//     tile that finds it unset forms x @ a itself, with the same result.
 // The reference's fused kernel recomputes x @ a untiled in every block
 // (cuda/src/lora_linear.cu:138-203).
 #include "cf_lora_fused.hpp"
@@ -51,8 +57,21 @@
 
 #include <type_traits>
 
+// Index of the current dispatch packet in its hardware queue: it grows with
+// every packet on that queue (graph replays included).
+extern "C" __device__ uint64_t cf_queue_dispatch_index() __asm("llvm.amdgcn.dispatch.id");
+
 namespace cf {
 namespace {
+
+/// A value no other dispatch of this process writes: the queue's packet
+/// index mixed with the queue's address (two queues repeat indices). Flags
+/// set to it are never cleared; whatever an earlier call (or the
+/// workspace's previous owner) left there reads as unset.
+__device__ __forceinline__ uint64_t dispatch_token() {
+    const uint64_t queue = reinterpret_cast<uint64_t>(__builtin_amdgcn_queue_ptr());
+    return cf_queue_dispatch_index() ^ (queue * 0x9E3779B97F4A7C15ull);
+}
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
@@ -77,7 +96,8 @@ constexpr int kXaBytes = (kBM / 16) * 64 * 8;            // 8 KiB: bf16 x @ a fr
 constexpr int kOffW = kXSlots * kXPair;
 constexpr int kOffB = kOffW + kStages * kStage;
 constexpr int kOffXa = kOffB + kTileB;
-constexpr int kLdsBytes = kOffXa + kXaBytes;             // 148 KiB
+constexpr int kOffReuse = kOffXa + kXaBytes;             // one word: take the published x @ a
+constexpr int kLdsBytes = kOffReuse + 16;                // 148 KiB + 16 B
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 workgroup");
 static_assert(kThreads / 64 * 64 * 256 <= kOffB, "bf16 output staging stays clear of b and x @ a");
 
@@ -134,6 +154,18 @@ struct FusedArgs {
     float scale;
     int tiles_m;
     int tiles_n;
+    // Sharing x @ a within a row tile (adapter kernel with a workspace;
+    // null otherwise): column tile 0 of row tile tm publishes its bf16 x @ a
+    // fragments (the kXaBytes the epilogue exchanges through LDS) at
+    // xa_pub + tm * kXaBytes, then sets xa_flags[tm] to the dispatch token.
+    // Workgroups with ids from reuse_from on (they start once a first
+    // round of workgroups has left its CUs) look at their row tile's flag
+    // once, at the start: if it is set they skip the adapter MFMAs of the
+    // K-loop and copy the fragments instead, else they compute x @ a as
+    // every tile does. Nothing ever waits for a flag.
+    uint8_t* xa_pub;
+    uint64_t* xa_flags;
+    int reuse_from;
 };
 
 /// Operand fragments of one K-step: x (B operand) row block rb(i), k
@@ -157,8 +189,9 @@ struct XFrags {
 /// only the high pass runs.
 template <bool kAdapter, bool kOutF32, bool kSplitB = true>
 __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds, f32x4_t (&acc)[8][4],
-                                            const f32x4_t (&xacc)[2], int wave, int lane, int tn,
-                                            int64_t m0, int64_t n0) {
+                                            const f32x4_t (&xacc)[2], int wave, int lane, int tm,
+                                            int tn, int64_t m0, int64_t n0, bool reused,
+                                            uint64_t token) {
     const int wm = wave >> 1;
     const int wn = wave & 1;
     const int g = lane >> 4;
@@ -170,6 +203,8 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
         // x @ a: lane holds (x @ a)[row wm*64 + 16 (2 wn + t) + lane%16][4 g .. 4 g + 3].
         uint2* xa_lds = reinterpret_cast<uint2*>(lds + kOffXa);
         const bool write_xa = args.xa_out != nullptr && tn == 0;
+        // A tile that took the published fragments has them in place already.
+        if (!reused) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int rb = wm * 4 + wn * 2 + t;
@@ -192,7 +227,25 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
                 }
             }
         }
+        }
         __syncthreads();
+        if (args.xa_flags != nullptr && tn == 0) {
+            // Publish the fragments for the row tile's other column tiles:
+            // one 16-byte device-scope store per thread, every wave waits
+            // until its stores are acknowledged (visible to all CUs), then
+            // thread 0 sets the flag to this dispatch's token.
+            const int tid = wave * 64 + lane;
+            const uint4 v = *reinterpret_cast<const uint4*>(lds + kOffXa + 16 * tid);
+            const u32x4_t bits = {v.x, v.y, v.z, v.w};
+            __builtin_amdgcn_raw_buffer_store_b128(
+                bits, make_buffer(args.xa_pub + static_cast<int64_t>(tm) * kXaBytes, kXaBytes),
+                static_cast<uint32_t>(16 * tid), 0, kCacheDeviceScope);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0) {
+                __hip_atomic_store(args.xa_flags + tm, token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
 
         // acc += scale * (b^T-block @ bf16(x @ a)^T-block), K = 16. scale * b
         // is formed in fp32 and split into two bf16 parts, hi + lo, each
@@ -437,7 +490,9 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     const int a_rd0 = a_offset(8 * g + (jl >> 2), (jl & 3) * 8);
     const int a_rd1 = a_offset(8 * g + 4 + (jl >> 2), (jl & 3) * 8);
 
-    auto read_x = [&](XFrags& f, int64_t kt) {
+    // `xa` (true/false type): this K-loop forms x @ a (the a fragments are
+    // read, the adapter MFMAs issued, a is copied into LDS).
+    auto read_x = [&](XFrags& f, int64_t kt, auto xa) {
         const uint8_t* sx = lds + static_cast<int>((kt >> 1) % kXSlots) * kXPair;
         const int x_off = x_rd ^ (static_cast<int>(kt & 1) << 6);
 #pragma unroll
@@ -445,7 +500,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
             const int rb = (i + 2 * wn) & 3;
             f.x[i] = *reinterpret_cast<const bf16x8_t*>(sx + x_off + rb * 2048);
         }
-        if (kAdapter) {
+        if constexpr (kAdapter && decltype(xa)::value) {
             const uint8_t* sa = lds + kOffW + static_cast<int>(kt % kStages) * kStage + kTileW;
             f.a = concat(lds_read_tr(sa, a_rd0), lds_read_tr(sa, a_rd1));
         }
@@ -474,8 +529,9 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     // On step kt the DMA goes out for K-step kt + 3 (w, a) and, on odd steps,
     // for x pair (kt + 3) / 2, whose slot the barrier of step kt has freed.
     auto multiply = [&](const XFrags& f, int64_t next_kt, auto read_next, auto issue, auto odd,
-                        auto issuer) {
-        if (kAdapter) {
+                        auto issuer, auto xa) {
+        constexpr int kW = kAdapter && decltype(xa)::value ? kWLoads : 4;
+        if constexpr (kAdapter && decltype(xa)::value) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 xacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a, f.x[t], xacc[t], 0, 0, 0);
@@ -491,7 +547,7 @@ void lora_fused_bf16_kernel(FusedArgs args) {
             if constexpr (decltype(read_next)::value) wf[jb] = read_w(next_kt, jb);
             if constexpr (decltype(issue)::value && decltype(issuer)::value) {
                 if constexpr (decltype(odd)::value) issue_x((next_kt + 2) >> 1, jb);
-                if (jb < kWLoads) issue_w(next_kt + 2, jb);
+                if (jb < kW) issue_w(next_kt + 2, jb);
             }
             // Left alone, the scheduler sinks each next-step w read to a few
             // MFMAs before its use; a scheduling barrier after every second
@@ -510,10 +566,17 @@ void lora_fused_bf16_kernel(FusedArgs args) {
             row < rank && col < N ? static_cast<uint32_t>((row * N + col) * 2) : kOutOfRange;
         dma16_m0(bbuf, lds_addr + kOffB + wave * 1024, off, 0);
     }
+    // Sharing x @ a: whether this tile may take its row tile's published
+    // fragments (decided once, by wave 4, before the first barrier).
+    const bool may_reuse = kAdapter && args.xa_flags != nullptr && tn != 0 &&
+                           static_cast<int>(blockIdx.x) >= args.reuse_from;
+    const uint64_t token = kAdapter && args.xa_flags != nullptr ? dispatch_token() : 0;
+
     // The K-loop, instantiated for issuing (waves 0-3) and non-issuing waves;
     // the latter wait for nothing but the barriers (their vmcnt waits find
-    // no DMA of their own in flight).
-    auto run = [&](auto issuer) {
+    // no DMA of their own in flight, or only the published fragments below).
+    // Returns whether the tile took the published x @ a.
+    auto run = [&](auto issuer) -> bool {
     const int64_t k_tiles = args.k_steps;  // even, >= 2
     auto issue_w_all = [&](int64_t kt) {
 #pragma unroll
@@ -535,12 +598,30 @@ void lora_fused_bf16_kernel(FusedArgs args) {
         } else {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
         }
+    } else {
+        // One device-scope read of the flag, while waves 0-3 wait for the
+        // first K-step; the answer goes to LDS before the barrier.
+        if (may_reuse && wave == 4) {
+            const uint64_t seen =
+                __hip_atomic_load(args.xa_flags + tm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) *reinterpret_cast<uint32_t*>(lds + kOffReuse) = seen == token ? 1u : 0u;
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));  // lgkmcnt(0)
+        }
     }
     bare_barrier();  // step 0 in LDS
+    const bool reuse =
+        may_reuse && __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t*>(lds + kOffReuse)) != 0;
 
+    using yes = std::true_type;
+    using no = std::false_type;
+    auto loop = [&](auto xa) {
+    // w (+ a) DMA per K-step of this loop (the prologue above sent a for
+    // K-steps 0-2 either way; without x @ a they are not read, and the
+    // waits below only become more conservative for the first steps).
+    constexpr int kW = kAdapter && decltype(xa)::value ? kWLoads : 4;
     XFrags f0;
     XFrags f1;
-    read_x(f0, 0);
+    read_x(f0, 0, xa);
 #pragma unroll
     for (int jb = 0; jb < 8; ++jb) wf[jb] = read_w(0, jb);
 
@@ -559,8 +640,6 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     // lets exactly the previous step's loads stay in flight: w (+ a) after
     // an even step, w (+ a) and an x pair after an odd one. The last four
     // steps are peeled so the loop body has no branches.
-    using yes = std::true_type;
-    using no = std::false_type;
     // Steps with f0 as the current fragments are even, with f1 odd.
     auto step = [&](int64_t kt, XFrags& cur, XFrags& nxt, auto issue, auto wait_all, auto read,
                     auto odd) {
@@ -568,14 +647,14 @@ void lora_fused_bf16_kernel(FusedArgs args) {
             if constexpr (decltype(wait_all)::value) {
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             } else if constexpr (decltype(odd)::value) {
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads) & ~(15 << 8));  // and lgkmcnt(0)
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kW) & ~(15 << 8));  // and lgkmcnt(0)
             } else {
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads + kXLoads));
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(kW + kXLoads));
             }
             bare_barrier();
-            read_x(nxt, kt + 1);
+            read_x(nxt, kt + 1, xa);
         }
-        multiply(cur, kt + 1, read, issue, odd, issuer);
+        multiply(cur, kt + 1, read, issue, odd, issuer, xa);
     };
     int64_t kt = 0;
     for (; kt + 4 < k_tiles; kt += 2) {
@@ -590,13 +669,32 @@ void lora_fused_bf16_kernel(FusedArgs args) {
     step(kt, f0, f1, no{}, yes{}, yes{}, no{});
     step(kt + 1, f1, f0, no{}, no{}, no{}, yes{});
     };
-    if (wave < 4) {
-        run(std::true_type{});
+    if (kAdapter && reuse) {
+        // Waves 4-7 copy the published fragments (8 KiB) into the x @ a
+        // area, at device scope: they were written by another workgroup,
+        // possibly behind another XCD's L2, and were complete before the
+        // flag was set. Nothing reads the area before the epilogue; the
+        // last K-steps' vmcnt(0) and barrier order the copy before it.
+        if constexpr (!decltype(issuer)::value) {
+            const i32x4_t pbuf = raw_buffer_words(args.xa_pub + static_cast<int64_t>(tm) * kXaBytes,
+                                                  static_cast<uint32_t>(kXaBytes));
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int piece = 2 * (wave - 4) + i;
+                dma16_device_m0(pbuf, lds_addr + kOffXa + piece * 1024, static_cast<uint32_t>(16 * lane),
+                                static_cast<uint32_t>(piece * 1024));
+            }
+        }
+        loop(no{});
     } else {
-        run(std::false_type{});
+        loop(yes{});
     }
+    return reuse;
+    };
+    const bool reused = wave < 4 ? run(std::true_type{}) : run(std::false_type{});
 
-    finish_tile<kAdapter, kOutF32, kSplitB>(args, lds, acc, xacc, wave, lane, tn, m0, n0);
+    finish_tile<kAdapter, kOutF32, kSplitB>(args, lds, acc, xacc, wave, lane, tm, tn, m0, n0, reused,
+                                            token);
 }
 
 }  // namespace
@@ -614,9 +712,15 @@ bool lora_fused_eligible(const void* x, const void* w, const void* a, const void
            ceil_div<int64_t>(M, kBM) * ceil_div<int64_t>(N, kBN) < (1LL << 31);
 }
 
+size_t lora_fused_workspace_bytes(int64_t M, int64_t rank) {
+    if (M <= 0 || rank <= 0) return 0;
+    const int64_t tiles_m = ceil_div<int64_t>(M, kBM);
+    return static_cast<size_t>(ceil_div<int64_t>(tiles_m * 8, 256) * 256 + tiles_m * kXaBytes);
+}
+
 cf_status launch_lora_fused(const void* x, const void* w, const void* a, const void* b, void* y,
                             float* xa_out, int64_t M, int64_t N, int64_t K, int64_t rank,
-                            float scale, hipStream_t stream) {
+                            float scale, void* workspace, hipStream_t stream) {
     FusedArgs args;
     args.x = static_cast<const uint16_t*>(x);
     args.w = static_cast<const uint16_t*>(w);
@@ -634,6 +738,18 @@ cf_status launch_lora_fused(const void* x, const void* w, const void* a, const v
     args.tiles_m = static_cast<int>(ceil_div<int64_t>(M, kBM));
     args.tiles_n = static_cast<int>(ceil_div<int64_t>(N, kBN));
     const int grid = args.tiles_m * args.tiles_n;
+    // One workgroup fits a CU (148 KiB of LDS), so workgroups from id
+    // cu_count() on start as the first ones leave; by then the first column
+    // tile of their row tile (dealt to its XCD ahead of the row tile's other
+    // column tiles) has usually published x @ a.
+    args.xa_pub = nullptr;
+    args.xa_flags = nullptr;
+    args.reuse_from = grid;
+    if (workspace != nullptr && rank > 0) {
+        args.xa_flags = static_cast<uint64_t*>(workspace);
+        args.xa_pub = static_cast<uint8_t*>(workspace) + ceil_div<int64_t>(args.tiles_m * 8, 256) * 256;
+        args.reuse_from = cu_count();
+    }
     // scale * b is exact in bf16 for every bf16 b when the scale is 0 or
     // +-2^k with k >= 0 (the exponent only moves up; an overflow gives the
     // infinity the fp32 product has): the epilogue then skips the pass over

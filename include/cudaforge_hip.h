@@ -257,22 +257,28 @@ cf_status cf_lora_linear(const void* x, const void* w, const void* a, const void
                          float* xa_out, cf_dtype dtype, int64_t batch, int64_t in_features,
                          int64_t out_features, int64_t rank, float scale, void* stream);
 
-/* Workspace bytes cf_lora_linear_ws can use to split the reduction of a small
- * fp32 problem across workgroups (0 when it would not split: bf16, large
- * outputs, shapes the fp32 MFMA kernel does not take). It has no counterpart
- * in the reference, whose launcher's workspace is the batch x rank
- * intermediate (cuda/include/cudaforge/lora_linear.cuh:62). */
+/* Workspace bytes cf_lora_linear_ws can use. fp32: to split the reduction of
+ * a small problem across workgroups (0 when it would not split: large
+ * outputs, shapes the fp32 MFMA kernel does not take). bf16 (shapes of the
+ * fused MFMA kernel with rank > 0): a flag block and 8 KiB per 256 rows of x,
+ * through which the output tiles that start late take x @ a from the first
+ * tile of their rows instead of forming it again. It has no counterpart in
+ * the reference, whose launcher's workspace is the batch x rank intermediate
+ * (cuda/include/cudaforge/lora_linear.cuh:62). */
 size_t cf_lora_linear_ws_bytes(cf_dtype dtype, int64_t batch, int64_t in_features,
                                int64_t out_features, int64_t rank);
 
 /* cf_lora_linear with a workspace of cf_lora_linear_ws_bytes(...) bytes
- * (16-byte aligned; NULL when that is 0). fp32 problems with rank <= 16 and
- * in_features, out_features multiples of 4 run on the MFMA units with each
- * operand split into bf16 high and low parts (three products per term, about
- * 2^-16 relative error per product; fp32 accumulation), and a small problem
- * splits its reduction range across workgroups, partial results summed in a
- * fixed order (deterministic). cf_lora_linear runs the same kernel without
- * the split. Replaces launch_lora_linear
+ * (16-byte aligned, in any state; NULL when that is 0). fp32 problems with
+ * rank <= 16 and in_features, out_features multiples of 4 run on the MFMA
+ * units with each operand split into bf16 high and low parts (three products
+ * per term, about 2^-16 relative error per product; fp32 accumulation), and a
+ * small problem splits its reduction range across workgroups, partial results
+ * summed in a fixed order (deterministic). bf16 problems on the fused kernel
+ * share x @ a between output tiles through it; the output is bit-identical
+ * to cf_lora_linear's. cf_lora_linear runs the same kernels without the split
+ * and the sharing. Calls that overlap (other streams) need workspaces of
+ * their own. Replaces launch_lora_linear
  * (cuda/include/cudaforge/lora_linear.cuh:49-51) for callers that can give
  * it a workspace. */
 cf_status cf_lora_linear_ws(const void* x, const void* w, const void* a, const void* b, void* y,

@@ -88,9 +88,27 @@ def test_invalid_arguments_are_reported_not_thrown(lib):
                                null, 0, 0, null)
     assert status == _lib.CF_ERR_INVALID_ARGUMENT
     assert b"workspace" in lib.cf_last_error()
-    # The fp32 LoRA workspace: 0 for bf16 and for shapes the fp32 MFMA kernel
-    # does not take; one smaller than asked for is rejected before any launch.
-    assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 32, 1024, 1024, 8) == 0
+    # The LoRA workspace. bf16: a 256-byte flag block plus 8 KiB per 256-row
+    # tile for the fused kernel's shared x @ a (0 for rank 0, odd ranks and
+    # shapes the fused kernel does not take). fp32: 0 for shapes the fp32 MFMA
+    # kernel does not take. One smaller than asked for is rejected before any
+    # launch.
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 32, 1024, 1024, 8) == 256 + 8192
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 8192, 4096, 4096, 16) == 256 + 32 * 8192
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 8192 * 8 + 1, 4096, 4096, 16) == 2304 + 257 * 8192
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 32, 1024, 1024, 0) == 0
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 32, 1024, 1024, 7) == 0
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 32, 1000, 1024, 8) == 0
+    assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 32, 1024, 1020, 8) == 0
+    bf16_bytes = lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 32, 1024, 1024, 8)
+    status = lib.cf_lora_linear_ws(p4k := ctypes.c_void_p(4096), p4k, p4k, p4k, p4k, null, _lib.CF_BF16,
+                                   32, 1024, 1024, 8, 0.5, p4k, bf16_bytes - 16, null)
+    assert status == _lib.CF_ERR_INVALID_ARGUMENT
+    assert b"workspace" in lib.cf_last_error()
+    status = lib.cf_lora_linear_ws(p4k, p4k, p4k, p4k, p4k, null, _lib.CF_BF16, 32, 1024, 1024, 8, 0.5,
+                                   ctypes.c_void_p(4096 + 8), bf16_bytes, null)
+    assert status == _lib.CF_ERR_INVALID_ARGUMENT
+    assert b"aligned" in lib.cf_last_error()
     assert lib.cf_lora_linear_ws_bytes(_lib.CF_F32, 32, 1022, 1024, 8) == 0
     assert lib.cf_lora_linear_ws_bytes(_lib.CF_F32, 32, 1024, 1024, 17) == 0
     nbytes = lib.cf_lora_linear_ws_bytes(_lib.CF_F32, 32, 1024, 1024, 8)
