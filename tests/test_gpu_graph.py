@@ -82,3 +82,32 @@ def test_block_forward_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(out_res, eager_res), f"replay {r}: residual"
         assert (out.float() - eager_out.float()).abs().max().item() <= 1e-2 * scale, f"replay {r}"
+
+
+def test_fused_lora_with_shared_xa_replays_on_new_inputs():
+    """Config 3's shape (512 output tiles, two rounds of workgroups) through the
+    torch operator, whose workspace lets late column tiles take x @ a from the
+    first tile of their rows. Each replay runs on new x (copied into the
+    captured input) and must equal the plain entry point on that x bit for bit:
+    the flags the previous replay left hold another dispatch's token."""
+    from cuda_force_amd import _lib
+
+    from . import gpu_util as g
+
+    announce("graph capture: fused LoRA bf16 8192x4096x4096 r16 with shared x @ a, new x per replay")
+    m, k, n, r = 8192, 4096, 4096, 16
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    x = torch.randn(m, k, generator=gen, device="cuda").to(torch.bfloat16)
+    w = (0.02 * torch.randn(k, n, generator=gen, device="cuda")).to(torch.bfloat16)
+    a = (torch.randn(k, r, generator=gen, device="cuda") / 64).to(torch.bfloat16)
+    b = (0.02 * torch.randn(r, n, generator=gen, device="cuda")).to(torch.bfloat16)
+    graph, out = capture(lambda: torch.ops.cudaforge.lora_linear(x, w, a, b, 2.0))
+    want = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    for rep in range(REPLAYS):
+        torch.cuda.synchronize()
+        x.copy_(torch.randn(m, k, generator=gen, device="cuda").to(torch.bfloat16))
+        g.call("cf_lora_linear", x.data_ptr(), w.data_ptr(), a.data_ptr(), b.data_ptr(), want.data_ptr(),
+               None, _lib.CF_BF16, m, k, n, r, 2.0, g.stream())
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {rep}"
