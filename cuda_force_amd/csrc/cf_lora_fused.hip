@@ -206,27 +206,27 @@ __device__ __forceinline__ void finish_tile(const FusedArgs& args, uint8_t* lds,
         // A tile that took the published fragments has them in place already.
         if (!reused) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int rb = wm * 4 + wn * 2 + t;
-            // Columns past the rank are padding (a reads zero there); an
-            // infinite x makes them inf * 0 = NaN, kept out of the product
-            // with b's zero rows.
-            float v[4];
+            for (int t = 0; t < 2; ++t) {
+                const int rb = wm * 4 + wn * 2 + t;
+                // Columns past the rank are padding (a reads zero there); an
+                // infinite x makes them inf * 0 = NaN, kept out of the product
+                // with b's zero rows.
+                float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = 4 * g + e < rank ? xacc[t][e] : 0.0f;
-            uint2 packed;
-            packed.x = f32x2_to_bf16x2_canon(v[0], v[1]);
-            packed.y = f32x2_to_bf16x2_canon(v[2], v[3]);
-            xa_lds[rb * 64 + lane] = packed;
-            const int64_t row = m0 + rb * 16 + jl;
-            if (write_xa && row < M) {
-                float* dst = args.xa_out + row * rank;
+                for (int e = 0; e < 4; ++e) v[e] = 4 * g + e < rank ? xacc[t][e] : 0.0f;
+                uint2 packed;
+                packed.x = f32x2_to_bf16x2_canon(v[0], v[1]);
+                packed.y = f32x2_to_bf16x2_canon(v[2], v[3]);
+                xa_lds[rb * 64 + lane] = packed;
+                const int64_t row = m0 + rb * 16 + jl;
+                if (write_xa && row < M) {
+                    float* dst = args.xa_out + row * rank;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (4 * g + e < rank) dst[4 * g + e] = xacc[t][e];
+                    for (int e = 0; e < 4; ++e) {
+                        if (4 * g + e < rank) dst[4 * g + e] = xacc[t][e];
+                    }
                 }
             }
-        }
         }
         __syncthreads();
         if (args.xa_flags != nullptr && tn == 0) {
