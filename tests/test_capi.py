@@ -88,11 +88,11 @@ def test_invalid_arguments_are_reported_not_thrown(lib):
                                null, 0, 0, null)
     assert status == _lib.CF_ERR_INVALID_ARGUMENT
     assert b"workspace" in lib.cf_last_error()
-    # The LoRA workspace. bf16: a 256-byte flag block plus 8 KiB per 256-row
-    # tile for the fused kernel's shared x @ a (0 for rank 0, odd ranks and
-    # shapes the fused kernel does not take). fp32: 0 for shapes the fp32 MFMA
-    # kernel does not take. One smaller than asked for is rejected before any
-    # launch.
+    # The LoRA workspace. bf16: an 8-byte flag per 256-row tile (the block
+    # rounded up to 256 bytes) plus 8 KiB per tile for the fused kernel's
+    # shared x @ a (0 for rank 0, odd ranks and shapes the fused kernel does
+    # not take). fp32: 0 for shapes the fp32 MFMA kernel does not take. One
+    # smaller than asked for is rejected before any launch.
     assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 32, 1024, 1024, 8) == 256 + 8192
     assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 8192, 4096, 4096, 16) == 256 + 32 * 8192
     assert lib.cf_lora_linear_ws_bytes(_lib.CF_BF16, 8192 * 8 + 1, 4096, 4096, 16) == 2304 + 257 * 8192
