@@ -105,3 +105,24 @@ def test_the_torch_operator_takes_the_workspace_path():
     y1 = torch.ops.cudaforge.lora_linear(x, w, a, b, 2.0)
     torch.cuda.synchronize()
     assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+
+
+def test_two_streams_with_workspaces_of_their_own():
+    """The torch operator on two default-priority streams at once, each call
+    with the workspace torch's caching allocator gives it on its stream: the
+    flags and fragments of one call never reach the other."""
+    g.announce("fused LoRA bf16 with shared x @ a on two streams at once, 8192x4096x4096 r16")
+    m, k, n, r = 8192, 4096, 4096, 16
+    ops = [_operands(m, k, n, r, seed) for seed in (31, 32)]
+    want = [_plain(*op, 2.0)[0] for op in ops]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [None, None]
+    for rep in range(3):
+        for i, (s, op) in enumerate(zip(streams, ops)):
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                outs[i] = torch.ops.cudaforge.lora_linear(*op, 2.0)
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(outs[i].view(torch.int16), want[i].view(torch.int16)), f"rep {rep} stream {i}"
