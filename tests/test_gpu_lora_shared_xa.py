@@ -4,7 +4,8 @@ holding the dispatch's token, and workgroups that start late copy them
 instead of forming x @ a in their K-loop. Whichever happens, the output must
 be bit-identical to the call without a workspace (cf_lora_linear): the same
 MFMA sequence forms x @ a in either tile. Checked on shapes of one and of
-several rounds of workgroups, ragged edges and ranks 2-16, with a workspace
+several rounds of workgroups, ragged edges, ranks 2-16 and K-loops of 2, 4
+and 6 steps (the peeled steps alone, and with one loop pass), with a workspace
 that starts as garbage and is then reused by a call on other inputs (stale
 flags of the first call must read as unset in the second), and the
 published fragments themselves against bf16(x @ a).
@@ -28,6 +29,9 @@ SHAPES = [
     (16384, 1024, 2048, 2),
     (32768, 1024, 4096, 16),  # 2048 tiles, eight rounds
     (2048, 2048, 4096, 8),    # 128 tiles: one round, nothing shared
+    (32768, 64, 2048, 16),    # the shortest K-loops: 2, 4 and 6 K-steps
+    (32768, 128, 2048, 8),
+    (32768, 192, 2048, 4),
 ]
 
 
